@@ -1,0 +1,230 @@
+"""Drop-in attention sublayer: norm1 -> multi-head attention -> +residual -> norm2.
+
+``CobraAttentionSublayer`` is the attention half of the reference block
+(``torch_transformer_benchmark.py:135-142``) with the reference module's
+parameter names, shapes and construction order, so ``load_state_dict`` works
+in both directions and ``torch.manual_seed(s)`` draws the same weights.  Its
+``forward(x, valid_token_mask=None)`` keeps the reference call surface
+(TTB:1512-1516) and returns ``y = norm2(x + attention(norm1(x)))`` in x.dtype.
+
+Every forward runs on hand-written HIP kernels through the C ABI
+(``cobra_layer_fwd``): there is no PyTorch compute fallback.  The host side
+mirrors the reference's orchestration (TTB:857-1541):
+
+* weights are packed lazily on the first forward, as plain attributes so
+  ``state_dict`` is unchanged (TTB:857-864): one fp16 ``[3D, D]`` q|k|v
+  matrix in that order (TTB:876-883), fp16 ``W_o``, fp32 biases and LayerNorm
+  parameters.  The pack is rebuilt whenever a parameter changes (in-place
+  updates bump its version), which the reference did only on shape changes;
+* small inputs (<= 64 MiB, TTB:1077-1079) are captured once into a hipGraph
+  (``torch.cuda.CUDAGraph`` on ROCm) and replayed; the output buffer is
+  returned without a clone, as the reference does (TTB:1356-1360);
+* inputs that do not fit one device pass are streamed in batch chunks sized
+  from ``hipMemGetInfo`` with halve-on-OOM (``streaming``, TTB:1364-1508).
+"""
+
+from __future__ import annotations
+
+import gc
+from typing import Optional, Tuple, Union
+
+import torch
+import torch.nn as nn
+
+from . import ops, streaming
+
+GRAPH_MAX_INPUT_BYTES = 64 * 1024 * 1024
+
+
+class CobraSelfAttention(nn.Module):
+    """Parameters of ``BaselineSelfAttention`` (TTB:60-76): q, k, v, out projections.
+
+    Only a container here -- the sublayer runs the whole attention in its
+    kernels -- but with identical names, shapes, init and draw order.
+    """
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__()
+        if d_model % num_heads != 0:
+            raise ValueError("d_model must be divisible by num_heads")
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.q_proj = nn.Linear(d_model, d_model, bias=True)
+        self.k_proj = nn.Linear(d_model, d_model, bias=True)
+        self.v_proj = nn.Linear(d_model, d_model, bias=True)
+        self.out_proj = nn.Linear(d_model, d_model, bias=True)
+
+
+class _Pack:
+    """Kernel-ready copies of the parameters (never registered on the module)."""
+
+    __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "key")
+
+    def __init__(self, m: "CobraAttentionSublayer", key) -> None:
+        att = m.attention
+        with torch.no_grad():
+            self.w_qkv = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(
+                torch.float16).contiguous()
+            self.b_qkv = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).float().contiguous()
+            self.w_o = att.out_proj.weight.to(torch.float16).contiguous()
+            self.b_o = att.out_proj.bias.float().contiguous()
+            self.ln1_w = m.norm1.weight.float().contiguous()
+            self.ln1_b = m.norm1.bias.float().contiguous()
+            self.ln2_w = m.norm2.weight.float().contiguous()
+            self.ln2_b = m.norm2.bias.float().contiguous()
+        self.key = key
+
+
+class CobraAttentionSublayer(nn.Module):
+    def __init__(self, d_model: int, num_heads: int, causal: bool = False, eps: float = 1e-5) -> None:
+        super().__init__()
+        # Construction order = BaselineTransformerBlock's first members (TTB:129-131).
+        self.norm1 = nn.LayerNorm(d_model, eps=eps)
+        self.attention = CobraSelfAttention(d_model, num_heads)
+        self.norm2 = nn.LayerNorm(d_model, eps=eps)
+        self.causal = causal
+        self._pack: Optional[_Pack] = None
+        self._sig = None
+        self._ws: Optional[torch.Tensor] = None
+        self._graph_ok = False
+        self._graph = None
+        self._static_x: Optional[torch.Tensor] = None
+        self._static_y: Optional[torch.Tensor] = None
+        self._static_r: Optional[torch.Tensor] = None
+
+    # -- parameters ---------------------------------------------------------
+
+    def _param_key(self):
+        return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in self.parameters())
+
+    def _packed(self) -> _Pack:
+        key = self._param_key()
+        if self._pack is None or self._pack.key != key:
+            if not self.norm1.weight.is_cuda:
+                raise RuntimeError("CobraAttentionSublayer runs on the GPU only: move it with .to('cuda')")
+            self._pack = _Pack(self, key)
+            self._graph = None  # the graph baked in the old buffers' addresses
+        return self._pack
+
+    # -- entry point ----------------------------------------------------------
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor] = None,
+        causal: Optional[bool] = None,
+        return_residual: bool = False,
+    ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+        causal = self.causal if causal is None else bool(causal)
+        if valid_token_mask is not None and not bool(valid_token_mask.all()):
+            raise NotImplementedError("padded sequences (valid_token_mask with False entries) are not supported yet")
+        if x.dim() != 3 or x.shape[-1] != self.attention.d_model:
+            raise ValueError(f"x must be [B, S, {self.attention.d_model}], got {tuple(x.shape)}")
+        if x.dtype not in (torch.float16, torch.float32):
+            raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
+        pack = self._packed()
+        if self._stream_needed(x):
+            return self._run_streamed(x, causal, return_residual)
+        x = x.contiguous()
+        sig = (tuple(x.shape), x.dtype, x.device, causal, return_residual)
+        if sig != self._sig:
+            self._prepare(sig, x)
+        if self._graph_ok:
+            return self._run_graphed(x, pack, causal, return_residual)
+        return self._run_eager(x, pack, causal, return_residual)
+
+    # -- planning -------------------------------------------------------------
+
+    def _prepare(self, sig, x: torch.Tensor) -> None:
+        B, S, D = x.shape
+        self._sig = sig
+        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, self.attention.num_heads),
+                               dtype=torch.uint8, device=x.device)
+        self._graph_ok = x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
+        self._graph = None
+        self._static_x = self._static_y = self._static_r = None
+
+    def _launch(self, x, y, r, pack: _Pack, ws: torch.Tensor, causal: bool) -> None:
+        ops.layer_fwd(x, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w, pack.ln1_b, pack.ln2_w,
+                      pack.ln2_b, y, ws, self.attention.num_heads, causal, self.norm1.eps, resid_out=r)
+
+    def _run_eager(self, x, pack, causal, return_residual, ws=None):
+        y = torch.empty_like(x)
+        r = torch.empty(x.shape, dtype=torch.float32, device=x.device) if return_residual else None
+        self._launch(x, y, r, pack, self._ws if ws is None else ws, causal)
+        return (r, y) if return_residual else y
+
+    def _run_graphed(self, x, pack, causal, return_residual):
+        if self._graph is None:
+            self._static_x = x.clone()
+            self._static_y = torch.empty_like(x)
+            self._static_r = (torch.empty(x.shape, dtype=torch.float32, device=x.device)
+                              if return_residual else None)
+            # One eager pass first: loads the code objects outside the capture.
+            self._launch(self._static_x, self._static_y, self._static_r, pack, self._ws, causal)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._launch(self._static_x, self._static_y, self._static_r, pack, self._ws, causal)
+            self._graph = graph
+        if x.data_ptr() != self._static_x.data_ptr():
+            self._static_x.copy_(x)
+        self._graph.replay()
+        return (self._static_r, self._static_y) if return_residual else self._static_y
+
+    def input_buffer(self) -> Optional[torch.Tensor]:
+        """The captured graph's static input: writing into it and passing it
+        back to ``forward`` skips the input copy."""
+        return self._static_x
+
+    # -- streaming ------------------------------------------------------------
+
+    def _per_seq_bytes(self, x: torch.Tensor, return_residual: bool) -> int:
+        B, S, D = x.shape
+        ws = ops.layer_workspace_bytes(1, S, D, self.attention.num_heads)
+        return streaming.live_bytes_per_sequence(ws, S, D, x.element_size(), return_residual)
+
+    def _stream_needed(self, x: torch.Tensor) -> bool:
+        dev = self.norm1.weight.device
+        nbytes = x.numel() * x.element_size()
+        if x.is_cuda and nbytes < streaming.STREAM_MIN_BYTES:
+            return False  # small shapes never pay for the free-memory query
+        free, _ = torch.cuda.mem_get_info(dev)
+        live = self._per_seq_bytes(x, False) * x.shape[0]
+        return streaming.should_stream(x.is_cuda, nbytes, x.shape[0], live, free)
+
+    def _run_streamed(self, x, causal, return_residual):
+        dev = self.norm1.weight.device
+        pack = self._packed()
+        B, S, D = x.shape
+        host = not x.is_cuda
+        free, _ = torch.cuda.mem_get_info(dev)
+        step = streaming.plan_chunk(B, self._per_seq_bytes(x, return_residual), free)
+        y_all = torch.empty_like(x)
+        r_all = torch.empty(x.shape, dtype=torch.float32, device=x.device) if return_residual else None
+        ws_cache = {}
+
+        def run_chunk(b0: int, b1: int) -> None:
+            xc = x[b0:b1]
+            xc = xc.to(dev, non_blocking=True) if host else xc.contiguous()
+            n = b1 - b0
+            if n not in ws_cache:
+                ws_cache.clear()
+                ws_cache[n] = torch.empty(ops.layer_workspace_bytes(n, S, D, self.attention.num_heads),
+                                          dtype=torch.uint8, device=dev)
+            out = self._run_eager(xc, pack, causal, return_residual, ws=ws_cache[n])
+            if return_residual:
+                r_all[b0:b1].copy_(out[0])
+                y_all[b0:b1].copy_(out[1])
+            else:
+                y_all[b0:b1].copy_(out)
+
+        def on_oom() -> None:
+            ws_cache.clear()
+            gc.collect()
+            torch.cuda.empty_cache()
+
+        streaming.run_chunked(B, step, run_chunk, on_oom,
+                              lambda e: isinstance(e, torch.cuda.OutOfMemoryError))
+        return (r_all, y_all) if return_residual else y_all

@@ -1,0 +1,243 @@
+"""Tensor-level wrappers of the C ABI, mirroring the reference's kernel launchers.
+
+Each function keeps the name stem, argument order and meaning of the
+reference launcher it replaces (``torch_transformer_benchmark.py``, "TTB"),
+allocates its outputs with ``torch.empty`` like the reference does, enqueues
+on ``torch.cuda.current_stream()`` and never synchronises.  Differences:
+
+* weights are nn.Linear's ``[N, K]`` layout; the reference passed a
+  transposed ``[K, N]`` copy to its GEMMs (TTB:895-904).  No copy is needed here;
+* attention takes ``causal`` (the reference kernel was causal-only);
+* row masks (``mask_row`` / ``rmask`` / ``mask_out``) and the GELU epilogue
+  belong to padding support and the FFN, which are not on this path: passing
+  them raises ``NotImplementedError`` rather than silently ignoring them.
+
+Argument errors raise ``ValueError``/``TypeError`` before anything is
+enqueued; a non-zero code from the library raises ``CobraError``.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import F16, F32, call
+
+_DT = {torch.float16: F16, torch.float32: F32}
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: dtype {t.dtype} not supported (float16 or float32)") from None
+
+
+def _dev(t: torch.Tensor, what: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a device tensor (got {t.device}); the HIP path has no host fallback")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return t
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _f32_param(t: torch.Tensor, n: int, what: str) -> torch.Tensor:
+    if t.shape != (n,):
+        raise ValueError(f"{what} must have shape ({n},), got {tuple(t.shape)}")
+    return t.to(dtype=torch.float32).contiguous()
+
+
+def _no_masks(**kw) -> None:
+    for k, v in kw.items():
+        if v not in (None, False):
+            raise NotImplementedError(f"{k}: row masks / padding are not supported on this path yet")
+
+
+def add_ln(
+    resid: torch.Tensor,
+    branch: Optional[torch.Tensor],
+    mask_row: Optional[torch.Tensor],
+    w: torch.Tensor,
+    b: torch.Tensor,
+    cast_fp16: bool = True,
+    eps: float = 1e-5,
+    store_resid: bool = True,
+    mask_out: bool = False,
+) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
+    """``(resid + branch)`` then LayerNorm -> ``(new_resid | None, normed)``.
+
+    Mirrors ``_tl_add_ln`` (TTB:539-569).  The stored residual is always fp32.
+    """
+    _no_masks(mask_row=mask_row, mask_out=mask_out)
+    _dev(resid, "resid")
+    if resid.dim() != 2:
+        raise ValueError("resid must be [M, N]")
+    M, N = resid.shape
+    if branch is not None:
+        _dev(branch, "branch")
+        if branch.shape != resid.shape:
+            raise ValueError("branch must match resid")
+    gw, gb = _f32_param(w, N, "w"), _f32_param(b, N, "b")
+    out_r = torch.empty((M, N), device=resid.device, dtype=torch.float32) if store_resid else None
+    out_n = torch.empty((M, N), device=resid.device, dtype=torch.float16 if cast_fp16 else torch.float32)
+    call(
+        "cobra_ln_fwd", resid.data_ptr(), _dtype_code(resid, "resid"), _ptr(branch),
+        _dtype_code(branch, "branch") if branch is not None else 0, gw.data_ptr(), gb.data_ptr(),
+        _ptr(out_r), out_n.data_ptr(), _dtype_code(out_n, "normed"), M, N, float(eps), _stream(resid),
+    )
+    return out_r, out_n
+
+
+def linear(
+    a: torch.Tensor,
+    w: torch.Tensor,
+    bias: Optional[torch.Tensor],
+    gelu: bool = False,
+    out_fp32: bool = False,
+    resid: Optional[torch.Tensor] = None,
+    rmask: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """``a @ w.T + bias (+ resid)`` with fp32 accumulate.  Mirrors ``_tl_linear`` (TTB:355-381).
+
+    a: [M, K] fp16; w: [N, K] fp16; bias: [N]; resid: [M, N] fp16/fp32.
+    """
+    if gelu:
+        raise NotImplementedError("the GELU epilogue belongs to the FFN sublayer, not on this path")
+    _no_masks(rmask=rmask)
+    _dev(a, "a")
+    _dev(w, "w")
+    if a.dtype != torch.float16 or w.dtype != torch.float16:
+        raise TypeError("a and w must be float16 (fp16 operands, fp32 accumulate)")
+    M, K = a.shape
+    N, K2 = w.shape
+    if K2 != K:
+        raise ValueError(f"inner dimensions differ: a {tuple(a.shape)}, w {tuple(w.shape)}")
+    b32 = _f32_param(bias, N, "bias") if bias is not None else None
+    if resid is not None:
+        _dev(resid, "resid")
+        if resid.shape != (M, N):
+            raise ValueError("resid must be [M, N]")
+    out = torch.empty((M, N), device=a.device, dtype=torch.float32 if out_fp32 else torch.float16)
+    call(
+        "cobra_linear_fwd", a.data_ptr(), w.data_ptr(), _ptr(b32), _ptr(resid),
+        _dtype_code(resid, "resid") if resid is not None else 0, out.data_ptr(), _dtype_code(out, "out"),
+        M, N, K, _stream(a),
+    )
+    return out
+
+
+def linear_ln(
+    a: torch.Tensor,
+    w: torch.Tensor,
+    bias: torch.Tensor,
+    resid: torch.Tensor,
+    nw: torch.Tensor,
+    nb: torch.Tensor,
+    rmask: Optional[torch.Tensor] = None,
+    norm_fp16: bool = True,
+    mask_out: bool = False,
+    eps: float = 1e-5,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``r = a @ w.T + bias + resid``; ``(r fp32, LayerNorm(r))``.  Mirrors ``_tl_linear_ln`` (TTB:465-488).
+
+    Requires N <= 128, like the reference (TTB:471).
+    """
+    _no_masks(rmask=rmask, mask_out=mask_out)
+    _dev(a, "a")
+    _dev(w, "w")
+    _dev(resid, "resid")
+    if a.dtype != torch.float16 or w.dtype != torch.float16:
+        raise TypeError("a and w must be float16")
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K or resid.shape != (M, N):
+        raise ValueError("shape mismatch")
+    if N > 128:
+        raise ValueError("fused-LN GEMM requires N <= 128 (one workgroup owns a whole row)")
+    b32 = _f32_param(bias, N, "bias")
+    gw, gb = _f32_param(nw, N, "nw"), _f32_param(nb, N, "nb")
+    out = torch.empty((M, N), device=a.device, dtype=torch.float32)
+    normed = torch.empty((M, N), device=a.device, dtype=torch.float16 if norm_fp16 else torch.float32)
+    call(
+        "cobra_linear_ln_fwd", a.data_ptr(), w.data_ptr(), b32.data_ptr(), resid.data_ptr(),
+        _dtype_code(resid, "resid"), out.data_ptr(), gw.data_ptr(), gb.data_ptr(), normed.data_ptr(),
+        _dtype_code(normed, "normed"), M, N, K, float(eps), _stream(a),
+    )
+    return out, normed
+
+
+def attn(
+    qkv: torch.Tensor,
+    batch: int,
+    seq_len: int,
+    heads: int,
+    head_dim: int,
+    scale: float,
+    out_dtype: torch.dtype = torch.float16,
+    cfgs=None,
+    causal: bool = True,
+) -> torch.Tensor:
+    """Attention on packed ``qkv [B*S, 3*H*hd]`` -> ``ctx [B*S, H*hd]``.  Mirrors ``_tl_attn`` (TTB:828-854).
+
+    ``cfgs`` (the reference's tile ladder) is accepted and ignored: tiles are
+    chosen inside the library from (seq_len, head_dim).
+    """
+    _dev(qkv, "qkv")
+    if qkv.dtype != torch.float16 or out_dtype != torch.float16:
+        raise TypeError("attention operands and output are float16")
+    D = heads * head_dim
+    if qkv.shape != (batch * seq_len, 3 * D):
+        raise ValueError(f"qkv must be [{batch * seq_len}, {3 * D}], got {tuple(qkv.shape)}")
+    out = torch.empty((batch * seq_len, D), device=qkv.device, dtype=torch.float16)
+    call(
+        "cobra_attn_fwd", qkv.data_ptr(), out.data_ptr(), batch, seq_len, heads, head_dim, float(scale),
+        1 if causal else 0, _stream(qkv),
+    )
+    return out
+
+
+def layer_workspace_bytes(batch: int, seq_len: int, d_model: int, heads: int) -> int:
+    n = _lib.lib().cobra_layer_workspace_bytes(batch, seq_len, d_model, heads)
+    if n < 0:
+        raise ValueError(f"unsupported sublayer shape B={batch} S={seq_len} D={d_model} H={heads}")
+    return int(n)
+
+
+def layer_fwd(
+    x: torch.Tensor,
+    w_qkv: torch.Tensor,
+    b_qkv: torch.Tensor,
+    w_o: torch.Tensor,
+    b_o: torch.Tensor,
+    ln1_w: torch.Tensor,
+    ln1_b: torch.Tensor,
+    ln2_w: torch.Tensor,
+    ln2_b: torch.Tensor,
+    y: torch.Tensor,
+    workspace: torch.Tensor,
+    heads: int,
+    causal: bool,
+    eps: float = 1e-5,
+    resid_out: Optional[torch.Tensor] = None,
+) -> None:
+    """Enqueue the whole sublayer into caller-provided buffers (no allocation).
+
+    x, y: [B, S, D] (same dtype); packed weights as produced by ``CobraAttentionSublayer``.
+    """
+    B, S, D = x.shape
+    call(
+        "cobra_layer_fwd", x.data_ptr(), _dtype_code(x, "x"), w_qkv.data_ptr(), b_qkv.data_ptr(),
+        w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(), ln2_w.data_ptr(),
+        ln2_b.data_ptr(), y.data_ptr(), _ptr(resid_out), workspace.data_ptr(), workspace.numel(),
+        B, S, D, heads, 1 if causal else 0, float(eps), _stream(x),
+    )

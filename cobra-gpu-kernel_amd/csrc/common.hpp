@@ -1,0 +1,104 @@
+// Shared device helpers for the CDNA4 (gfx950) kernels of the attention sublayer.
+//
+// Matrix-core conventions used by every kernel (v_mfma_f32_32x32x16_f16, wave64):
+//   A operand (32 x 16, M x K): lane l holds row (l % 32), k = 8*(l / 32) + e, e = 0..7
+//   B operand (16 x 32, K x N): lane l holds col (l % 32), k = 8*(l / 32) + e
+//   C/D (32 x 32, fp32, 16 regs): lane l, reg r holds
+//        row = 8*(r / 4) + 4*(l / 32) + (r % 4),  col = l % 32
+// Only the pairing of A and B along k matters for a product, so a kernel may
+// feed any permutation of k as long as both operands use the same one; the
+// attention kernel relies on that to use softmax output registers directly as
+// an operand.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cobra {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// dtype codes of the C ABI (include/cobra_amd.h)
+enum : int { kF16 = 0, kF32 = 1 };
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ f32x16 mfma32x32x16(const f16x8& a, const f16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f16x8 zero8() {
+  f16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (f16)0.0f;
+  return z;
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64); every lane of
+// the group receives the group total.  All 64 lanes must execute it.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// 8 consecutive elements <-> fp32 registers.
+__device__ __forceinline__ void load8(const f16* p, float (&v)[8]) {
+  const f16x8 h = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)h[i];
+}
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = a[i];
+    v[i + 4] = b[i];
+  }
+}
+__device__ __forceinline__ void store8(f16* p, const float (&v)[8]) {
+  f16x8 h;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = (f16)v[i];
+  *reinterpret_cast<f16x8*>(p) = h;
+}
+__device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
+  f32x4 a, b;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[i] = v[i];
+    b[i] = v[i + 4];
+  }
+  *reinterpret_cast<f32x4*>(p) = a;
+  *reinterpret_cast<f32x4*>(p + 4) = b;
+}
+
+// Workgroup-id remap so that consecutive logical tiles land on the same XCD
+// (the hardware deals workgroups round-robin over 8 XCDs, each with its own
+// L2).  A bijection on [0, n) for any n.
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+  constexpr int kXcd = 8;
+  if (n < kXcd) return id;
+  const int per = (n + kXcd - 1) / kXcd;  // ids per XCD, rounded up
+  int tall = n % kXcd;                    // XCDs that get `per` ids
+  if (tall == 0) tall = kXcd;
+  const int xcd = id % kXcd, local = id / kXcd;
+  return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+}
+
+}  // namespace cobra

@@ -1,0 +1,64 @@
+// Internal launcher interface between the kernels and the C ABI (capi.hip).
+// Every launcher validates its arguments, enqueues on the given stream and
+// returns a hipError_t; none allocates, frees or synchronises, so each is
+// safe to record into a hipGraph.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cobra {
+
+constexpr int kLnMaxD = 4096;  // widest row the LayerNorm kernels hold in registers
+
+struct LnArgs {
+  const void* x;           // [rows, d], x_dtype
+  int x_dtype;
+  const void* branch;      // optional [rows, d] added to x before the norm
+  int branch_f32;          // branch dtype: 1 = fp32, 0 = fp16
+  const float* gamma;      // [d]
+  const float* beta;       // [d]
+  float* resid_out;        // optional [rows, d] fp32 store of x (+ branch)
+  void* y;                 // [rows, d], y_dtype
+  int y_dtype;
+  int64_t rows;
+  int d;
+  float eps;
+  hipStream_t stream;
+};
+hipError_t run_ln(const LnArgs& a);
+
+struct GemmArgs {
+  const void* a;           // [M, K] fp16, row-major
+  const void* w;           // [N, K] fp16 (nn.Linear layout)
+  const float* bias;       // optional [N] fp32
+  const void* resid;       // optional [M, N] added in the epilogue
+  int resid_dtype;
+  void* c;                 // [M, N] c_dtype; with the LN epilogue: optional fp32 residual store
+  int c_dtype;
+  int64_t M;
+  int N;
+  int K;
+  const float* ln_gamma;   // non-null selects the LayerNorm epilogue (requires N <= 128)
+  const float* ln_beta;
+  void* ln_y;              // [M, N] LayerNorm output
+  int ln_y_dtype;
+  float eps;
+  hipStream_t stream;
+};
+hipError_t run_gemm(const GemmArgs& a);
+
+struct AttnArgs {
+  const void* qkv;         // [B*S, 3*H*hd] fp16: q | k | v column blocks, head-major inside each
+  void* ctx;               // [B*S, H*hd] fp16
+  int64_t batch;
+  int seq_len;
+  int heads;
+  int head_dim;
+  float scale;             // softmax scale (head_dim ** -0.5 in the layer)
+  int causal;
+  hipStream_t stream;
+};
+hipError_t run_attn(const AttnArgs& a);
+
+}  // namespace cobra

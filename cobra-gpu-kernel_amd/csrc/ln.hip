@@ -1,0 +1,120 @@
+// Row LayerNorm with optional residual branch:  r = x (+ branch);  y = LN(r).
+//
+// Replaces the reference's _add_ln_kernel / _tl_add_ln
+// (torch_transformer_benchmark.py:491-569): two-pass fp32 statistics over the
+// row held in registers (mean, then centred biased variance, /N), eps inside
+// the square root, affine, cast on store.
+//
+// Layout: LPR lanes own one row, each lane holds NCH chunks of 8 consecutive
+// elements (16 B of fp16, 32 B of fp32), so every global access is a full
+// vector access and the row reductions never leave the LPR-lane group.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cobra {
+
+template <typename TX, typename TY, int LPR, int NCH>
+__global__ __launch_bounds__(256) void ln_rows_kernel(const TX* __restrict__ x, const void* __restrict__ branch,
+                                                      int branch_f32, const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta, float* __restrict__ resid_out,
+                                                      TY* __restrict__ y, int64_t rows, int d, float eps) {
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * (blockDim.x >> 6) + wave) * RPW + lane / LPR;
+  const bool active = row < rows;
+  const int nch = d >> 3;
+  const int64_t base = row * d;
+
+  float v[NCH][8];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int ch = li + c * LPR;
+    if (active && ch < nch) {
+      load8(x + base + ch * 8, v[c]);
+      if (branch) {
+        float bv[8];
+        if (branch_f32)
+          load8(static_cast<const float*>(branch) + base + ch * 8, bv);
+        else
+          load8(static_cast<const f16*>(branch) + base + ch * 8, bv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[c][i] += bv[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += v[c][i];
+  }
+  const float mean = group_sum<LPR>(s) / (float)d;
+
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (active && li + c * LPR < nch) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float t = v[c][i] - mean;
+        q += t * t;
+      }
+    }
+  }
+  const float rstd = rsqrtf(group_sum<LPR>(q) / (float)d + eps);
+
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int ch = li + c * LPR;
+    if (!(active && ch < nch)) continue;
+    if (resid_out) store8(resid_out + base + ch * 8, v[c]);
+    const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + ch * 8);
+    const f32x4 g1 = *reinterpret_cast<const f32x4*>(gamma + ch * 8 + 4);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(beta + ch * 8);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(beta + ch * 8 + 4);
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[i] = (v[c][i] - mean) * rstd * g0[i] + b0[i];
+      o[i + 4] = (v[c][i + 4] - mean) * rstd * g1[i] + b1[i];
+    }
+    store8(y + base + ch * 8, o);
+  }
+}
+
+template <typename TX, typename TY, int LPR, int NCH>
+static hipError_t launch_ln(const LnArgs& a) {
+  constexpr int RPB = 4 * (64 / LPR);  // rows per 256-thread block
+  const int64_t blocks = (a.rows + RPB - 1) / RPB;
+  hipLaunchKernelGGL((ln_rows_kernel<TX, TY, LPR, NCH>), dim3((unsigned)blocks), dim3(256), 0, a.stream,
+                     static_cast<const TX*>(a.x), a.branch, a.branch_f32, a.gamma, a.beta, a.resid_out,
+                     static_cast<TY*>(a.y), a.rows, a.d, a.eps);
+  return hipGetLastError();
+}
+
+template <typename TX, typename TY>
+static hipError_t dispatch_ln_geometry(const LnArgs& a) {
+  const int nch = a.d / 8;
+  if (nch <= 4) return launch_ln<TX, TY, 4, 1>(a);
+  if (nch <= 8) return launch_ln<TX, TY, 8, 1>(a);
+  if (nch <= 16) return launch_ln<TX, TY, 16, 1>(a);
+  if (nch <= 32) return launch_ln<TX, TY, 32, 1>(a);
+  if (nch <= 64) return launch_ln<TX, TY, 64, 1>(a);
+  if (nch <= 128) return launch_ln<TX, TY, 64, 2>(a);
+  if (nch <= 256) return launch_ln<TX, TY, 64, 4>(a);
+  return launch_ln<TX, TY, 64, 8>(a);
+}
+
+hipError_t run_ln(const LnArgs& a) {
+  if (a.rows < 0 || a.d <= 0 || a.d % 8 != 0 || a.d > kLnMaxD) return hipErrorInvalidValue;
+  if (a.rows == 0) return hipSuccess;
+  if (a.x_dtype == kF16 && a.y_dtype == kF16) return dispatch_ln_geometry<f16, f16>(a);
+  if (a.x_dtype == kF16 && a.y_dtype == kF32) return dispatch_ln_geometry<f16, float>(a);
+  if (a.x_dtype == kF32 && a.y_dtype == kF16) return dispatch_ln_geometry<float, f16>(a);
+  if (a.x_dtype == kF32 && a.y_dtype == kF32) return dispatch_ln_geometry<float, float>(a);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cobra

@@ -1,0 +1,110 @@
+/*
+ * cobra_amd -- C ABI of the MI355X (gfx950) attention-sublayer forward.
+ *
+ * The reference (dalberrt/COBRA-GPU-Kernel) is a single Python file whose GPU
+ * path is five Triton kernels behind Python launchers; it has no native ABI.
+ * Each entry point below replaces one of those launchers (cited as
+ * torch_transformer_benchmark.py:LINE, "TTB"), so a host that used the
+ * reference's ops can bind these symbols instead (ctypes / cffi / any FFI).
+ *
+ * Conventions shared by every entry point:
+ *   - all tensors are device pointers to row-major, densely packed buffers,
+ *     16-byte aligned; the caller allocates every buffer (outputs included);
+ *   - dtype codes: COBRA_F16 (IEEE half) or COBRA_F32;
+ *   - `stream` is a hipStream_t (NULL = legacy default stream).  Work is only
+ *     enqueued: nothing allocates, frees or synchronises, so every call may be
+ *     captured into a hipGraph;
+ *   - the return value is a hipError_t code: 0 on success, non-zero when the
+ *     arguments are rejected (nothing is enqueued then) or the launch failed.
+ *     cobra_error_string() names it.  No C++ exception crosses the ABI.
+ */
+#ifndef COBRA_AMD_H
+#define COBRA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define COBRA_ABI_VERSION 1
+
+enum { COBRA_F16 = 0, COBRA_F32 = 1 };
+
+/* ABI version of the loaded library (COBRA_ABI_VERSION it was built with). */
+int cobra_version(void);
+
+/* Human-readable name of a code returned by any entry point. */
+const char* cobra_error_string(int code);
+
+/*
+ * Row LayerNorm with optional residual branch:
+ *     r = x + branch (branch optional);  resid_out = r (optional, fp32);
+ *     y = (r - mean(r)) * rsqrt(var(r) + eps) * gamma + beta     (biased var)
+ * x, branch, y: [rows, d]; gamma, beta: [d] fp32.  d % 8 == 0, d <= 4096.
+ * Replaces _tl_add_ln / _add_ln_kernel (TTB:539-569, 491-535); row masks of
+ * the reference (MASK_RESID / MASK_OUT) are not part of this entry point.
+ */
+int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtype, const float* gamma,
+                 const float* beta, float* resid_out, void* y, int y_dtype, int64_t rows, int64_t d, float eps,
+                 void* stream);
+
+/*
+ * Projection GEMM with fused epilogue:
+ *     c = a . w^T + bias (+ resid)
+ * a: [M, K] fp16, w: [N, K] fp16 (nn.Linear weight layout), bias: [N] fp32
+ * (optional), resid: [M, N] (optional), c: [M, N] in c_dtype.  fp32 accumulate.
+ * K % 8 == 0.  Replaces _tl_linear / _gemm_kernel (TTB:355-381, 283-353)
+ * without the GELU and row-mask options (FFN and padding are not on this path).
+ */
+int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype, void* c,
+                     int c_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * Projection GEMM + residual + LayerNorm over whole rows:
+ *     r = a . w^T + bias + resid;  resid_out = r (optional, fp32);
+ *     y = LayerNorm(r) * gamma + beta
+ * Shapes as cobra_linear_fwd; requires N <= 128 (one workgroup owns a row) and
+ * N % 8 == 0.  Replaces _tl_linear_ln / _gemm_ln_kernel (TTB:465-488, 394-463).
+ */
+int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
+                        float* resid_out, const float* gamma, const float* beta, void* y, int y_dtype, int64_t M,
+                        int64_t N, int64_t K, float eps, void* stream);
+
+/*
+ * Multi-head attention on a packed projection buffer:
+ *     qkv: [batch*seq_len, 3*D] fp16 with column blocks q | k | v, each split
+ *          into `heads` contiguous slices of head_dim (D = heads*head_dim);
+ *     ctx: [batch*seq_len, D] fp16, ctx_i = softmax((q_i k^T) * scale) v per head.
+ * causal != 0 masks keys j > i.  head_dim % 8 == 0, head_dim <= 256.
+ * Replaces _tl_attn / _attn_kernel (TTB:828-854, 572-649; causal only there)
+ * and the SDPA call used for non-causal attention (TTB:1240-1253).
+ */
+int cobra_attn_fwd(const void* qkv, void* ctx, int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim,
+                   float scale, int causal, void* stream);
+
+/* Device workspace (bytes) cobra_layer_fwd needs for this shape. */
+int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads);
+
+/*
+ * The whole attention sublayer (TTB:141-142 with TTB:88-123):
+ *     h = LN1(x);  [q|k|v] = h . w_qkv^T + b_qkv;  c = MHA(q, k, v)
+ *     r = x + (c . w_o^T + b_o);   y = LN2(r)
+ * x, y: [batch*seq_len, d_model] in x_dtype; w_qkv: [3*d_model, d_model] fp16
+ * (rows: q_proj, k_proj, v_proj weights, in that order); b_qkv: [3*d_model]
+ * fp32; w_o: [d_model, d_model] fp16; b_o and the LayerNorm parameters fp32.
+ * resid_out (optional): r in fp32.  workspace: cobra_layer_workspace_bytes().
+ * Replaces the attention half of UserOptimizedTransformer._run_fused
+ * (TTB:1216-1268), which is what its CUDA graph replays (TTB:1331-1360).
+ */
+int cobra_layer_fwd(const void* x, int x_dtype, const void* w_qkv, const float* b_qkv, const void* w_o,
+                    const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
+                    const float* ln2_b, void* y, float* resid_out, void* workspace, int64_t workspace_bytes,
+                    int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COBRA_AMD_H */

@@ -1,0 +1,59 @@
+"""Shared helpers of the GPU parity tests (not collected: no test_ prefix)."""
+
+from __future__ import annotations
+
+import sys
+
+import torch
+
+from oracle import compare_outputs, make_input, make_sublayer, quantize_like
+from oracle.cases import LayerCase, oracle_forward
+
+DEV = torch.device("cuda:0") if torch.cuda.is_available() else None
+
+
+def log(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def build_pair(d_model: int, heads: int, seed: int = 0, dtype: torch.dtype = torch.float16):
+    """(fp32 oracle on dtype-rounded weights, HIP module in dtype on the GPU)."""
+    from cobra_amd import CobraAttentionSublayer
+
+    ref = make_sublayer(d_model, heads, seed=seed)
+    if dtype == torch.float16:
+        quantize_like(ref, torch.float16)
+    mod = CobraAttentionSublayer(d_model, heads)
+    mod.load_state_dict(ref.state_dict(), strict=True)
+    mod = mod.to(device=DEV, dtype=dtype).eval()
+    return ref, mod
+
+
+def oracle_on(ref, x: torch.Tensor, causal: bool, device, block_q=None, return_residual=False):
+    """Run the fp32 oracle on ``device`` (CPU for small cases, the GPU for big ones)."""
+    layer = ref.to(device)
+    try:
+        out = oracle_forward(layer, x.to(device), causal=causal, block_q=block_q, return_residual=return_residual)
+    finally:
+        ref.to("cpu")
+    if return_residual:
+        return out[0].cpu(), out[1].cpu()
+    return out.cpu()
+
+
+def check_case(case: LayerCase, seed: int = 0, input_seed: int = 0, oracle_device="cpu", subset=None):
+    """Run the HIP sublayer on the full batch; compare (a subset of) sequences."""
+    log(f"[case] {case.name} B{case.batch} S{case.seq_len} D{case.d_model} H{case.heads} causal={case.causal}")
+    ref, mod = build_pair(case.d_model, case.heads, seed=seed)
+    x = make_input(case.batch, case.seq_len, case.d_model, seed=input_seed).half()
+    with torch.inference_mode():
+        y = mod(x.to(DEV), causal=case.causal)
+        torch.cuda.synchronize()
+    y = y.float().cpu()
+    rows = list(range(case.batch)) if subset is None else subset
+    want = oracle_on(ref, x[rows].float(), case.causal, oracle_device)
+    res = compare_outputs(want, y[rows])
+    log(f"[case] {case.name}: max_abs={res.max_abs_error:.3e} max_rel={res.max_relative_error:.3e} "
+        f"failed={res.failed_elements}/{res.total_elements}")
+    return res

@@ -1,0 +1,180 @@
+"""CPU tests of the host side: C-ABI library, planner, drop-in contract."""
+
+import ast
+import os
+import re
+
+import pytest
+import torch
+
+from oracle import OracleAttentionSublayer, make_sublayer
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cobra_amd.h")
+PKG = os.path.join(ROOT, "cobra-gpu-kernel_amd", "cobra_amd")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\*?\s+\*?(cobra_[a-z0-9_]+)\(", text, re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from cobra_amd import _lib
+
+    lib = _lib.lib()
+    names = _header_functions()
+    assert len(names) >= 8
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in cobra_amd.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert lib.cobra_version() == _lib.ABI_VERSION
+    assert lib.cobra_error_string(0)
+
+
+def test_argument_validation_rejects_before_any_launch():
+    """Invalid arguments return an error without touching the GPU."""
+    from cobra_amd import _lib
+
+    lib = _lib.lib()
+    bad = lib.cobra_ln_fwd(None, 0, None, 0, None, None, None, None, 0, 8, 128, 1e-5, None)
+    assert bad != 0
+    assert lib.cobra_attn_fwd(16, 16, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
+    assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10) == -1      # head_dim 12
+    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 4) > 0
+
+
+def test_workspace_size_formula():
+    from cobra_amd import ops
+
+    # h fp16 [T, D] + qkv fp16 [T, 3D] (+ fp32 residual for D > 128), 256-B aligned
+    assert ops.layer_workspace_bytes(64, 128, 128, 4) == 8192 * 128 * 2 + 8192 * 384 * 2
+    t, d = 32 * 100000, 1024
+    assert ops.layer_workspace_bytes(32, 100000, 1024, 16) == t * d * 2 + t * 3 * d * 2 + t * d * 4
+
+
+def test_state_dict_identical_to_reference_sublayer():
+    from cobra_amd import CobraAttentionSublayer
+
+    ref = make_sublayer(128, 4, seed=0)
+    torch.manual_seed(0)
+    mod = CobraAttentionSublayer(128, 4)
+    sd_r, sd_m = ref.state_dict(), mod.state_dict()
+    assert list(sd_r) == list(sd_m)
+    for k in sd_r:
+        assert torch.equal(sd_r[k], sd_m[k]), k  # same seeded draws, same order
+    mod.load_state_dict(sd_r, strict=True)
+    ref.load_state_dict(sd_m, strict=True)
+
+
+def test_module_refuses_to_run_without_gpu():
+    from cobra_amd import CobraAttentionSublayer
+
+    mod = CobraAttentionSublayer(128, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        mod(torch.zeros(1, 4, 128))
+
+
+def test_ops_reject_host_tensors():
+    from cobra_amd import ops
+
+    with pytest.raises(ValueError, match="device"):
+        ops.linear(torch.zeros(4, 8, dtype=torch.float16), torch.zeros(8, 8, dtype=torch.float16), None)
+    with pytest.raises(NotImplementedError):
+        ops.linear(torch.zeros(4, 8), torch.zeros(8, 8), None, gelu=True)
+
+
+def test_product_never_imports_the_oracle():
+    for root, _, files in os.walk(os.path.join(ROOT, "cobra-gpu-kernel_amd")):
+        for f in files:
+            if not f.endswith(".py"):
+                continue
+            tree = ast.parse(open(os.path.join(root, f)).read())
+            for node in ast.walk(tree):
+                if isinstance(node, ast.Import):
+                    mods = [a.name for a in node.names]
+                elif isinstance(node, ast.ImportFrom):
+                    mods = [node.module or ""]
+                else:
+                    continue
+                assert not any(m.split(".")[0] == "oracle" for m in mods), f"{f} imports the oracle"
+
+
+# ---- streaming planner (TTB:1364-1508 restated as pure functions) ----------
+
+def test_should_stream_rules():
+    from cobra_amd.streaming import should_stream
+
+    gib = 1 << 30
+    assert should_stream(False, 10, 1, 0, 100 * gib)            # host input always streams
+    assert not should_stream(True, gib - 1, 32, 10**15, gib)     # small input never
+    assert not should_stream(True, 2 * gib, 1, 10**15, gib)      # one sequence: nothing to split
+    assert should_stream(True, 2 * gib, 4, 61 * gib, 100 * gib)  # live set > 60 % of free
+    assert not should_stream(True, 2 * gib, 4, 59 * gib, 100 * gib)
+
+
+def test_plan_chunk():
+    from cobra_amd.streaming import plan_chunk
+
+    assert plan_chunk(32, 10, 1000) == 32
+    assert plan_chunk(32, 100, 1000) == 6      # 600 // 100
+    assert plan_chunk(32, 10**9, 1000) == 1    # never below one sequence
+
+
+def test_long_config_fits_one_pass_on_288gb():
+    """B32 S1e5 D1024 fp16 on a 288 GB device: one chunk, no streaming."""
+    from cobra_amd import ops
+    from cobra_amd.streaming import live_bytes_per_sequence, plan_chunk, should_stream
+
+    per_seq = live_bytes_per_sequence(ops.layer_workspace_bytes(1, 100000, 1024, 16), 100000, 1024, 2)
+    free = 280 * 10**9
+    assert not should_stream(True, 32 * 100000 * 1024 * 2, 32, 32 * per_seq, free)
+    assert plan_chunk(32, per_seq, free) == 32
+    assert plan_chunk(32, per_seq, 16 * 10**9) < 32
+
+
+class _FakeOOM(Exception):
+    pass
+
+
+def test_halve_on_oom_then_succeed():
+    from cobra_amd.streaming import run_chunked
+
+    calls, frees = [], []
+
+    def run(b0, b1):
+        calls.append((b0, b1))
+        if b1 - b0 > 3:
+            raise _FakeOOM()
+
+    done = run_chunked(10, 8, run, lambda: frees.append(1), lambda e: isinstance(e, _FakeOOM))
+    assert done == [(0, 2), (2, 4), (4, 6), (6, 8), (8, 10)]
+    assert calls[:2] == [(0, 8), (0, 4)] and len(frees) == 2
+
+
+def test_oom_at_step_one_propagates():
+    from cobra_amd.streaming import run_chunked
+
+    def run(b0, b1):
+        raise _FakeOOM()
+
+    with pytest.raises(_FakeOOM):
+        run_chunked(4, 4, run, lambda: None, lambda e: isinstance(e, _FakeOOM))
+
+
+def test_non_oom_errors_propagate_immediately():
+    from cobra_amd.streaming import run_chunked
+
+    def run(b0, b1):
+        raise ValueError("boom")
+
+    with pytest.raises(ValueError):
+        run_chunked(4, 2, run, lambda: None, lambda e: isinstance(e, _FakeOOM))
+
+
+def test_oracle_and_product_share_parameter_names():
+    from cobra_amd import CobraAttentionSublayer
+
+    a = dict(OracleAttentionSublayer(64, 2).named_parameters())
+    b = dict(CobraAttentionSublayer(64, 2).named_parameters())
+    assert {k: v.shape for k, v in a.items()} == {k: v.shape for k, v in b.items()}
