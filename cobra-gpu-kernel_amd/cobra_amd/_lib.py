@@ -19,6 +19,8 @@ ABI_VERSION = 1
 
 F16 = 0
 F32 = 1
+PLAN_FUSED = 0
+PLAN_STAGED = 1
 
 _c_int = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -36,6 +38,7 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_f32, _vp],
     ),
     "cobra_attn_fwd": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp]),
+    "cobra_layer_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "cobra_layer_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "cobra_layer_fwd": (
         _c_int,

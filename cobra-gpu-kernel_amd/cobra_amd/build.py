@@ -37,6 +37,14 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-file backend options.  The fused sublayer kernel keeps MFMA results in
+# VGPRs (its accumulators feed VALU softmax / LayerNorm work directly); the
+# default AGPR form costs ~900 extra accumulator copy instructions there.
+FILE_FLAGS = {
+    "layer_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -50,7 +58,8 @@ def sources() -> List[str]:
 
 def _compile(src: str, cc: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [cc, *DEVICE_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c", src, "-o", obj]
+    cmd = [cc, *DEVICE_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-I", INCLUDE, "-I", CSRC,
+           "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stdout}\n{res.stderr}")

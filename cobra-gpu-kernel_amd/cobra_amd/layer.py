@@ -16,9 +16,13 @@ mirrors the reference's orchestration (TTB:857-1541):
   matrix in that order (TTB:876-883), fp16 ``W_o``, fp32 biases and LayerNorm
   parameters.  The pack is rebuilt whenever a parameter changes (in-place
   updates bump its version), which the reference did only on shape changes;
-* small inputs (<= 64 MiB, TTB:1077-1079) are captured once into a hipGraph
-  (``torch.cuda.CUDAGraph`` on ROCm) and replayed; the output buffer is
-  returned without a clone, as the reference does (TTB:1356-1360);
+* the library picks the plan: one fused kernel for the whole sublayer
+  (S <= 128, d_model <= 128) or a staged pipeline of four kernels.  A staged
+  plan on a small input (<= 64 MiB, TTB:1077-1079) is captured once into a
+  hipGraph (``torch.cuda.CUDAGraph`` on ROCm) and replayed, with the output
+  buffer returned without a clone as the reference does (TTB:1356-1360); the
+  fused plan is one direct launch, because replaying a one-node graph costs
+  about four times a direct launch on this runtime (``graph=True`` forces it);
 * inputs that do not fit one device pass are streamed in batch chunks sized
   from ``hipMemGetInfo`` with halve-on-OOM (``streaming``, TTB:1364-1508).
 """
@@ -60,9 +64,9 @@ class CobraSelfAttention(nn.Module):
 class _Pack:
     """Kernel-ready copies of the parameters (never registered on the module)."""
 
-    __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "key")
+    __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "versions")
 
-    def __init__(self, m: "CobraAttentionSublayer", key) -> None:
+    def __init__(self, m: "CobraAttentionSublayer", versions) -> None:
         att = m.attention
         with torch.no_grad():
             self.w_qkv = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(
@@ -74,17 +78,24 @@ class _Pack:
             self.ln1_b = m.norm1.bias.float().contiguous()
             self.ln2_w = m.norm2.weight.float().contiguous()
             self.ln2_b = m.norm2.bias.float().contiguous()
-        self.key = key
+        self.versions = versions
 
 
 class CobraAttentionSublayer(nn.Module):
-    def __init__(self, d_model: int, num_heads: int, causal: bool = False, eps: float = 1e-5) -> None:
+    def __init__(self, d_model: int, num_heads: int, causal: bool = False, eps: float = 1e-5,
+                 graph: Optional[bool] = None) -> None:
         super().__init__()
         # Construction order = BaselineTransformerBlock's first members (TTB:129-131).
         self.norm1 = nn.LayerNorm(d_model, eps=eps)
         self.attention = CobraSelfAttention(d_model, num_heads)
         self.norm2 = nn.LayerNorm(d_model, eps=eps)
         self.causal = causal
+        # hipGraph replay: None = automatic (multi-kernel plans on inputs <= 64 MiB;
+        # a single-kernel plan launches directly, which measures ~4x cheaper than
+        # replaying a one-node graph); True / False force it.
+        self.graph = graph
+        self.plan: Optional[int] = None
+        self._params = list(self.parameters())
         self._pack: Optional[_Pack] = None
         self._sig = None
         self._ws: Optional[torch.Tensor] = None
@@ -96,15 +107,21 @@ class CobraAttentionSublayer(nn.Module):
 
     # -- parameters ---------------------------------------------------------
 
-    def _param_key(self):
-        return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in self.parameters())
+    def _apply(self, fn, *args, **kwargs):
+        # .to() / .half() / .cuda() replace parameter storage: drop every cache.
+        out = super()._apply(fn, *args, **kwargs)
+        self._params = list(self.parameters())
+        self._pack = None
+        self._sig = None
+        return out
 
     def _packed(self) -> _Pack:
-        key = self._param_key()
-        if self._pack is None or self._pack.key != key:
+        # In-place updates (load_state_dict, optimiser-style edits) bump _version.
+        versions = tuple([p._version for p in self._params])
+        if self._pack is None or self._pack.versions != versions:
             if not self.norm1.weight.is_cuda:
                 raise RuntimeError("CobraAttentionSublayer runs on the GPU only: move it with .to('cuda')")
-            self._pack = _Pack(self, key)
+            self._pack = _Pack(self, versions)
             self._graph = None  # the graph baked in the old buffers' addresses
         return self._pack
 
@@ -120,31 +137,46 @@ class CobraAttentionSublayer(nn.Module):
         causal = self.causal if causal is None else bool(causal)
         if valid_token_mask is not None and not bool(valid_token_mask.all()):
             raise NotImplementedError("padded sequences (valid_token_mask with False entries) are not supported yet")
-        if x.dim() != 3 or x.shape[-1] != self.attention.d_model:
-            raise ValueError(f"x must be [B, S, {self.attention.d_model}], got {tuple(x.shape)}")
-        if x.dtype not in (torch.float16, torch.float32):
-            raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
         pack = self._packed()
-        if self._stream_needed(x):
-            return self._run_streamed(x, causal, return_residual)
-        x = x.contiguous()
-        sig = (tuple(x.shape), x.dtype, x.device, causal, return_residual)
+        # Free memory moves between calls, so big or host-resident inputs are
+        # re-checked every time (TTB:1402-1406); small ones never pay for it.
+        if not x.is_cuda or x.numel() * x.element_size() >= streaming.STREAM_MIN_BYTES:
+            self._validate(x)
+            if self._stream_needed(x):
+                return self._run_streamed(x, causal, return_residual)
+        sig = (x.shape, x.dtype, x.device, causal, return_residual)
         if sig != self._sig:
+            self._validate(x)
             self._prepare(sig, x)
+        if not x.is_contiguous():
+            x = x.contiguous()
         if self._graph_ok:
             return self._run_graphed(x, pack, causal, return_residual)
         return self._run_eager(x, pack, causal, return_residual)
 
     # -- planning -------------------------------------------------------------
 
+    def _validate(self, x: torch.Tensor) -> None:
+        if x.dim() != 3 or x.shape[-1] != self.attention.d_model:
+            raise ValueError(f"x must be [B, S, {self.attention.d_model}], got {tuple(x.shape)}")
+        if x.dtype not in (torch.float16, torch.float32):
+            raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
+
     def _prepare(self, sig, x: torch.Tensor) -> None:
+        """Per-signature set-up (the reference's _prepare, TTB:948-1081): plan,
+        workspace, graph gate.  Never runs on the steady-state path."""
         B, S, D = x.shape
-        self._sig = sig
-        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, self.attention.num_heads),
-                               dtype=torch.uint8, device=x.device)
-        self._graph_ok = x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
+        H = self.attention.num_heads
+        self.plan = ops.layer_plan(B, S, D, H)
+        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H), dtype=torch.uint8, device=x.device)
+        small = x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
+        if self.graph is None:
+            self._graph_ok = small and self.plan != ops.PLAN_FUSED
+        else:
+            self._graph_ok = bool(self.graph) and small
         self._graph = None
         self._static_x = self._static_y = self._static_r = None
+        self._sig = sig
 
     def _launch(self, x, y, r, pack: _Pack, ws: torch.Tensor, causal: bool) -> None:
         ops.layer_fwd(x, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w, pack.ln1_b, pack.ln2_w,
@@ -189,7 +221,7 @@ class CobraAttentionSublayer(nn.Module):
         dev = self.norm1.weight.device
         nbytes = x.numel() * x.element_size()
         if x.is_cuda and nbytes < streaming.STREAM_MIN_BYTES:
-            return False  # small shapes never pay for the free-memory query
+            return False
         free, _ = torch.cuda.mem_get_info(dev)
         live = self._per_seq_bytes(x, False) * x.shape[0]
         return streaming.should_stream(x.is_cuda, nbytes, x.shape[0], live, free)

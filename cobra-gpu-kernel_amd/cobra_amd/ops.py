@@ -206,6 +206,18 @@ def attn(
     return out
 
 
+PLAN_FUSED = _lib.PLAN_FUSED
+PLAN_STAGED = _lib.PLAN_STAGED
+
+
+def layer_plan(batch: int, seq_len: int, d_model: int, heads: int) -> int:
+    """PLAN_FUSED (one kernel) or PLAN_STAGED for this shape (host-only query)."""
+    p = _lib.lib().cobra_layer_plan(batch, seq_len, d_model, heads)
+    if p < 0:
+        raise ValueError(f"unsupported sublayer shape B={batch} S={seq_len} D={d_model} H={heads}")
+    return int(p)
+
+
 def layer_workspace_bytes(batch: int, seq_len: int, d_model: int, heads: int) -> int:
     n = _lib.lib().cobra_layer_workspace_bytes(batch, seq_len, d_model, heads)
     if n < 0:

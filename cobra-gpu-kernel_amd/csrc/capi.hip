@@ -97,9 +97,15 @@ int cobra_attn_fwd(const void* qkv, void* ctx, int64_t batch, int64_t seq_len, i
   return code(cobra::run_attn(a));
 }
 
-int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads) {
+int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads) {
   if (!layer_shape_ok(batch, seq_len, d_model, heads)) return -1;
-  return layer_buffers(batch * seq_len, d_model).total;
+  return cobra::layer_small_ok(seq_len, d_model, heads) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
+}
+
+int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads) {
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads);
+  if (plan < 0) return -1;
+  return plan == COBRA_PLAN_FUSED ? 0 : layer_buffers(batch * seq_len, d_model).total;
 }
 
 int cobra_layer_fwd(const void* x, int x_dtype, const void* w_qkv, const float* b_qkv, const void* w_o,
@@ -107,17 +113,24 @@ int cobra_layer_fwd(const void* x, int x_dtype, const void* w_qkv, const float* 
                     const float* ln2_b, void* y, float* resid_out, void* workspace, int64_t workspace_bytes,
                     int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
                     void* stream) {
-  if (!layer_shape_ok(batch, seq_len, d_model, heads) || !is_dtype(x_dtype)) return kBad;
-  const void* must[] = {x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, workspace};
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads);
+  if (plan < 0 || !is_dtype(x_dtype)) return kBad;
+  const void* must[] = {x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y};
   for (const void* p : must)
     if (!p || !aligned16(p)) return kBad;
-  if (!opt_aligned16(resid_out)) return kBad;
+  if (!opt_aligned16(resid_out) || !opt_aligned16(workspace)) return kBad;
   const int64_t T = batch * seq_len;
   const int64_t D = d_model;
-  const LayerBuffers lb = layer_buffers(T, D);
-  if (workspace_bytes < lb.total) return kBad;
-  if (T == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (plan == COBRA_PLAN_FUSED) {
+    if (T == 0) return 0;
+    cobra::SmallLayerArgs a{x,     x_dtype, w_qkv, b_qkv, w_o,     b_o,     ln1_w,     ln1_b,   ln2_w, ln2_b,
+                            y,     resid_out, batch, seq_len, d_model, heads, causal ? 1 : 0, eps, s};
+    return code(cobra::run_layer_small(a));
+  }
+  const LayerBuffers lb = layer_buffers(T, D);
+  if (!workspace || workspace_bytes < lb.total) return kBad;
+  if (T == 0) return 0;
   char* ws = static_cast<char*>(workspace);
   void* h = ws + lb.h_off;
   void* qkv = ws + lb.qkv_off;

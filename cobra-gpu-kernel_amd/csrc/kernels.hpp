@@ -61,4 +61,29 @@ struct AttnArgs {
 };
 hipError_t run_attn(const AttnArgs& a);
 
+// Whole sublayer in one kernel (layer_small.hip).
+struct SmallLayerArgs {
+  const void* x;           // [B*S, D], x_dtype
+  int x_dtype;
+  const void* w_qkv;       // [3D, D] fp16
+  const float* b_qkv;      // [3D]
+  const void* w_o;         // [D, D] fp16
+  const float* b_o;        // [D]
+  const float* ln1_w;
+  const float* ln1_b;
+  const float* ln2_w;
+  const float* ln2_b;
+  void* y;                 // [B*S, D], x_dtype
+  float* resid_out;        // optional fp32 residual
+  int64_t batch;
+  int64_t seq_len;
+  int64_t d_model;
+  int64_t heads;
+  int causal;
+  float eps;
+  hipStream_t stream;
+};
+bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads);
+hipError_t run_layer_small(const SmallLayerArgs& a);
+
 }  // namespace cobra

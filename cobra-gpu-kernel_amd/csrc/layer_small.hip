@@ -1,0 +1,514 @@
+// The whole attention sublayer in ONE kernel for short sequences and narrow
+// models (S <= 128, d_model <= 128, head_dim in {32, 64}): one wave per 32
+// tokens, persistent workgroups that loop over sequences.
+//
+//   h = LN1(x);  q,k,v = h W^T + b;  ctx = softmax(q k^T * scale) v;
+//   r = x + ctx W_o^T + b_o;  y = LN2(r)
+//
+// This is the fusion of the reference's _add_ln_kernel, _qkvattn_kernel and
+// _gemm_ln_kernel (torch_transformer_benchmark.py:491-535, 654-741, 394-463),
+// which the reference ran as three launches inside a CUDA graph; here nothing
+// but x, the weights and y touches HBM.
+//
+// Every intermediate stays in the register layout the next matrix product
+// consumes (v_mfma_f32_32x32x16_f16, conventions in common.hpp):
+//   * LN1 is computed in the lane that owns token (lane % 32) and k-slice
+//     8*(lane / 32) of each 16-wide k-step -- exactly the B operand of
+//     Q^T = W_q h^T and K^T = W_k h^T, and the A operand of V = h W_v^T;
+//   * the C layout of Q^T / K^T puts d-values {4g..4g+3, 8+4g..8+4g+3} of one
+//     token in lane (token, g); that is the (k-permuted) operand layout of
+//     S^T = K Q^T, so Q never leaves the registers and K is written to LDS as
+//     ready-made 16-byte operand chunks for the other waves;
+//   * the C layout of V holds, for one d, keys {4g.., 8+4g..} -- the A operand
+//     of O^T = V^T P^T in the same key order as the probabilities, which come
+//     straight from the S^T accumulators;
+//   * O^T holds, per lane, one query and d-values in that same permuted order:
+//     the B operand of out^T = W_o ctx^T.  out^T then holds 64 of the 128
+//     values of one output row per lane (the rest in lane ^ 32), so LN2 is an
+//     in-lane sum plus one lane-pair exchange.
+// With all keys of the sequence present (S <= 128) the softmax is exact in one
+// pass: no running max, no rescaling.
+//
+// All weights (W_qkv and W_o, 128 KB at d_model 128) are staged into LDS once
+// per workgroup, already cut into the 16-byte per-lane operand chunks of the
+// products above, so every matrix operand is one conflict-free ds_read_b128
+// and no product waits on a global load.  Each workgroup then walks sequences
+// blockIdx.x, blockIdx.x + gridDim.x, ... so the weights are loaded once per
+// CU rather than once per sequence.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cobra {
+
+namespace {
+
+__device__ __forceinline__ void store4(f16* p, const float (&v)[4]) {
+  f16x4 h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = (f16)v[i];
+  *reinterpret_cast<f16x4*>(p) = h;
+}
+__device__ __forceinline__ void store4(float* p, const float (&v)[4]) {
+  f32x4 a;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = v[i];
+  *reinterpret_cast<f32x4*>(p) = a;
+}
+
+// A zero the optimiser cannot see through.  Offsetting the parameter
+// pointers by it inside the persistent sequence loop keeps their loads in the
+// loop (hoisting them would pin every LayerNorm and bias parameter in
+// registers for the kernel's lifetime) while the pointers stay global.
+__device__ __forceinline__ int opaque_zero() {
+  int z = 0;
+  asm volatile("" : "+s"(z));
+  return z;
+}
+
+// Registers 8*half .. 8*half+7 of a 32x32 accumulator times `scale`, as fp16.
+__device__ __forceinline__ f16x8 scaled_f16(const f32x16& acc, int half, float scale) {
+  f16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (f16)(acc[8 * half + e] * scale);
+  return o;
+}
+
+// Registers 8*half .. 8*half+7 of a 32x32 accumulator (+ per-register bias), as fp16.
+__device__ __forceinline__ f16x8 half_to_f16(const f32x16& acc, int half, const float (&bias)[16]) {
+  f16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (f16)(acc[8 * half + e] + bias[8 * half + e]);
+  return o;
+}
+
+}  // namespace
+
+constexpr int kSmallMaxS = 128;
+constexpr int kLdsBytes = 163840;  // gfx950: LDS per workgroup
+
+// LDS plan of the fused kernel, in 16-byte chunks.
+template <int D, int HD>
+struct SmallLds {
+  static constexpr int KD = D / 16;
+  static constexpr int NDT = HD / 32;
+  static constexpr int KSH = HD / 16;
+  static constexpr int MAXT = kSmallMaxS / 32;
+  static constexpr int WQKV = 3 * (D / 32) * KD * 64;
+  static constexpr int WO = (D / 32) * KD * 64;
+  static constexpr int KCH = MAXT * KSH * 64;
+  static constexpr int VCH = MAXT * NDT * 2 * 64;
+  static constexpr int CORE = WQKV + WO + KCH + VCH;
+  // Biases and LayerNorm parameters [b_qkv 3D | b_o | g1 | b1 | g2 | b2] = 8D
+  // floats, kept in LDS too when they fit (otherwise read from global memory).
+  static constexpr int PCH = 8 * D * 4 / 16;
+  static constexpr bool PARAMS = (CORE + PCH) * 16 <= kLdsBytes;
+  static constexpr int TOTAL = CORE + (PARAMS ? PCH : 0);
+  static_assert(D % 32 == 0 && HD % 32 == 0 && D % HD == 0, "layout");
+  static_assert(CORE * 16 <= kLdsBytes, "weights + K/V must fit the workgroup's LDS");
+};
+
+template <typename TX>
+struct XChunks;
+template <>
+struct XChunks<f16> {
+  using c8 = f16x8;
+  using c4 = f16x4;
+};
+template <>
+struct XChunks<float> {
+  using c8 = float __attribute__((ext_vector_type(8)));
+  using c4 = f32x4;
+};
+
+template <int D, int HD, bool CAUSAL, typename TX>
+__global__ __launch_bounds__(256) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
+                                                          const float* __restrict__ bqkv, const f16* __restrict__ wo,
+                                                          const float* __restrict__ bo, const float* __restrict__ g1,
+                                                          const float* __restrict__ be1, const float* __restrict__ g2,
+                                                          const float* __restrict__ be2, TX* __restrict__ y,
+                                                          float* __restrict__ resid_out, int B, int S, float c2,
+                                                          float eps) {
+  using L = SmallLds<D, HD>;
+  constexpr int KD = L::KD;     // k-steps over d_model
+  constexpr int NH = D / HD;    // heads
+  constexpr int NDT = L::NDT;   // 32-row d-tiles per head
+  constexpr int KSH = L::KSH;   // k-steps per head in Q K^T
+  constexpr int NNT = D / 32;   // 32-column output tiles
+  constexpr int MAXT = L::MAXT;
+
+  // [W_qkv chunks | W_o chunks | K^T of head j | V of head j], all operand-ready.
+  __shared__ f16x8 lds[L::TOTAL];
+  f16x8* const Wl = lds;
+  f16x8* const Wol = Wl + L::WQKV;
+  f16x8* const Kl = Wol + L::WO;
+  f16x8* const Vl = Kl + L::KCH;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, provably uniform
+  const int nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
+  const int li = lane & 31, g = lane >> 5;
+  const int nkt = (S + 31) >> 5;
+  const int tok = w * 32 + li;
+  const bool tok_ok = tok < S;
+
+  // ---- stage the weights, one 64-chunk row (one k-step of one 32-row tile) per
+  // wave at a time, so every branch below is wave-uniform:
+  // W_qkv row (rt, kk): lane -> W[32rt + lane%32][16kk + 8(lane/32) .. +8]
+  // W_o row (nt, ks):   lane -> W_o[32nt + lane%32][16ks + 4(lane/32) + {0..3, 8..11}]
+  {
+    constexpr int ROWS_QKV = L::WQKV / 64, ROWS = (L::WQKV + L::WO) / 64;
+    constexpr int BATCH = (ROWS + 3) / 4;  // every row in flight at once with 4 waves
+    const f16* wq_lane = wqkv + (int64_t)(lane & 31) * D + 8 * (lane >> 5);
+    const f16* wo_lane = wo + (int64_t)(lane & 31) * D + 4 * (lane >> 5);
+    for (int r0 = w; r0 < ROWS; r0 += BATCH * nw) {
+      f16x8 tmp[BATCH];
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int r = r0 + u * nw;
+        if (r < ROWS_QKV) {
+          tmp[u] = *reinterpret_cast<const f16x8*>(wq_lane + (int64_t)(32 * (r / KD)) * D + 16 * (r % KD));
+        } else if (r < ROWS) {
+          const int ro = r - ROWS_QKV;
+          const f16* p = wo_lane + (int64_t)(32 * (ro / KD)) * D + 16 * (ro % KD);
+          const f16x4 lo = *reinterpret_cast<const f16x4*>(p);
+          const f16x4 hi = *reinterpret_cast<const f16x4*>(p + 8);
+          tmp[u] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int r = r0 + u * nw;
+        if (r < ROWS) lds[r * 64 + lane] = tmp[u];
+      }
+    }
+  }
+  float* const Pf = reinterpret_cast<float*>(lds + L::CORE);
+  if constexpr (L::PARAMS) {
+    const float* src[6] = {bqkv, bo, g1, be1, g2, be2};
+    const int len[6] = {3 * D, D, D, D, D, D};
+    int off = 0;
+#pragma unroll
+    for (int v = 0; v < 6; ++v) {
+      for (int i = 4 * (int)threadIdx.x; i < len[v]; i += 4 * (int)blockDim.x)
+        *reinterpret_cast<f32x4*>(Pf + off + i) = *reinterpret_cast<const f32x4*>(src[v] + i);
+      off += len[v];
+    }
+  }
+  __syncthreads();
+
+  using Raw8 = typename XChunks<TX>::c8;
+  using Raw4 = typename XChunks<TX>::c4;
+  // LN1 input of the next sequence, loaded one sequence ahead.
+  Raw8 xpre[KD];
+  auto load_ln1_input = [&](int sq) {
+    const TX* xr = x + ((int64_t)sq * S + tok) * D + 8 * g;
+#pragma unroll
+    for (int kk = 0; kk < KD; ++kk) {
+      if (tok_ok && sq < B) {
+        xpre[kk] = *reinterpret_cast<const Raw8*>(xr + 16 * kk);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xpre[kk][e] = (TX)0.0f;
+      }
+    }
+  };
+  load_ln1_input(blockIdx.x);
+
+  for (int seq = blockIdx.x; seq < B; seq += gridDim.x) {
+    const int64_t row = (int64_t)seq * S + tok;
+    const TX* xrow = x + row * D;
+    const float *gamma1, *beta1, *gamma2, *beta2, *bias_o, *bias_qkv;
+    if constexpr (L::PARAMS) {
+      bias_qkv = Pf;
+      bias_o = Pf + 3 * D;
+      gamma1 = Pf + 4 * D;
+      beta1 = Pf + 5 * D;
+      gamma2 = Pf + 6 * D;
+      beta2 = Pf + 7 * D;
+    } else {
+      const int z = opaque_zero();
+      bias_qkv = bqkv + z;
+      bias_o = bo + z;
+      gamma1 = g1 + z;
+      beta1 = be1 + z;
+      gamma2 = g2 + z;
+      beta2 = be2 + z;
+    }
+
+    // ---- LN1: token `tok`, columns 16kk + 8g + e -------------------------------
+    f16x8 hB[KD];
+    {
+      float xv[KD][8];
+      float s = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xv[kk][e] = (float)xpre[kk][e];
+          s += xv[kk][e];
+        }
+      }
+      const float mean = (s + __shfl_xor(s, 32)) * (1.0f / D);
+      float q = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float t = xv[kk][e] - mean;
+          q += t * t;
+        }
+      const float rstd = rsqrtf((q + __shfl_xor(q, 32)) * (1.0f / D) + eps);
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) {
+        float gv[8], bv[8];
+        load8(gamma1 + 16 * kk + 8 * g, gv);
+        load8(beta1 + 16 * kk + 8 * g, bv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hB[kk][e] = (f16)((xv[kk][e] - mean) * rstd * gv[e] + bv[e]);
+      }
+    }
+
+    // Attention output of every head as fp16 B operands of out^T = W_o ctx^T:
+    // k-step ks of d_model covers head ks / KSH.
+    f16x8 cB[KD];
+
+#pragma unroll
+    for (int j = 0; j < NH; ++j) {
+      __builtin_amdgcn_sched_barrier(0);  // keep heads from interleaving (register pressure)
+      // ---- projections of this wave's 32 tokens for head j ----------------------
+      f16x8 qB[KSH];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        f32x16 qa = zero16(), ka = zero16(), va = zero16();
+        const int d0 = j * HD + dt * 32;
+        const f16x8* wq = Wl + (d0 / 32) * KD * 64 + lane;
+        const f16x8* wk = wq + (D / 32) * KD * 64;
+        const f16x8* wv = wk + (D / 32) * KD * 64;
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) {
+          const f16x8 aq = wq[kk * 64];
+          const f16x8 ak = wk[kk * 64];
+          const f16x8 bv = wv[kk * 64];
+          qa = mfma32x32x16(aq, hB[kk], qa);
+          ka = mfma32x32x16(ak, hB[kk], ka);
+          va = mfma32x32x16(hB[kk], bv, va);
+        }
+        float bq[16], bk[16], bvv[16];
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4 tq = *reinterpret_cast<const f32x4*>(bias_qkv + d0 + 8 * qd + 4 * g);
+          const f32x4 tk = *reinterpret_cast<const f32x4*>(bias_qkv + D + d0 + 8 * qd + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            bq[4 * qd + e] = tq[e];
+            bk[4 * qd + e] = tk[e];
+          }
+        }
+        const float bvl = bias_qkv[2 * D + d0 + li];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bvv[r] = bvl;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          qB[2 * dt + half] = half_to_f16(qa, half, bq);
+          Kl[(w * KSH + 2 * dt + half) * 64 + lane] = half_to_f16(ka, half, bk);
+          Vl[((w * NDT + dt) * 2 + half) * 64 + lane] = half_to_f16(va, half, bvv);
+        }
+      }
+      __syncthreads();
+
+      // ---- S^T = K Q^T over all key tiles, exact softmax --------------------------
+      f32x16 sacc[MAXT];
+      float mx = kNegInf;
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) {
+        if (t < nkt && (!CAUSAL || t <= w)) {
+          sacc[t] = zero16();
+#pragma unroll
+          for (int ks = 0; ks < KSH; ++ks) sacc[t] = mfma32x32x16(Kl[(t * KSH + ks) * 64 + lane], qB[ks], sacc[t]);
+          // Only the last key tile (keys >= S) and, causally, the diagonal tile need masks.
+          if (32 * t + 32 > S || (CAUSAL && t == w)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+              if (key >= S || (CAUSAL && key > tok)) sacc[t][r] = kNegInf;
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mc = mx * c2;
+      float l = 0.f;
+      f16x8 pB[MAXT][2];
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) {
+        if (t < nkt && (!CAUSAL || t <= w)) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -mc));
+            l += p;
+            pB[t][r >> 3][r & 7] = (f16)p;
+          }
+        }
+      }
+      l += __shfl_xor(l, 32);
+
+      // ---- O^T = V^T P^T, normalised into this head's ctx operands -------------
+      f32x16 ot[NDT];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) ot[dt] = zero16();
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) {
+        if (t < nkt && (!CAUSAL || t <= w)) {
+#pragma unroll
+          for (int half = 0; half < 2; ++half)
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+              ot[dt] = mfma32x32x16(Vl[((t * NDT + dt) * 2 + half) * 64 + lane], pB[t][half], ot[dt]);
+        }
+      }
+      const float inv = __builtin_amdgcn_rcpf(l);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) cB[j * KSH + 2 * dt + half] = scaled_f16(ot[dt], half, inv);
+      __syncthreads();  // K/V of head j are dead; the next head may overwrite them
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- prefetch: this sequence's residual, the next sequence's LN1 input -------
+    Raw4 xres[NNT][4];
+#pragma unroll
+    for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        if (tok_ok) {
+          xres[nt][qd] = *reinterpret_cast<const Raw4*>(xrow + 32 * nt + 8 * qd + 4 * g);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xres[nt][qd][e] = (TX)0.0f;
+        }
+      }
+    load_ln1_input(seq + gridDim.x);
+
+    // ---- out^T = W_o ctx^T over all heads -----------------------------------------
+    f32x16 oacc[NNT];  // lane (tok, g), reg r -> column 32nt + 8(r/4) + 4g + r%4
+#pragma unroll
+    for (int nt = 0; nt < NNT; ++nt) oacc[nt] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KD; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < NNT; ++nt) oacc[nt] = mfma32x32x16(Wol[(nt * KD + ks) * 64 + lane], cB[ks], oacc[nt]);
+
+    // ---- r = out + b_o + x;  y = LN2(r) ------------------------------------------
+    float v[NNT][4][4];
+    float s = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n0 = 32 * nt + 8 * qd + 4 * g;
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(bias_o + n0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[nt][qd][e] = oacc[nt][4 * qd + e] + bb[e] + (float)xres[nt][qd][e];
+          s += v[nt][qd][e];
+        }
+      }
+    const float mean = (s + __shfl_xor(s, 32)) * (1.0f / D);
+    float q = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float t = v[nt][qd][e] - mean;
+          q += t * t;
+        }
+    const float rstd = rsqrtf((q + __shfl_xor(q, 32)) * (1.0f / D) + eps);
+    if (tok_ok) {
+      TX* yrow = y + row * D;
+#pragma unroll
+      for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int n0 = 32 * nt + 8 * qd + 4 * g;
+          const f32x4 gg = *reinterpret_cast<const f32x4*>(gamma2 + n0);
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(beta2 + n0);
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = (v[nt][qd][e] - mean) * rstd * gg[e] + bb[e];
+          store4(yrow + n0, o);
+          if (resid_out) store4(resid_out + row * D + n0, v[nt][qd]);
+        }
+    }
+  }  // sequence loop
+}
+
+bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads) {
+  if (heads <= 0 || d_model % heads != 0) return false;
+  const int64_t hd = d_model / heads;
+  const bool shape = (d_model == 128 && (hd == 32 || hd == 64)) || (d_model == 64 && (hd == 32 || hd == 64)) ||
+                     (d_model == 96 && hd == 32);
+  return shape && seq_len >= 1 && seq_len <= kSmallMaxS;
+}
+
+// Persistent grid: one workgroup per CU (the staged weights fill most of the
+// LDS), each walking the batch with stride gridDim.x.
+static int compute_units() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+// Always four waves: the waves past the sequence's last 32-token tile still
+// share the weight staging (and compute masked tiles nobody reads).
+template <int D, int HD, bool CAUSAL, typename TX>
+static hipError_t launch_small(const SmallLayerArgs& a, float c2) {
+  const int64_t grid = a.batch < compute_units() ? a.batch : compute_units();
+  hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, TX>), dim3((unsigned)grid), dim3(256), 0, a.stream,
+                     static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
+                     static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
+                     static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps);
+  return hipGetLastError();
+}
+
+template <int D, int HD, bool CAUSAL>
+static hipError_t small_dtype(const SmallLayerArgs& a, float c2) {
+  return a.x_dtype == kF16 ? launch_small<D, HD, CAUSAL, f16>(a, c2) : launch_small<D, HD, CAUSAL, float>(a, c2);
+}
+
+template <bool CAUSAL>
+static hipError_t small_shape(const SmallLayerArgs& a, float c2) {
+  const int64_t hd = a.d_model / a.heads;
+  if (a.d_model == 128) {
+    if (hd == 32) return small_dtype<128, 32, CAUSAL>(a, c2);
+    return small_dtype<128, 64, CAUSAL>(a, c2);
+  }
+  if (a.d_model == 64) {
+    if (hd == 32) return small_dtype<64, 32, CAUSAL>(a, c2);
+    return small_dtype<64, 64, CAUSAL>(a, c2);
+  }
+  return small_dtype<96, 32, CAUSAL>(a, c2);
+}
+
+hipError_t run_layer_small(const SmallLayerArgs& a) {
+  if (!layer_small_ok(a.seq_len, a.d_model, a.heads) || (a.x_dtype != kF16 && a.x_dtype != kF32) ||
+      a.batch < 0 || a.batch > 0x7fffffff)
+    return hipErrorInvalidValue;
+  if (a.batch == 0) return hipSuccess;
+  const double hd = (double)(a.d_model / a.heads);
+  const float c2 = (float)(1.0 / sqrt(hd)) * 1.4426950408889634f;
+  return a.causal ? small_shape<true>(a, c2) : small_shape<false>(a, c2);
+}
+
+}  // namespace cobra

@@ -83,7 +83,22 @@ int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const v
 int cobra_attn_fwd(const void* qkv, void* ctx, int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim,
                    float scale, int causal, void* stream);
 
-/* Device workspace (bytes) cobra_layer_fwd needs for this shape. */
+/* Execution plans of cobra_layer_fwd. */
+enum {
+  COBRA_PLAN_FUSED = 0,  /* one kernel for the whole sublayer, no workspace */
+  COBRA_PLAN_STAGED = 1  /* LN1, QKV GEMM, attention, out-proj GEMM (+LN) through a workspace */
+};
+
+/*
+ * Which plan cobra_layer_fwd runs for this shape, or -1 if the shape is not
+ * supported.  FUSED covers seq_len <= 128 with d_model 128 (head_dim 32 or
+ * 64), 64 (32, 64) or 96 (32).  Host-only: no device work.  The reference's
+ * counterpart is the gate set of UserOptimizedTransformer._prepare
+ * (TTB:1030-1071).
+ */
+int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads);
+
+/* Device workspace (bytes) cobra_layer_fwd needs for this shape (0 for FUSED). */
 int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads);
 
 /*
@@ -93,7 +108,8 @@ int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_mo
  * x, y: [batch*seq_len, d_model] in x_dtype; w_qkv: [3*d_model, d_model] fp16
  * (rows: q_proj, k_proj, v_proj weights, in that order); b_qkv: [3*d_model]
  * fp32; w_o: [d_model, d_model] fp16; b_o and the LayerNorm parameters fp32.
- * resid_out (optional): r in fp32.  workspace: cobra_layer_workspace_bytes().
+ * resid_out (optional): r in fp32.  workspace: cobra_layer_workspace_bytes()
+ * bytes (may be NULL when that is 0).  One launch for the FUSED plan.
  * Replaces the attention half of UserOptimizedTransformer._run_fused
  * (TTB:1216-1268), which is what its CUDA graph replays (TTB:1331-1360).
  */

@@ -17,14 +17,14 @@ def log(msg: str) -> None:
     sys.stdout.flush()
 
 
-def build_pair(d_model: int, heads: int, seed: int = 0, dtype: torch.dtype = torch.float16):
+def build_pair(d_model: int, heads: int, seed: int = 0, dtype: torch.dtype = torch.float16, graph=None):
     """(fp32 oracle on dtype-rounded weights, HIP module in dtype on the GPU)."""
     from cobra_amd import CobraAttentionSublayer
 
     ref = make_sublayer(d_model, heads, seed=seed)
     if dtype == torch.float16:
         quantize_like(ref, torch.float16)
-    mod = CobraAttentionSublayer(d_model, heads)
+    mod = CobraAttentionSublayer(d_model, heads, graph=graph)
     mod.load_state_dict(ref.state_dict(), strict=True)
     mod = mod.to(device=DEV, dtype=dtype).eval()
     return ref, mod
@@ -51,6 +51,7 @@ def check_case(case: LayerCase, seed: int = 0, input_seed: int = 0, oracle_devic
         y = mod(x.to(DEV), causal=case.causal)
         torch.cuda.synchronize()
     y = y.float().cpu()
+    log(f"[case] {case.name}: plan={'fused' if mod.plan == 0 else 'staged'}")
     rows = list(range(case.batch)) if subset is None else subset
     want = oracle_on(ref, x[rows].float(), case.causal, oracle_device)
     res = compare_outputs(want, y[rows])

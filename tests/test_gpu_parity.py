@@ -66,6 +66,10 @@ def test_b10000_sampled_sequences():
         (2, 200, 32, 4, True),      # D 32, hd 8 (case 7 geometry)
         (5, 65, 128, 2, False),     # hd 64, ragged S
         (1, 40, 512, 2, True),      # hd 256
+        (3, 100, 128, 1, False),    # staged, hd 128, ragged S
+        (2, 128, 64, 2, True),      # fused, D 64, hd 32
+        (7, 1, 128, 4, True),       # fused, S = 1 causal
+        (2, 96, 64, 1, False),      # fused, D 64, hd 64
     ],
 )
 def test_odd_shapes(B, S, D, H, causal):
@@ -120,18 +124,57 @@ def test_bit_repeatable():
     assert torch.equal(a, b) and torch.equal(a, c)
 
 
-def test_graph_replays_match_eager():
-    """Replays with fresh inputs, eager work in between, each against eager."""
-    _, mod = build_pair(128, 4)
-    xs = [make_input(16, 128, 128, seed=s).half().to(DEV) for s in range(4)]
+@pytest.mark.parametrize("D,H", [(128, 4), (128, 16)])
+def test_graph_replays_match_eager(D, H):
+    """hipGraph replays with fresh inputs, eager work in between, each equal to
+    the eager result (fused plan at H4, staged plan at H16)."""
+    _, mod = build_pair(D, H, graph=True)
+    xs = [make_input(16, 128, D, seed=s).half().to(DEV) for s in range(4)]
     with torch.inference_mode():
-        outs = [mod(x).clone() for x in xs]  # first call captures, later ones replay
+        outs = []
+        for x in xs:  # first call captures, later ones replay
+            outs.append(mod(x).clone())
+            torch.cuda.synchronize()
+            (x.float() * 2).sum().item()  # unrelated eager work between replays
         assert mod._graph is not None
         mod._graph_ok = False
         eager = [mod(x).clone() for x in xs]
         torch.cuda.synchronize()
     for o, e in zip(outs, eager):
         assert torch.equal(o, e)
+
+
+def test_base_config_runs_fused_single_kernel():
+    from cobra_amd import ops
+
+    _, mod = build_pair(128, 4)
+    with torch.inference_mode():
+        mod(make_input(2, 128, 128).half().to(DEV))
+    assert mod.plan == ops.PLAN_FUSED and mod._ws.numel() == 0 and not mod._graph_ok
+
+
+@pytest.mark.parametrize("H,causal", [(4, False), (4, True), (2, False), (1, True)])
+def test_staged_pipeline_at_fused_shapes(H, causal):
+    """The staged kernels (LN, QKV GEMM, attention, GEMM+LN), composed through
+    the op wrappers exactly as cobra_layer_fwd's staged plan does, at a shape
+    the library would otherwise run fused."""
+    from cobra_amd import ops
+
+    ref, mod = build_pair(128, H)
+    B, S, D = 16, 128, 128
+    x = make_input(B, S, D, seed=11).half()
+    xd = x.to(DEV).view(B * S, D)
+    with torch.inference_mode():
+        p = mod._packed()
+        _, h = ops.add_ln(xd, None, None, p.ln1_w, p.ln1_b, True, 1e-5, False)
+        qkv = ops.linear(h, p.w_qkv, p.b_qkv)
+        ctx = ops.attn(qkv, B, S, H, D // H, (D // H) ** -0.5, causal=causal)
+        _, y = ops.linear_ln(ctx, p.w_o, p.b_o, xd, p.ln2_w, p.ln2_b)
+        torch.cuda.synchronize()
+    want = oracle_on(ref, x.float(), causal, "cpu")
+    res = compare_outputs(want, y.view(B, S, D).float().cpu())
+    log(f"[staged H{H} causal={causal}] max_abs={res.max_abs_error:.3e} failed={res.failed_elements}")
+    assert res.passed, res
 
 
 def test_weight_update_repacks():

@@ -41,16 +41,34 @@ def test_argument_validation_rejects_before_any_launch():
     assert bad != 0
     assert lib.cobra_attn_fwd(16, 16, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
     assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10) == -1      # head_dim 12
-    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 4) > 0
+    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16) > 0     # staged plan (head_dim 8)
+    assert lib.cobra_layer_plan(2, 16, 128, 4) == _lib.PLAN_FUSED
 
 
 def test_workspace_size_formula():
     from cobra_amd import ops
 
-    # h fp16 [T, D] + qkv fp16 [T, 3D] (+ fp32 residual for D > 128), 256-B aligned
-    assert ops.layer_workspace_bytes(64, 128, 128, 4) == 8192 * 128 * 2 + 8192 * 384 * 2
+    # fused plan: no workspace
+    assert ops.layer_workspace_bytes(64, 128, 128, 4) == 0
+    # staged: h fp16 [T, D] + qkv fp16 [T, 3D] (+ fp32 residual for D > 128), 256-B aligned
+    assert ops.layer_workspace_bytes(64, 128, 128, 16) == 8192 * 128 * 2 + 8192 * 384 * 2
     t, d = 32 * 100000, 1024
     assert ops.layer_workspace_bytes(32, 100000, 1024, 16) == t * d * 2 + t * 3 * d * 2 + t * d * 4
+
+
+def test_plan_selection_per_config():
+    """One fused kernel for S <= 128 at d_model 128 with head_dim 32 or 64; staged otherwise."""
+    from cobra_amd import ops
+    from oracle import CONFIGS
+
+    fused = {"plumbing", "base", "b1", "b4", "b16", "b128", "b10000", "s32", "h2"}
+    for name, c in CONFIGS.items():
+        want = ops.PLAN_FUSED if name in fused else ops.PLAN_STAGED
+        assert ops.layer_plan(c.batch, c.seq_len, c.d_model, c.heads) == want, name
+    assert ops.layer_plan(2, 129, 128, 4) == ops.PLAN_STAGED
+    assert ops.layer_plan(2, 17, 96, 3) == ops.PLAN_FUSED
+    with pytest.raises(ValueError):
+        ops.layer_plan(2, 16, 120, 10)
 
 
 def test_state_dict_identical_to_reference_sublayer():
