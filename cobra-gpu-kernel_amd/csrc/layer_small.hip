@@ -84,6 +84,7 @@ __device__ __forceinline__ f16x8 half_to_f16(const f32x16& acc, int half, const 
 }  // namespace
 
 constexpr int kSmallMaxS = 128;
+constexpr int kSmallWaves = kSmallMaxS / 32;  // one wave per 32-token tile; always launched in full
 constexpr int kLdsBytes = 163840;  // gfx950: LDS per workgroup
 
 // LDS plan of the fused kernel, in 16-byte chunks.
@@ -121,7 +122,7 @@ struct XChunks<float> {
 };
 
 template <int D, int HD, bool CAUSAL, typename TX>
-__global__ __launch_bounds__(256) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
+__global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
                                                           const float* __restrict__ bqkv, const f16* __restrict__ wo,
                                                           const float* __restrict__ bo, const float* __restrict__ g1,
                                                           const float* __restrict__ be1, const float* __restrict__ g2,
@@ -145,42 +146,42 @@ __global__ __launch_bounds__(256) void layer_small_kernel(const TX* __restrict__
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, provably uniform
-  const int nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
   const int li = lane & 31, g = lane >> 5;
-  const int nkt = (S + 31) >> 5;
   const int tok = w * 32 + li;
   const bool tok_ok = tok < S;
 
-  // ---- stage the weights, one 64-chunk row (one k-step of one 32-row tile) per
-  // wave at a time, so every branch below is wave-uniform:
+  // ---- stage the weights: 64-chunk row r (one k-step of one 32-row tile) goes
+  // to wave r % 4, so every trip count below is a compile-time constant:
   // W_qkv row (rt, kk): lane -> W[32rt + lane%32][16kk + 8(lane/32) .. +8]
   // W_o row (nt, ks):   lane -> W_o[32nt + lane%32][16ks + 4(lane/32) + {0..3, 8..11}]
   {
-    constexpr int ROWS_QKV = L::WQKV / 64, ROWS = (L::WQKV + L::WO) / 64;
-    constexpr int BATCH = (ROWS + 3) / 4;  // every row in flight at once with 4 waves
+    constexpr int ROWS_Q = L::WQKV / 64, ROWS_O = L::WO / 64;
+    constexpr int RQ = (ROWS_Q + kSmallWaves - 1) / kSmallWaves, RO = (ROWS_O + kSmallWaves - 1) / kSmallWaves;
     const f16* wq_lane = wqkv + (int64_t)(lane & 31) * D + 8 * (lane >> 5);
     const f16* wo_lane = wo + (int64_t)(lane & 31) * D + 4 * (lane >> 5);
-    for (int r0 = w; r0 < ROWS; r0 += BATCH * nw) {
-      f16x8 tmp[BATCH];
+    f16x8 tq[RQ], to[RO];
 #pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int r = r0 + u * nw;
-        if (r < ROWS_QKV) {
-          tmp[u] = *reinterpret_cast<const f16x8*>(wq_lane + (int64_t)(32 * (r / KD)) * D + 16 * (r % KD));
-        } else if (r < ROWS) {
-          const int ro = r - ROWS_QKV;
-          const f16* p = wo_lane + (int64_t)(32 * (ro / KD)) * D + 16 * (ro % KD);
-          const f16x4 lo = *reinterpret_cast<const f16x4*>(p);
-          const f16x4 hi = *reinterpret_cast<const f16x4*>(p + 8);
-          tmp[u] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-      }
+    for (int u = 0; u < RQ; ++u) {
+      const int r = w + kSmallWaves * u;
+      if (ROWS_Q % kSmallWaves == 0 || r < ROWS_Q)
+        tq[u] = *reinterpret_cast<const f16x8*>(wq_lane + (int64_t)(32 * (r / KD)) * D + 16 * (r % KD));
+    }
 #pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int r = r0 + u * nw;
-        if (r < ROWS) lds[r * 64 + lane] = tmp[u];
+    for (int u = 0; u < RO; ++u) {
+      const int r = w + kSmallWaves * u;
+      if (ROWS_O % kSmallWaves == 0 || r < ROWS_O) {
+        const f16* p = wo_lane + (int64_t)(32 * (r / KD)) * D + 16 * (r % KD);
+        const f16x4 lo = *reinterpret_cast<const f16x4*>(p);
+        const f16x4 hi = *reinterpret_cast<const f16x4*>(p + 8);
+        to[u] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
     }
+#pragma unroll
+    for (int u = 0; u < RQ; ++u)
+      if (ROWS_Q % kSmallWaves == 0 || w + kSmallWaves * u < ROWS_Q) Wl[(w + kSmallWaves * u) * 64 + lane] = tq[u];
+#pragma unroll
+    for (int u = 0; u < RO; ++u)
+      if (ROWS_O % kSmallWaves == 0 || w + kSmallWaves * u < ROWS_O) Wol[(w + kSmallWaves * u) * 64 + lane] = to[u];
   }
   float* const Pf = reinterpret_cast<float*>(lds + L::CORE);
   if constexpr (L::PARAMS) {
@@ -189,7 +190,7 @@ __global__ __launch_bounds__(256) void layer_small_kernel(const TX* __restrict__
     int off = 0;
 #pragma unroll
     for (int v = 0; v < 6; ++v) {
-      for (int i = 4 * (int)threadIdx.x; i < len[v]; i += 4 * (int)blockDim.x)
+      for (int i = 4 * (int)threadIdx.x; i < len[v]; i += 4 * 64 * kSmallWaves)
         *reinterpret_cast<f32x4*>(Pf + off + i) = *reinterpret_cast<const f32x4*>(src[v] + i);
       off += len[v];
     }
@@ -316,58 +317,71 @@ __global__ __launch_bounds__(256) void layer_small_kernel(const TX* __restrict__
       }
       __syncthreads();
 
-      // ---- S^T = K Q^T over all key tiles, exact softmax --------------------------
-      f32x16 sacc[MAXT];
-      float mx = kNegInf;
-#pragma unroll
-      for (int t = 0; t < MAXT; ++t) {
-        if (t < nkt && (!CAUSAL || t <= w)) {
-          sacc[t] = zero16();
-#pragma unroll
-          for (int ks = 0; ks < KSH; ++ks) sacc[t] = mfma32x32x16(Kl[(t * KSH + ks) * 64 + lane], qB[ks], sacc[t]);
-          // Only the last key tile (keys >= S) and, causally, the diagonal tile need masks.
-          if (32 * t + 32 > S || (CAUSAL && t == w)) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-              if (key >= S || (CAUSAL && key > tok)) sacc[t][r] = kNegInf;
-            }
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-        }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mc = mx * c2;
-      float l = 0.f;
-      f16x8 pB[MAXT][2];
-#pragma unroll
-      for (int t = 0; t < MAXT; ++t) {
-        if (t < nkt && (!CAUSAL || t <= w)) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -mc));
-            l += p;
-            pB[t][r >> 3][r & 7] = (f16)p;
-          }
-        }
-      }
-      l += __shfl_xor(l, 32);
-
-      // ---- O^T = V^T P^T, normalised into this head's ctx operands -------------
+      // ---- S^T = K Q^T, softmax and O^T = V^T P^T over two blocks of two key
+      // tiles (64 keys): the running max / sum rescale happens once, between the
+      // blocks, and only half of the scores are live at a time.
       f32x16 ot[NDT];
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) ot[dt] = zero16();
+      float m_run = 0.f, l = 0.f;
+      // Every key tile is computed, branch-free: all four waves always write their
+      // K/V slots (finite values, also past S), and masked keys get p = 0.  The
+      // wasted tiles cost no latency -- the slowest wave bounds every barrier.
 #pragma unroll
-      for (int t = 0; t < MAXT; ++t) {
-        if (t < nkt && (!CAUSAL || t <= w)) {
+      for (int blk = 0; blk < MAXT / 2; ++blk) {
+        f32x16 sacc[2];
+        float mx = kNegInf;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int t = 2 * blk + u;
+          sacc[u] = zero16();
+#pragma unroll
+          for (int ks = 0; ks < KSH; ++ks) sacc[u] = mfma32x32x16(Kl[(t * KSH + ks) * 64 + lane], qB[ks], sacc[u]);
+          // Keys past S (last tile) and keys after the query (diagonal and later
+          // tiles).  The bound is made opaque per head so that the 16 per-register
+          // lane masks are formed here rather than hoisted (and spilled) across loops.
+          if (32 * t + 32 > S || (CAUSAL && t >= w)) {
+            int lim = S - 32 * t - 4 * g + opaque_zero();  // valid: offset < lim
+            if (CAUSAL) lim = min(lim, tok - 32 * t - 4 * g + 1);
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (8 * (r >> 2) + (r & 3) >= lim) sacc[u][r] = kNegInf;
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);  // block 0 always holds key 0
+        const float alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        f16x8 pB[2][2];
+        float ps = 0.f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[u][r], c2, -m_new));
+            ps += pv;
+            pB[u][r >> 3][r & 7] = (f16)pv;
+          }
+        if (blk == 0) {
+          l = ps;
+        } else {
+          l = l * alpha + ps;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ot[dt][r] *= alpha;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int half = 0; half < 2; ++half)
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
-              ot[dt] = mfma32x32x16(Vl[((t * NDT + dt) * 2 + half) * 64 + lane], pB[t][half], ot[dt]);
-        }
+              ot[dt] = mfma32x32x16(Vl[(((2 * blk + u) * NDT + dt) * 2 + half) * 64 + lane], pB[u][half], ot[dt]);
       }
+      l += __shfl_xor(l, 32);
       const float inv = __builtin_amdgcn_rcpf(l);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
@@ -475,7 +489,7 @@ static int compute_units() {
 template <int D, int HD, bool CAUSAL, typename TX>
 static hipError_t launch_small(const SmallLayerArgs& a, float c2) {
   const int64_t grid = a.batch < compute_units() ? a.batch : compute_units();
-  hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, TX>), dim3((unsigned)grid), dim3(256), 0, a.stream,
+  hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, TX>), dim3((unsigned)grid), dim3(64 * kSmallWaves), 0, a.stream,
                      static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
                      static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
                      static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps);
