@@ -96,6 +96,7 @@ class CobraAttentionSublayer(nn.Module):
         self.graph = graph
         self.plan: Optional[int] = None
         self._params = list(self.parameters())
+        self._versioned = [not p.is_inference() for p in self._params]
         self._pack: Optional[_Pack] = None
         self._sig = None
         self._ws: Optional[torch.Tensor] = None
@@ -111,13 +112,16 @@ class CobraAttentionSublayer(nn.Module):
         # .to() / .half() / .cuda() replace parameter storage: drop every cache.
         out = super()._apply(fn, *args, **kwargs)
         self._params = list(self.parameters())
+        self._versioned = [not p.is_inference() for p in self._params]
         self._pack = None
         self._sig = None
         return out
 
     def _packed(self) -> _Pack:
         # In-place updates (load_state_dict, optimiser-style edits) bump _version.
-        versions = tuple([p._version for p in self._params])
+        # Inference tensors (made under torch.inference_mode) keep no version
+        # counter; for those only a storage change is detected.
+        versions = tuple([p._version if v else p.data_ptr() for p, v in zip(self._params, self._versioned)])
         if self._pack is None or self._pack.versions != versions:
             if not self.norm1.weight.is_cuda:
                 raise RuntimeError("CobraAttentionSublayer runs on the GPU only: move it with .to('cuda')")

@@ -177,6 +177,19 @@ def test_staged_pipeline_at_fused_shapes(H, causal):
     assert res.passed, res
 
 
+def test_module_built_under_inference_mode():
+    """Parameters created inside torch.inference_mode() have no version counter."""
+    from cobra_amd import CobraAttentionSublayer
+
+    with torch.inference_mode():
+        torch.manual_seed(0)
+        mod = CobraAttentionSublayer(128, 4).to(DEV, torch.float16).eval()
+        x = make_input(2, 128, 128).half().to(DEV)
+        y = mod(x)
+        torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+
+
 def test_weight_update_repacks():
     ref, mod = build_pair(128, 4)
     x = make_input(4, 128, 128, seed=1).half().to(DEV)
