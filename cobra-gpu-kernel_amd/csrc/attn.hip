@@ -17,14 +17,44 @@
 //   * the output is accumulated transposed as well, O^T += V^T . P^T.  The
 //     probabilities of a 16-key step already sit in the lane in the B-operand
 //     position (col = query); their key order is the C layout's row order
-//     {4g..4g+3, 8+4g..8+4g+3} (g = lane / 32), so the V^T operand is read from
-//     LDS in that same key order and the product is exact;
-//   * K tiles are stored [key][d] and V tiles transposed [d][key] in LDS, the
-//     next key block is prefetched into registers during the matrix work.
+//     {4g..4g+3, 8+4g..8+4g+3} (g = lane / 32).  V stays row-major in LDS and
+//     the V^T operand is read in exactly that key order with two
+//     ds_read_b64_tr_b16 (a 4x4 transpose within each 16-lane group);
+//   * K and V tiles are row-major in LDS, 16-byte chunks XOR-swizzled by row
+//     (no padding, conflict-free operand reads), double-buffered: the next key
+//     block is prefetched into registers during the matrix work and stored to
+//     the other buffer, one barrier per block;
+//   * lazy rescale: a query's running max only moves (rescaling O and the sum)
+//     when a block raises it by more than 2^8 -- the probabilities stay below
+//     256, well inside fp16 -- and the whole wave skips the rescale when no
+//     lane needs it.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace cobra {
+
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16* p) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  return __builtin_bit_cast(f16x4, r);
+}
+
+// Chunk swizzle of a [rows][HD] fp16 tile: 16-byte chunk c of row r lives at
+// chunk c ^ swz(r).  Any 16 consecutive rows reading one chunk column hit 16
+// distinct 4-bank groups.
+template <int HD>
+__device__ __forceinline__ int swz(int row) {
+  constexpr int kRowsPer256B = HD >= 128 ? 1 : 128 / HD;
+  constexpr int kMask = (HD / 8 < 16 ? HD / 8 : 16) - 1;
+  return (row / kRowsPer256B) & kMask;
+}
+
+constexpr float kLazyRescale = 8.0f;  // log2 units
+
+}  // namespace
 
 template <int HD, int NW, int BN, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict__ qkv, f16* __restrict__ ctx,
@@ -32,17 +62,14 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   constexpr int BM = 32 * NW;          // queries per workgroup
   constexpr int KS = HD / 16;          // k-steps of the QK^T product
   constexpr int ND = (HD + 31) / 32;   // 32-row blocks of d in O^T
-  constexpr int HDV = ND * 32;         // rows of the V^T tile (zero beyond hd)
-  constexpr int LDK = HD + 8;          // K tile row stride (halves)
-  constexpr int LDV = BN + 4;          // V^T tile row stride (halves)
   constexpr int NT = NW * 64;
   constexpr int CPR = HD / 8;          // 16-byte chunks per key row
   constexpr int CH = BN * CPR;         // chunks per tile
   constexpr int IT = (CH + NT - 1) / NT;
   static_assert(HD % 16 == 0 && BN % 32 == 0, "tile geometry");
 
-  __shared__ __attribute__((aligned(16))) f16 Ks[BN * LDK];
-  __shared__ __attribute__((aligned(16))) f16 Vt[HDV * LDV];
+  __shared__ __attribute__((aligned(16))) f16 Ks[2][BN * HD];
+  __shared__ __attribute__((aligned(16))) f16 Vs[2][BN * HD];
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = id % nqb;
@@ -56,9 +83,11 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   const f16* vbase = qbase + 2 * D;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, li = lane & 31;
-  const int qi = qb * BM + w * 32 + li;  // this lane's query
+  const int q0w = qb * BM + w * 32;  // this wave's first query
+  const int qi = q0w + li;           // this lane's query
 
   // Q^T fragments: B operand of S^T = K . Q^T (k = d).
   f16x8 qf[KS];
@@ -68,11 +97,6 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     qf[kk] = (qi < S && d0 < hd) ? *reinterpret_cast<const f16x8*>(qbase + qi * ld + d0) : zero8();
   }
 
-  // Rows [HD, HDV) of V^T are never loaded; they must read as zero.
-  if constexpr (HDV > HD) {
-    for (int i = tid; i < (HDV - HD) * LDV; i += NT) Vt[HD * LDV + i] = (f16)0.0f;
-  }
-
   f16x8 rk[IT], rv[IT];
   auto gload = [&](int kb) {
 #pragma unroll
@@ -80,21 +104,20 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
       const int c = tid + i * NT;
       const int key = kb + c / CPR;
       const int d0 = (c % CPR) * 8;
-      const bool ok = c < CH && key < S && d0 < hd;
+      const bool ok = (CH % NT == 0 || c < CH) && key < S && d0 < hd;
       rk[i] = ok ? *reinterpret_cast<const f16x8*>(kbase + key * ld + d0) : zero8();
       rv[i] = ok ? *reinterpret_cast<const f16x8*>(vbase + key * ld + d0) : zero8();
     }
   };
-  auto sstore = [&]() {
+  auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = tid + i * NT;
       if (CH % NT == 0 || c < CH) {
-        const int key = c / CPR;
-        const int d0 = (c % CPR) * 8;
-        *reinterpret_cast<f16x8*>(Ks + key * LDK + d0) = rk[i];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[(d0 + e) * LDV + key] = rv[i][e];
+        const int row = c / CPR;
+        const int off = row * HD + (((c % CPR) ^ swz<HD>(row)) * 8);
+        *reinterpret_cast<f16x8*>(&Ks[buf][off]) = rk[i];
+        *reinterpret_cast<f16x8*>(&Vs[buf][off]) = rv[i];
       }
     }
   };
@@ -102,78 +125,100 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   f32x16 o[ND];
 #pragma unroll
   for (int j = 0; j < ND; ++j) o[j] = zero16();
-  float m_run = -1e30f;  // running max in the scaled (log2) domain
-  float l_run = 0.f;     // this lane's share of the running sum
+  float m_run = 0.f;  // running max in the scaled (log2) domain, set by block 0
+  float l_run = 0.f;  // this lane's share of the running sum
+
+  // Per-lane V^T read geometry (see the header): row within a 16-key step,
+  // column within a 32-wide d tile.
+  const int vr = 4 * g + ((lane & 15) >> 2);
+  const int vc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   const int kend = CAUSAL ? min(S, (qb + 1) * BM) : S;
+  const int nblk = (kend + BN - 1) / BN;
   gload(0);
-  sstore();
+  sstore(0);
   __syncthreads();
-  for (int kb = 0; kb < kend; kb += BN) {
-    const bool more = kb + BN < kend;
+  for (int n = 0; n < nblk; ++n) {
+    const int kb = n * BN;
+    const int cur = n & 1;
+    const bool more = n + 1 < nblk;
     if (more) gload(kb + BN);
+    const f16* Kc = Ks[cur];
+    const f16* Vc = Vs[cur];
 
     f32x16 s[BN / 32];
 #pragma unroll
     for (int t = 0; t < BN / 32; ++t) {
       s[t] = zero16();
+      const int row = t * 32 + li;
+      const f16* krow = Kc + row * HD;
+      const int sw = swz<HD>(row);
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(Ks + (t * 32 + li) * LDK + kk * 16 + g * 8);
+        const f16x8 a = *reinterpret_cast<const f16x8*>(krow + (((2 * kk + g) ^ sw) * 8));
         s[t] = mfma32x32x16(a, qf[kk], s[t]);
       }
     }
 
-    // Mask, block max over this lane's keys, then across the lane pair.
-    float mx = kNegInf;
-    const bool edge = (kb + BN > S) || (CAUSAL && kb + BN > qb * BM + w * 32);
+    // Masks only where a block reaches past S or, causally, past this wave's first query.
+    if (kb + BN > S || (CAUSAL && kb + BN > q0w + 1)) {
 #pragma unroll
-    for (int t = 0; t < BN / 32; ++t)
+      for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (edge) {
+        for (int r = 0; r < 16; ++r) {
           const int key = kb + t * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
           if (key >= S || (CAUSAL && key > qi)) s[t][r] = kNegInf;
         }
-        mx = fmaxf(mx, s[t][r]);
-      }
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx * c2);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    const float mc = mx * c2;
+    if (n == 0) {
+      m_run = mc;  // block 0 holds key 0, valid for every query: finite
+    } else if (__builtin_amdgcn_ballot_w64(mc > m_run + kLazyRescale)) {
+      const float m_new = fmaxf(m_run, mc);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int j = 0; j < ND; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+      m_run = m_new;
+    }
 
     f16x8 pf[BN / 16];
-    float psum = 0.f;
 #pragma unroll
     for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_new));
-        psum += p;
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_run));
+        l_run += p;
         pf[t * 2 + (r >> 3)][r & 7] = (f16)p;
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int j = 0; j < ND; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
 
 #pragma unroll
     for (int ks = 0; ks < BN / 16; ++ks)
 #pragma unroll
       for (int j = 0; j < ND; ++j) {
-        const f16* vp = Vt + (j * 32 + li) * LDV + ks * 16 + 4 * g;
-        const f16x4 lo = *reinterpret_cast<const f16x4*>(vp);
-        const f16x4 hi = *reinterpret_cast<const f16x4*>(vp + 8);
+        f16x4 lo, hi;
+        if (HD >= 32 || vc < HD) {
+          const int c = j * 32 + vc;
+          const int r0 = ks * 16 + vr, r1 = r0 + 8;
+          lo = lds_read_tr16(Vc + r0 * HD + (((c >> 3) ^ swz<HD>(r0)) * 8) + (c & 7));
+          hi = lds_read_tr16(Vc + r1 * HD + (((c >> 3) ^ swz<HD>(r1)) * 8) + (c & 7));
+        } else {
+          lo = hi = f16x4{(f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f};  // d beyond a 16-wide head
+        }
         const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[j] = mfma32x32x16(a, pf[ks], o[j]);
       }
 
+    if (more) sstore(cur ^ 1);
     __syncthreads();
-    if (more) {
-      sstore();
-      __syncthreads();
-    }
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
