@@ -37,11 +37,13 @@ DEVICE_FLAGS = [
 ]
 
 
-# Per-file backend options.  The fused sublayer kernel keeps MFMA results in
-# VGPRs (its accumulators feed VALU softmax / LayerNorm work directly); the
-# default AGPR form costs ~900 extra accumulator copy instructions there.
+# Per-file backend options.  The attention kernels keep MFMA results in VGPRs:
+# their accumulators feed VALU softmax / rescale / LayerNorm work directly, and
+# the default AGPR form adds an accumulator copy per use (~900 instructions in
+# the fused sublayer kernel, ~160 per key block in flash attention).
 FILE_FLAGS = {
     "layer_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -24,10 +24,16 @@
 //     (no padding, conflict-free operand reads), double-buffered: the next key
 //     block is prefetched into registers during the matrix work and stored to
 //     the other buffer, one barrier per block;
+//   * the Q fragments are pre-scaled by scale * log2(e) and each score tile's
+//     accumulator starts at -m (the query's running max), so the matrix cores
+//     deliver s - m in the exp2 domain and p = exp2 of the accumulator;
 //   * lazy rescale: a query's running max only moves (rescaling O and the sum)
 //     when a block raises it by more than 2^8 -- the probabilities stay below
 //     256, well inside fp16 -- and the whole wave skips the rescale when no
-//     lane needs it.
+//     lane needs it;
+//   * the running sum adds the fp16 probabilities the P.V product consumes
+//     (v_dot2_f32_f16 against ones, fp32 accumulation), and the max/sum
+//     exchange with lane ^ 32 uses v_permlane32_swap.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -43,16 +49,43 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const f16* p) {
 }
 
 // Chunk swizzle of a [rows][HD] fp16 tile: 16-byte chunk c of row r lives at
-// chunk c ^ swz(r).  Any 16 consecutive rows reading one chunk column hit 16
-// distinct 4-bank groups.
+// chunk c ^ swz(r).  Chosen so that both LDS read patterns are conflict-free:
+// the K operand (16 consecutive rows, one chunk each) and the V^T transpose
+// read (4 consecutive rows x 4 consecutive chunks per 32 lanes).
 template <int HD>
 __device__ __forceinline__ int swz(int row) {
-  constexpr int kRowsPer256B = HD >= 128 ? 1 : 128 / HD;
-  constexpr int kMask = (HD / 8 < 16 ? HD / 8 : 16) - 1;
-  return (row / kRowsPer256B) & kMask;
+  if constexpr (HD == 16) {
+    return (row >> 3) & 1;  // 8 rows per 256 bytes
+  } else if constexpr (HD == 32) {
+    return (row >> 2) & 3;  // 4 rows per 256 bytes
+  } else if constexpr (HD == 64) {
+    const int p = (row >> 1) & 7;     // row pair (2 rows per 256 bytes)
+    return ((p & 1) << 2) | (p >> 1);  // consecutive pairs differ in the 4-chunk group
+  } else {
+    const int r = row & 15;            // >= 256-byte rows
+    return ((r & 3) << 2) | (r >> 2);  // 4 consecutive rows in 4 distinct 4-chunk groups
+  }
 }
 
 constexpr float kLazyRescale = 8.0f;  // log2 units
+
+// max(v, v of lane ^ 32): v_permlane32_swap exchanges the two 32-lane halves
+// on the vector ALU (no LDS round trip, unlike a bpermute shuffle).
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ f32x16 splat16(float v) {
+  f32x16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = v;
+  return r;
+}
 
 }  // namespace
 
@@ -89,24 +122,51 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   const int q0w = qb * BM + w * 32;  // this wave's first query
   const int qi = q0w + li;           // this lane's query
 
-  // Q^T fragments: B operand of S^T = K . Q^T (k = d).
+  // Q^T fragments: B operand of S^T = K . Q^T (k = d), pre-scaled by
+  // scale * log2(e) so that the products come out in the exp2 domain.
   f16x8 qf[KS];
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
     const int d0 = kk * 16 + g * 8;
-    qf[kk] = (qi < S && d0 < hd) ? *reinterpret_cast<const f16x8*>(qbase + qi * ld + d0) : zero8();
+    if (qi < S && d0 < hd) {
+      const f16x8 q = *reinterpret_cast<const f16x8*>(qbase + qi * ld + d0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[kk][e] = (f16)((float)q[e] * c2);
+    } else {
+      qf[kk] = zero8();
+    }
   }
 
+  // K/V tile loads: a wave-uniform block base plus a fixed per-thread offset;
+  // only a block reaching past S needs the per-row predicate.  (256-wide heads
+  // keep the single predicated path: their registers are full, and a second
+  // copy of the loads costs them accumulator moves.)
+  unsigned voff[IT];
+  bool vok[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = tid + i * NT;
+    vok[i] = (CH % NT == 0 || c < CH) && (c % CPR) * 8 < hd;
+    voff[i] = vok[i] ? (unsigned)((c / CPR) * ld + (c % CPR) * 8) : 0u;
+  }
   f16x8 rk[IT], rv[IT];
   auto gload = [&](int kb) {
+    const f16* kblk = kbase + (int64_t)kb * ld;
+    const f16* vblk = vbase + (int64_t)kb * ld;
+    if (HD <= 128 && kb + BN <= S) {
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-      const int c = tid + i * NT;
-      const int key = kb + c / CPR;
-      const int d0 = (c % CPR) * 8;
-      const bool ok = (CH % NT == 0 || c < CH) && key < S && d0 < hd;
-      rk[i] = ok ? *reinterpret_cast<const f16x8*>(kbase + key * ld + d0) : zero8();
-      rv[i] = ok ? *reinterpret_cast<const f16x8*>(vbase + key * ld + d0) : zero8();
+      for (int i = 0; i < IT; ++i) {
+        rk[i] = vok[i] ? *reinterpret_cast<const f16x8*>(kblk + voff[i]) : zero8();
+        rv[i] = vok[i] ? *reinterpret_cast<const f16x8*>(vblk + voff[i]) : zero8();
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < IT; ++i) {
+        const int c = tid + i * NT;
+        const bool ok = vok[i] && kb + c / CPR < S;
+        rk[i] = ok ? *reinterpret_cast<const f16x8*>(kblk + voff[i]) : zero8();
+        rv[i] = ok ? *reinterpret_cast<const f16x8*>(vblk + voff[i]) : zero8();
+      }
     }
   };
   auto sstore = [&](int buf) {
@@ -125,8 +185,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   f32x16 o[ND];
 #pragma unroll
   for (int j = 0; j < ND; ++j) o[j] = zero16();
-  float m_run = 0.f;  // running max in the scaled (log2) domain, set by block 0
+  float m_run = 0.f;  // running max in the exp2 domain, set by block 0
   float l_run = 0.f;  // this lane's share of the running sum
+  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
   // Per-lane V^T read geometry (see the header): row within a 16-key step,
   // column within a 32-wide d tile.
@@ -146,10 +207,12 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     const f16* Kc = Ks[cur];
     const f16* Vc = Vs[cur];
 
+    // s = scores in the exp2 domain minus the running max: the accumulator
+    // starts at -m_run (every register of a lane belongs to the lane's query).
     f32x16 s[BN / 32];
 #pragma unroll
     for (int t = 0; t < BN / 32; ++t) {
-      s[t] = zero16();
+      s[t] = splat16(-m_run);
       const int row = t * 32 + li;
       const f16* krow = Kc + row * HD;
       const int sw = swz<HD>(row);
@@ -175,29 +238,38 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mc = mx * c2;
-    if (n == 0) {
-      m_run = mc;  // block 0 holds key 0, valid for every query: finite
-    } else if (__builtin_amdgcn_ballot_w64(mc > m_run + kLazyRescale)) {
-      const float m_new = fmaxf(m_run, mc);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+    mx = max_xor32(mx);  // this block's max relative to m_run
+    // Block 0 sets the running max (it holds key 0, valid for every query, so
+    // mx is finite); later blocks raise it only past the lazy threshold.
+    if (n == 0 || __builtin_amdgcn_ballot_w64(mx > kLazyRescale)) {
+      const float inc = n == 0 ? mx : fmaxf(mx, 0.f);
+      if (n != 0) {
+        const float alpha = __builtin_amdgcn_exp2f(-inc);
+        l_run *= alpha;
 #pragma unroll
-      for (int j = 0; j < ND; ++j)
+        for (int j = 0; j < ND; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
-      m_run = m_new;
+          for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+      }
+#pragma unroll
+      for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[t][r] -= inc;
+      m_run += inc;
     }
 
     f16x8 pf[BN / 16];
 #pragma unroll
     for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[t][r], c2, -m_run));
-        l_run += p;
-        pf[t * 2 + (r >> 3)][r & 7] = (f16)p;
+      for (int r = 0; r < 16; ++r) pf[t * 2 + (r >> 3)][r & 7] = (f16)__builtin_amdgcn_exp2f(s[t][r]);
+    // Row sum of the fp16 probabilities (the values the P.V product uses), fp32 accumulation.
+#pragma unroll
+    for (int k = 0; k < BN / 16; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 pr = {pf[k][2 * e], pf[k][2 * e + 1]};
+        l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
       }
 
 #pragma unroll
@@ -221,7 +293,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     __syncthreads();
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = sum_xor32(l_run);
   const float inv = 1.0f / l_tot;
   if (qi < S) {
     f16* out = ctx + (b * S + qi) * (int64_t)D + h * hd;
@@ -254,12 +326,18 @@ static hipError_t launch_attn(const AttnArgs& a, float c2) {
 
 template <int HD, bool CAUSAL>
 static hipError_t dispatch_waves(const AttnArgs& a, float c2) {
-  // Fewer waves per workgroup for short sequences, except at wide heads, where
-  // the per-thread share of the K/V prefetch would no longer fit in registers.
+  // Waves per workgroup follow the sequence length: every K/V tile a
+  // workgroup stages is shared by all of its waves, so long sequences take 8
+  // (256 queries), short ones fewer so that no wave idles past S.  Wide heads
+  // keep 4: their per-thread share of the K/V prefetch and the O accumulator
+  // already fill the register file.
   constexpr int BN = HD >= 256 ? 32 : 64;
   if constexpr (HD <= 64) {
     if (a.seq_len <= 32) return launch_attn<HD, 1, BN, CAUSAL>(a, c2);
     if (a.seq_len <= 64) return launch_attn<HD, 2, BN, CAUSAL>(a, c2);
+  }
+  if constexpr (HD <= 128) {
+    if (a.seq_len > 128) return launch_attn<HD, 8, BN, CAUSAL>(a, c2);
   }
   return launch_attn<HD, 4, BN, CAUSAL>(a, c2);
 }
