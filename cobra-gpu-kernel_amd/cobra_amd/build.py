@@ -43,6 +43,7 @@ DEVICE_FLAGS = [
 # the fused sublayer kernel, ~160 per key block in flash attention).
 FILE_FLAGS = {
     "layer_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "layer_split.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 

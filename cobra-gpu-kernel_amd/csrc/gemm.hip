@@ -255,6 +255,7 @@ hipError_t run_gemm(const GemmArgs& a) {
   if (!a.c) return hipErrorInvalidValue;
   const bool c16 = a.c_dtype == kF16;
   if (!c16 && a.c_dtype != kF32) return hipErrorInvalidValue;
+  if (gemm_dma_ok(a)) return run_gemm_dma(a);
   if (!has_resid || a.resid_dtype == kF16) return c16 ? dispatch_plain<f16, f16>(a) : dispatch_plain<f16, float>(a);
   return c16 ? dispatch_plain<float, f16>(a) : dispatch_plain<float, float>(a);
 }

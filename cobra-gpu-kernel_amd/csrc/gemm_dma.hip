@@ -1,0 +1,269 @@
+// C[M,N] = A[M,K] . W[N,K]^T (+ bias[N]) (+ resid[M,N]) for the large
+// projections: fp16 operands, fp32 accumulate, C in fp16 or fp32.
+//
+// Same contract as the register-staged GEMM (replaces the reference's
+// _gemm_kernel / _tl_linear, torch_transformer_benchmark.py:283-381): each
+// output element is owned by exactly one workgroup, no split-K, no atomics.
+//
+// gfx950 mapping:
+//   * operand tiles move HBM/L2 -> LDS with global_load_lds_dwordx4 (no VGPR
+//     staging, no ds_write): one wave instruction fills one contiguous 1 KB
+//     band = 8 rows of a 64-wide k-tile.  The LDS tile is XOR-swizzled in
+//     16-byte chunks (chunk c of row r at c ^ ((r >> 1) & 7)); since the DMA
+//     destination of a lane is fixed (band base + 16 * lane), each lane instead
+//     fetches the global chunk that belongs in its slot;
+//   * ST stages of LDS, one barrier per k-tile: a wave waits for its own DMA
+//     of tile kt (vmcnt), the barrier makes every wave's DMA visible and
+//     retires the stage computed in the previous step, which then receives
+//     tile kt + ST - 1;
+//   * v_mfma_f32_32x32x16_f16 with the weight tile as the A operand, so the
+//     accumulator holds C^T: each lane owns one output row and 4 consecutive
+//     columns per register quad;
+//   * epilogue through LDS: the fp32 tile (+ bias) is staged, then written in
+//     whole-row, 16-byte-per-lane passes with the residual added on the way.
+#include "common.hpp"
+#include "kernels.hpp"
+#include "lds_dma.hpp"
+
+namespace cobra {
+
+namespace {
+
+template <int BM, int BN, int WM, int WN, int ST>
+struct DmaTile {
+  // (GM, the tile-order group height, is a kernel parameter of its own.)
+  static constexpr int BK = 64;
+  static constexpr int NW = WM * WN;
+  static constexpr int NT = NW * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;
+  static constexpr int ROWS = BM + BN;          // LDS rows per stage: A rows, then W rows
+  static constexpr int STAGE = ROWS * BK;       // halves per stage
+  static constexpr int BANDS = ROWS / 8;        // 1 KB bands per stage
+  static constexpr int LPT = BANDS / NW;        // DMA instructions per thread per k-tile
+  static constexpr int EPW = WN * 32;           // epilogue slice width: one 32-column block per wave column
+  static constexpr int LDC = EPW + 4;           // fp32 epilogue row stride (floats)
+  static constexpr int GEMM_LDS = ST * STAGE * 2;
+  static constexpr int EPI_LDS = BM * LDC * 4;
+  static constexpr int LDS = GEMM_LDS > EPI_LDS ? GEMM_LDS : EPI_LDS;
+  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+  static_assert(BANDS % NW == 0, "every wave issues the same number of DMA bands");
+  static_assert(BM % 16 == 0 && BN % 16 == 0, "swizzle period");
+  static_assert(LDS <= 163840, "LDS budget");
+};
+
+__device__ __forceinline__ int chunk_swz(int row) { return (row >> 1) & 7; }
+
+template <typename T>
+__device__ __forceinline__ float to_float(T v) {
+  return (float)v;
+}
+
+}  // namespace
+
+template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __restrict__ A, const f16* __restrict__ W,
+                                                              const float* __restrict__ bias,
+                                                              const TR* __restrict__ resid, TC* __restrict__ C,
+                                                              int64_t M, int N, int K) {
+  using T = DmaTile<BM, BN, WM, WN, ST>;
+  constexpr int BK = T::BK, NT = T::NT, NW = T::NW, LPT = T::LPT;
+  __shared__ __attribute__((aligned(1024))) char smem[T::LDS];
+  f16* lds = reinterpret_cast<f16*>(smem);
+
+  // Tile order: each XCD runs a contiguous range of tile ids; within it, ids
+  // walk GM row blocks x all column blocks, so the tiles resident on one XCD
+  // at a time share a few A row blocks and W column blocks in its L2.
+  const int nbn = (N + BN - 1) / BN;
+  const int nbm = (int)((M + BM - 1) / BM);
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int group = tile / (GM * nbn);
+  const int first_m = group * GM;
+  const int gm = min(nbm - first_m, GM);
+  const int in_group = tile - group * GM * nbn;
+  const int64_t m0 = (int64_t)(first_m + in_group % gm) * BM;
+  const int n0 = (in_group / gm) * BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int li = lane & 31, g = lane >> 5;
+
+  // DMA sources.  Band b = wave + i * NW covers stage rows 8b..8b+7; this lane
+  // fills row 8b + lane/8, slot lane%8, i.e. logical chunk slot ^ swz(row).
+  // Rows past M or N are clamped to the last valid row: their products land in
+  // accumulator entries that are never stored.
+  const f16* Ablk = A + m0 * K;
+  const f16* Wblk = W + (int64_t)n0 * K;
+  unsigned src_off[LPT];  // bytes from the block base (A rows) or W block base
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int row = 8 * (wave + i * NW) + (lane >> 3);
+    const int chunk = (lane & 7) ^ chunk_swz(row);
+    if (row < BM) {
+      const int64_t m = min(m0 + row, M - 1) - m0;
+      src_off[i] = (unsigned)((m * K + chunk * 8) * 2);
+    } else {
+      const int n = min(n0 + row - BM, N - 1) - n0;
+      src_off[i] = (unsigned)(((int64_t)n * K + chunk * 8) * 2);
+    }
+  }
+  auto issue = [&](int stage, int k0) {
+    char* sbase = smem + stage * T::STAGE * 2;
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int band = wave + i * NW;
+      const char* src = (8 * band < BM ? reinterpret_cast<const char*>(Ablk) : reinterpret_cast<const char*>(Wblk)) +
+                        (int64_t)k0 * 2 + src_off[i];
+      dma16(src, sbase + band * 1024);
+    }
+  };
+
+  f32x16 acc[T::TN][T::TM];
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i) acc[j][i] = zero16();
+
+  // Operand rows of this lane: A rows wm*WTM + i*32 + li, W rows BM + wn*WTN + j*32 + li;
+  // all share swz = (li >> 1) & 7 (tile offsets are multiples of 16).
+  const int sw = chunk_swz(li);
+  const int arow = (wm * T::WTM + li) * BK;
+  const int wrow = (BM + wn * T::WTN + li) * BK;
+
+  const int KT = K / BK;
+#pragma unroll
+  for (int s = 0; s < ST - 1; ++s)
+    if (s < KT) issue(s, s * BK);
+
+  for (int kt = 0; kt < KT; ++kt) {
+    if constexpr (ST >= 3) {
+      if (kt + 1 < KT) {
+        wait_vmcnt<(ST - 2) * LPT>();
+      } else {
+        wait_vmcnt<0>();
+      }
+    } else {
+      wait_vmcnt<0>();
+    }
+    stage_barrier();
+    if (kt + ST - 1 < KT) issue((kt + ST - 1) % ST, (kt + ST - 1) * BK);
+
+    // Operand fragments double-buffered across the four 16-deep k-steps: the
+    // LDS reads of step kk + 1 are in flight during the MFMAs of step kk.
+    const f16* sa = lds + (kt % ST) * T::STAGE;
+    f16x8 af[2][T::TM], wf[2][T::TN];
+    auto frags = [&](int kk, int b) {
+      const int co = ((2 * kk + g) ^ sw) * 8;
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i) af[b][i] = *reinterpret_cast<const f16x8*>(sa + arow + i * 32 * BK + co);
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) wf[b][j] = *reinterpret_cast<const f16x8*>(sa + wrow + j * 32 * BK + co);
+    };
+    frags(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      if (kk + 1 < BK / 16) frags(kk + 1, (kk + 1) & 1);
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+        for (int i = 0; i < T::TM; ++i) acc[j][i] = mfma32x32x16(wf[kk & 1][j], af[kk & 1][i], acc[j][i]);
+    }
+  }
+  __syncthreads();  // every wave is done with the operand stages
+
+  // Epilogue in TN slices: slice j holds, for every wave column wn, the 32
+  // output columns wn*WTN + j*32 .. +31 (EPW = WN * 32 columns in all), staged
+  // as fp32 rows (+ bias), then written 16 bytes per lane with the residual
+  // added.  Lane li owns row wm*WTM + i*32 + li and, per register quad q,
+  // columns 8q + 4g .. 8q + 4g + 3 of its 32-column block.
+  float* Cs = reinterpret_cast<float*>(smem);
+  constexpr int LPR = T::EPW / 4;  // lanes per staged row
+  constexpr int RPP = NT / LPR;    // rows per pass
+  static_assert(NT % LPR == 0 && BM % RPP == 0, "epilogue geometry");
+  const int c4 = (tid % LPR) * 4;                                 // column within the slice
+  const int ccol = (c4 / 32) * T::WTN + (c4 % 32);                // column within the tile (+ j*32)
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int scol = wn * 32 + 8 * q + 4 * g;
+      const int tcol = wn * T::WTN + j * 32 + 8 * q + 4 * g;
+      f32x4 bq = {0.f, 0.f, 0.f, 0.f};
+      if (bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bq[e] = n0 + tcol + e < N ? bias[n0 + tcol + e] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i) {
+        const int row = wm * T::WTM + i * 32 + li;
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[j][i][4 * q + e] + bq[e];
+        *reinterpret_cast<f32x4*>(Cs + row * T::LDC + scol) = v;
+      }
+    }
+    __syncthreads();
+    const int n = n0 + ccol + j * 32;
+    if (n < N) {  // N % 8 == 0, so a quad is all in or all out
+      for (int r = tid / LPR; r < BM; r += RPP) {
+        const int64_t m = m0 + r;
+        if (m >= M) break;
+        f32x4 v = *reinterpret_cast<const f32x4*>(Cs + r * T::LDC + c4);
+        if (resid) {
+          const TR* rp = resid + m * N + n;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += to_float(rp[e]);
+        }
+        TC* cp = C + m * N + n;
+        if constexpr (sizeof(TC) == 4) {
+          *reinterpret_cast<f32x4*>(cp) = v;
+        } else {
+          f16x4 h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (f16)v[e];
+          *reinterpret_cast<f16x4*>(cp) = h;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC>
+static hipError_t launch_dma(const GemmArgs& a) {
+  const int64_t tiles = ((a.M + BM - 1) / BM) * (int64_t)((a.N + BN - 1) / BN);
+  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WM, WN, ST, GM, TR, TC>), dim3((unsigned)tiles), dim3(WM * WN * 64), 0,
+                     a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+                     static_cast<const TR*>(a.resid), static_cast<TC*>(a.c), a.M, a.N, a.K);
+  return hipGetLastError();
+}
+
+// Tile choice (measured on MI355X): 256 x 256 tiles (128 x 128 per wave, two
+// stages) once there are several rounds of them -- the least LDS traffic per
+// MFMA; otherwise 256 x 128 tiles with three stages, tile ids grouped by eight
+// row blocks.
+template <typename TR, typename TC>
+static hipError_t dispatch_dma(const GemmArgs& a) {
+  const int64_t big = ((a.M + 255) / 256) * (int64_t)((a.N + 255) / 256);
+  if (big >= 4 * (int64_t)compute_units()) return launch_dma<256, 256, 2, 2, 2, 4, TR, TC>(a);
+  return launch_dma<256, 128, 2, 2, 3, 8, TR, TC>(a);
+}
+
+bool gemm_dma_ok(const GemmArgs& a) {
+  // K in whole 64-wide k-tiles; N in 8-column groups; a per-block byte offset
+  // (rows x K) that fits 32 bits; enough tiles to cover the chip.
+  if (a.ln_gamma || a.K % 64 != 0 || a.N % 8 != 0 || a.M <= 0) return false;
+  if ((int64_t)256 * a.K * 2 >= ((int64_t)1 << 32) || (int64_t)128 * a.K * 2 >= ((int64_t)1 << 32)) return false;
+  const int64_t tiles = ((a.M + 255) / 256) * (int64_t)((a.N + 127) / 128);
+  return tiles >= 256;
+}
+
+hipError_t run_gemm_dma(const GemmArgs& a) {
+  const bool c16 = a.c_dtype == kF16;
+  if (!a.resid || a.resid_dtype == kF16) return c16 ? dispatch_dma<f16, f16>(a) : dispatch_dma<f16, float>(a);
+  return c16 ? dispatch_dma<float, f16>(a) : dispatch_dma<float, float>(a);
+}
+
+}  // namespace cobra

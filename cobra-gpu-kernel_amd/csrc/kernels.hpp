@@ -46,7 +46,25 @@ struct GemmArgs {
   float eps;
   hipStream_t stream;
 };
+// Compute units of the current device (cached after the first call).
+inline int compute_units() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
 hipError_t run_gemm(const GemmArgs& a);
+// Large plain-epilogue GEMMs through LDS-DMA tiles (K % 64 == 0, N % 8 == 0,
+// >= 256 tiles); run_gemm routes eligible shapes there.
+bool gemm_dma_ok(const GemmArgs& a);
+hipError_t run_gemm_dma(const GemmArgs& a);
 
 struct AttnArgs {
   const void* qkv;         // [B*S, 3*H*hd] fp16: q | k | v column blocks, head-major inside each

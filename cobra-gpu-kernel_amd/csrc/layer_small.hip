@@ -37,55 +37,9 @@
 // CU rather than once per sequence.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "layer_common.hpp"
 
 namespace cobra {
-
-namespace {
-
-__device__ __forceinline__ void store4(f16* p, const float (&v)[4]) {
-  f16x4 h;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) h[i] = (f16)v[i];
-  *reinterpret_cast<f16x4*>(p) = h;
-}
-__device__ __forceinline__ void store4(float* p, const float (&v)[4]) {
-  f32x4 a;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a[i] = v[i];
-  *reinterpret_cast<f32x4*>(p) = a;
-}
-
-// A zero the optimiser cannot see through.  Offsetting the parameter
-// pointers by it inside the persistent sequence loop keeps their loads in the
-// loop (hoisting them would pin every LayerNorm and bias parameter in
-// registers for the kernel's lifetime) while the pointers stay global.
-__device__ __forceinline__ int opaque_zero() {
-  int z = 0;
-  asm volatile("" : "+s"(z));
-  return z;
-}
-
-// Registers 8*half .. 8*half+7 of a 32x32 accumulator times `scale`, as fp16.
-__device__ __forceinline__ f16x8 scaled_f16(const f32x16& acc, int half, float scale) {
-  f16x8 o;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = (f16)(acc[8 * half + e] * scale);
-  return o;
-}
-
-// Registers 8*half .. 8*half+7 of a 32x32 accumulator (+ per-register bias), as fp16.
-__device__ __forceinline__ f16x8 half_to_f16(const f32x16& acc, int half, const float (&bias)[16]) {
-  f16x8 o;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = (f16)(acc[8 * half + e] + bias[8 * half + e]);
-  return o;
-}
-
-}  // namespace
-
-constexpr int kSmallMaxS = 128;
-constexpr int kSmallWaves = kSmallMaxS / 32;  // one wave per 32-token tile; always launched in full
-constexpr int kLdsBytes = 163840;  // gfx950: LDS per workgroup
 
 // LDS plan of the fused kernel, in 16-byte chunks.
 template <int D, int HD>
@@ -106,19 +60,6 @@ struct SmallLds {
   static constexpr int TOTAL = CORE + (PARAMS ? PCH : 0);
   static_assert(D % 32 == 0 && HD % 32 == 0 && D % HD == 0, "layout");
   static_assert(CORE * 16 <= kLdsBytes, "weights + K/V must fit the workgroup's LDS");
-};
-
-template <typename TX>
-struct XChunks;
-template <>
-struct XChunks<f16> {
-  using c8 = f16x8;
-  using c4 = f16x4;
-};
-template <>
-struct XChunks<float> {
-  using c8 = float __attribute__((ext_vector_type(8)));
-  using c4 = f32x4;
 };
 
 template <int D, int HD, bool CAUSAL, typename TX>
@@ -471,18 +412,6 @@ bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads) {
 
 // Persistent grid: one workgroup per CU (the staged weights fill most of the
 // LDS), each walking the batch with stride gridDim.x.
-static int compute_units() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      n = v;
-    else
-      n = 256;
-  }
-  return n;
-}
 
 // Always four waves: the waves past the sequence's last 32-token tile still
 // share the weight staging (and compute masked tiles nobody reads).
@@ -522,6 +451,7 @@ hipError_t run_layer_small(const SmallLayerArgs& a) {
   if (a.batch == 0) return hipSuccess;
   const double hd = (double)(a.d_model / a.heads);
   const float c2 = (float)(1.0 / sqrt(hd)) * 1.4426950408889634f;
+  if (layer_split_pays(a.batch, a.seq_len)) return run_layer_split(a, c2);
   return a.causal ? small_shape<true>(a, c2) : small_shape<false>(a, c2);
 }
 

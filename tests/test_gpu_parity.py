@@ -144,6 +144,26 @@ def test_graph_replays_match_eager(D, H):
         assert torch.equal(o, e)
 
 
+@pytest.mark.parametrize(
+    "B,S,D,H,causal",
+    [
+        (1100, 128, 128, 4, True),
+        (1100, 128, 128, 2, False),
+        (2100, 65, 96, 3, False),
+        (4200, 40, 64, 1, True),
+    ],
+)
+def test_fused_persistent_kernel(B, S, D, H, causal):
+    """Batches of >= 4096 32-query slices take the persistent fused kernel (one
+    workgroup walks whole sequences); smaller ones take the query-split kernel,
+    which every other fused-plan case here exercises.  Sampled sequences are
+    checked on the CPU."""
+    assert B * ((S + 31) // 32) >= 4096
+    case = LayerCase(f"persistent_B{B}_S{S}_D{D}_H{H}", B, S, D, H, causal)
+    res = check_case(case, seed=7, input_seed=7, subset=[0, 1, B // 2, B - 1])
+    assert res.passed, res
+
+
 def test_base_config_runs_fused_single_kernel():
     from cobra_amd import ops
 
@@ -223,6 +243,38 @@ def test_linear_op():
         assert torch.allclose(got, want, atol=1e-3, rtol=1e-3), (M, N, K, (got - want).abs().max())
         got16 = ops.linear(a, w, b)
         assert torch.allclose(got16.float(), a.float() @ w.float().t() + b, atol=2e-2, rtol=2e-3)
+
+
+@pytest.mark.parametrize("M,N,K,resid", [
+    (8192, 3072, 1024, None),       # the B64 d1024 QKV projection
+    (8192, 1024, 1024, "f32"),      # its out-projection: fp32 store + fp32 residual
+    (8000, 1000, 256, "f32"),       # ragged M and N tiles
+    (4100, 2056, 64, "f16"),        # one k-tile, fp16 residual
+    (65536, 128, 128, "f16"),       # two k-tiles, a single column block
+    (32768, 2048, 256, "f32"),      # enough tiles for the 256 x 256 variant
+    (40000, 1544, 128, None),       # 256 x 256 variant, ragged M and N
+])
+def test_linear_large_tiles(M, N, K, resid):
+    """Shapes large enough (>= 256 tiles of 256 x 128, K % 64 == 0) for the
+    LDS-DMA GEMM, against an fp32 product."""
+    from cobra_amd import ops
+
+    log(f"linear large M{M} N{N} K{K} resid={resid}")
+    g = torch.Generator(device="cpu").manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).half().to(DEV)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).half().to(DEV)
+    b = torch.randn(N, generator=g).to(DEV)
+    r = None
+    if resid is not None:
+        r = torch.randn(M, N, generator=g).to(DEV)
+        r = r.half() if resid == "f16" else r
+    want = a.float() @ w.float().t() + b
+    if r is not None:
+        want = want + r.float()
+    got = ops.linear(a, w, b, out_fp32=True, resid=r)
+    assert torch.allclose(got, want, atol=1e-3, rtol=1e-3), (M, N, K, (got - want).abs().max().item())
+    got16 = ops.linear(a, w, b, resid=r)
+    assert torch.allclose(got16.float(), want, atol=2e-2, rtol=2e-3), (M, N, K)
 
 
 def test_linear_ln_op():
