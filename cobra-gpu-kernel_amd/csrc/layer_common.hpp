@@ -64,9 +64,10 @@ struct XChunks<float> {
   using c4 = f32x4;
 };
 
-// Query-split variant of the fused kernel (layer_split.hip): worth it while
-// batch * ceil(S/32) workgroups take at most two rounds of the chip.
-bool layer_split_pays(int64_t batch, int64_t seq_len);
+// Query-split variant of the fused kernel (layer_split.hip): fp16
+// activations at d_model 64 / 128, while batch * ceil(S/32) workgroups take at
+// most two rounds of the chip.
+bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dtype);
 hipError_t run_layer_split(const SmallLayerArgs& a, float c2);
 
 }  // namespace cobra

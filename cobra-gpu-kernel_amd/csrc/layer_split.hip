@@ -1,7 +1,7 @@
 // The whole attention sublayer in one kernel, split by query slices so that a
 // small batch still covers the chip: workgroup (b, s) produces the outputs of
-// queries 32s .. 32s+31 of sequence b (S <= 128, d_model <= 128, head_dim in
-// {32, 64}; the same shapes as the persistent fused kernel).
+// queries 32s .. 32s+31 of sequence b (S <= 128, fp16 activations, d_model
+// 64 or 128, head_dim 32 or 64).
 //
 //   h = LN1(x);  q,k,v = h W^T + b;  ctx = softmax(q k^T * scale) v;
 //   r = x + ctx W_o^T + b_o;  y = LN2(r)
@@ -13,9 +13,8 @@
 // sequence and walks the heads one after another; here the S/32 workgroups of a
 // sequence run side by side, and inside a workgroup the waves split every
 // phase four ways:
-//   1. wave w loads, straight into registers, the W_k / W_v rows of d-tile w,
-//      the W_q rows of head w and the W_o rows of output tile w, and
-//      normalises tokens 32w .. 32w+31 (LN1) into LDS while those loads fly;
+//   1. wave w normalises tokens 32w .. 32w+31 (LN1) while the W_k / W_v rows
+//      of d-tile w and the W_q rows of head w arrive;
 //   2. wave w projects K^T and V of d-tile w for ALL tokens (every workgroup
 //      of the sequence recomputes them: twice the projection FLOPs of the
 //      persistent kernel, but no cross-workgroup traffic at all), and Q^T of
@@ -25,12 +24,20 @@
 //   4. wave n multiplies the gathered attention output by the W_o rows of
 //      output columns 32n .. 32n+31, adds bias and residual, and LN2 combines
 //      the per-wave row sums through LDS.
-// Every global access is a plain load issued from straight-line code, so the
-// compiler's wait counts stay exact and nothing waits on a transfer it does
-// not need.
+//
+// Every global read is an LDS-DMA (global_load_lds_dwordx4) of whole 1 KB
+// spans: matrix rows land row-major in LDS with 16-byte chunks XOR-swizzled by
+// row, and each lane then reads its MFMA operand fragment (row = lane % 32) from
+// there without bank conflicts.  Reading operands straight from global memory
+// in that layout would touch 32 rows per load instruction; the coalesced DMA
+// moves the same bytes several times faster.  A wave only ever reads what its
+// own DMA wrote until the first barrier, so it waits for exactly the
+// transfers it needs (vmcnt retires in issue order); the barriers publish LDS
+// writes without waiting for DMA still in flight.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "layer_common.hpp"
+#include "lds_dma.hpp"
 
 namespace cobra {
 
@@ -39,124 +46,154 @@ namespace {
 constexpr int kSplitWaves = 4;
 constexpr int kSplitTiles = kSmallMaxS / 32;  // token tiles of a sequence
 
-// LDS plan, in 1 KB chunk rows (64 lanes x 16 bytes, one operand fragment each).
+// LDS plan (bytes) and per-wave DMA counts.
 template <int D, int HD>
-struct SplitLds {
+struct SplitPlan {
   static constexpr int KD = D / 16;    // k-steps over d_model
   static constexpr int NNT = D / 32;   // 32-wide tiles of d_model
   static constexpr int H = D / HD;
   static constexpr int NDT = HD / 32;  // 32-wide d tiles per head
   static constexpr int KSH = HD / 16;  // k-steps per head
-  static constexpr int HB = kSplitTiles * KD;            // LN1 output (token tile, k-step)
-  static constexpr int KT = H * kSplitTiles * KSH;       // K^T fragments (head, key tile, k-step)
-  static constexpr int VT = H * kSplitTiles * NDT * 2;   // V fragments (head, key tile, d tile, half)
-  static constexpr int CTX = KD;                         // attention output of the slice
-  static constexpr int LN1P = kSplitWaves;               // per-wave copy of [gamma1 | beta1]
-  static constexpr int ROWS = HB + KT + VT + CTX + LN1P;
-  static constexpr int STAT = 2 * kSplitWaves * 32;      // LN2 partial sums (pass, wave, query), floats
-  static_assert(D % 32 == 0 && HD % 32 == 0 && D % HD == 0, "layout");
+  static constexpr int ROWB = 2 * D;                   // one fp16 row of d_model
+  static constexpr int TILEB = 32 * ROWB;              // 32 such rows
+  static constexpr int KVB = 2 * kSplitTiles * KD * 1024;  // K^T then V fragments (1 KB each)
+  static constexpr int WKVB = NNT * 2 * TILEB;         // W_k / W_v rows, staged per d-tile
+  static constexpr int A = KVB > WKVB ? KVB : WKVB;    // W_k/W_v staging, then K^T / V
+  static constexpr int X = kSplitWaves * TILEB;        // token tiles, then LN1 output fragments
+  static constexpr int Q = D * ROWB;                   // W_q rows, then W_o rows
+  static constexpr int CX = KD * 1024;                 // attention output fragments
+  static constexpr int RB = 32 * 64;                   // residual block of one wave (32 x 32 fp16)
+  static constexpr int PB = 2048;                      // parameter rows of one wave
+  static constexpr int OFF_X = A, OFF_Q = OFF_X + X, OFF_CX = OFF_Q + Q, OFF_R = OFF_CX + CX;
+  static constexpr int OFF_P = OFF_R + kSplitWaves * RB, OFF_STAT = OFF_P + kSplitWaves * PB;
+  static constexpr int BYTES = OFF_STAT + 2 * kSplitWaves * 32 * 4;
+  // DMA instructions of one wave, in issue order: [gamma1|beta1] 1, token tile N_X,
+  // other parameters 1, W_k/W_v N_A, W_q N_Q, residual N_R; W_o N_O after barrier 1.
+  static constexpr int N_X = TILEB / 1024, N_A = 2 * TILEB / 1024, N_Q = NDT * TILEB / 1024;
+  static constexpr int N_R = RB / 1024, N_O = TILEB / 1024;
+  static_assert(D == 64 || D == 128, "swizzle and row geometry");
+  static_assert((HD == 32 || HD == 64) && D % HD == 0, "head geometry");
   static_assert(H <= kSplitWaves && NNT <= kSplitWaves, "one wave per head and per d / output tile");
-  static_assert(2 * D * 4 <= 1024, "LN1 parameters of one wave fit one 1 KB row");
-  static_assert(ROWS * 1024 + STAT * 4 <= kLdsBytes, "LDS budget");
+  static_assert(KD * 1024 == TILEB, "LN1 output fragments of a tile fill its input tile");
+  static_assert(2 * D * 4 <= 1024 && 2 * 32 + HD + 3 * 32 <= 256, "parameter rows");
+  static_assert(1 + N_X + 1 + N_A + N_Q + N_R < 64, "vmcnt range");
+  static_assert(BYTES <= kLdsBytes, "LDS budget");
 };
+
+// 16-byte chunk c of row r of a row-major fp16 tile with D columns sits at
+// chunk c ^ swz(r): 16 consecutive rows read at one chunk hit 16 distinct
+// 4-bank groups.
+template <int D>
+__device__ __forceinline__ int row_swz(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+
+// DMA of `NI` 1 KB spans of a swizzled row-major [rows][D] fp16 tile at `dst`;
+// src_row(r) is the global address of tile row r.
+template <int D, int NI, typename F>
+__device__ __forceinline__ void dma_rows(char* dst, int lane, F src_row) {
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int o = 1024 * i + 16 * lane;
+    const int r = o / (2 * D), pos = (o % (2 * D)) / 16;
+    dma16(src_row(r) + 8 * (pos ^ row_swz<D>(r)), dst + 1024 * i);
+  }
+}
+
+// Operand fragment of tile row r, logical chunk c.
+template <int D>
+__device__ __forceinline__ f16x8 tile_chunk(const char* tile, int r, int c) {
+  return *reinterpret_cast<const f16x8*>(tile + r * 2 * D + 16 * (c ^ row_swz<D>(r)));
+}
 
 }  // namespace
 
-template <int D, int HD, bool CAUSAL, typename TX>
+template <int D, int HD, bool CAUSAL>
 __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
-    const TX* __restrict__ x, const f16* __restrict__ wqkv, const float* __restrict__ bqkv,
+    const f16* __restrict__ x, const f16* __restrict__ wqkv, const float* __restrict__ bqkv,
     const f16* __restrict__ wo, const float* __restrict__ bo, const float* __restrict__ g1,
-    const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, TX* __restrict__ y,
+    const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, f16* __restrict__ y,
     float* __restrict__ resid_out, int S, int NS, float c2, float eps) {
-  using L = SplitLds<D, HD>;
-  constexpr int KD = L::KD, NNT = L::NNT, H = L::H, NDT = L::NDT, KSH = L::KSH;
-  using Raw8 = typename XChunks<TX>::c8;
-  using Raw4 = typename XChunks<TX>::c4;
+  using P = SplitPlan<D, HD>;
+  constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH;
 
-  __shared__ __attribute__((aligned(1024))) f16x8 lds[L::ROWS * 64 + L::STAT / 4];
-  f16x8* const Hb = lds;                    // LN1 output of every token tile
-  f16x8* const Kl = Hb + L::HB * 64;
-  f16x8* const Vl = Kl + L::KT * 64;
-  f16x8* const Cx = Vl + L::VT * 64;
-  f16x8* const Pw = Cx + L::CTX * 64;       // LN1 parameters, one 1 KB row per wave
-  float* const Stat = reinterpret_cast<float*>(Pw + L::LN1P * 64);
+  __shared__ __attribute__((aligned(1024))) char smem[P::BYTES];
+  char* const rA = smem;               // W_k/W_v staging, then K^T | V fragments
+  char* const rX = smem + P::OFF_X;    // token tiles, then LN1 output fragments
+  char* const rQ = smem + P::OFF_Q;    // W_q rows, then W_o rows
+  f16x8* const Kl = reinterpret_cast<f16x8*>(rA);
+  f16x8* const Vl = Kl + kSplitTiles * KD * 64;
+  f16x8* const Hb = reinterpret_cast<f16x8*>(rX);
+  f16x8* const Cx = reinterpret_cast<f16x8*>(smem + P::OFF_CX);
+  float* const Stat = reinterpret_cast<float*>(smem + P::OFF_STAT);
 
   const int b = blockIdx.x / NS;
   const int s = blockIdx.x - b * NS;  // query slice
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 31, g = lane >> 5;
-  const int tok = 32 * w + li;   // token of this lane for LN1
   const int qtok = 32 * s + li;  // query of this lane for attention, out-projection, LN2
-  const bool tok_ok = tok < S, q_ok = qtok < S;
-  const TX* xs = x + (int64_t)b * S * D;
+  const bool tok_ok = 32 * w + li < S, q_ok = qtok < S;
+  const f16* xs = x + (int64_t)b * S * D;
+  // Waves past the last d-tile / head issue the same transfers for tile / head 0
+  // (identical bytes to the same place), so every wave's wait counts are equal.
+  const int dq = w < NNT ? w : 0, hq = w < H ? w : 0;
+  char* const rP = smem + P::OFF_P + w * P::PB;  // [gamma1 | beta1], then the other parameters
+  char* const rR = smem + P::OFF_R + w * P::RB;  // residual block of this wave
+  char* const rWkv = rA + dq * 2 * P::TILEB;
+  char* const rWq = rQ + hq * NDT * P::TILEB;
+  char* const rWo = rQ + dq * P::TILEB;
+  char* const rTok = rX + w * P::TILEB;
 
-  // ---- 1. loads, in the order they are needed.  Waves past the last head or d-tile
-  // load a valid row they do not use; rows past S load row 0 (S >= 1) and are
-  // zeroed where used.
-  // gamma1 | beta1: 16 bytes per lane, through this wave's own LDS row.
-  f32x4 pv;
-  {
-    const int c = lane * 4;
-    const float* src = c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0);
-    pv = *reinterpret_cast<const f32x4*>(src);
+  // ---- DMA, in the order the data is needed -------------------------------------------
+  {  // [gamma1 | beta1]
+    const int c = 4 * lane;
+    dma16(c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0), rP);
   }
-  // LN1 input: token tok, columns 16kk + 8g + e.
-  Raw8 xin[KD];
-  {
-    const TX* xr = xs + (int64_t)(tok_ok ? tok : 0) * D + 8 * g;
-#pragma unroll
-    for (int kk = 0; kk < KD; ++kk) xin[kk] = *reinterpret_cast<const Raw8*>(xr + 16 * kk);
+  // Token tile w (rows past S fetch row 0, S >= 1, and are zeroed where used).
+  dma_rows<D, P::N_X>(rTok, lane, [&](int r) { return xs + (int64_t)(32 * w + r < S ? 32 * w + r : 0) * D; });
+  {  // 32-float segments: b_k, b_v of d-tile dq; b_q of head hq (2 x 32); b_o, gamma2, beta2 of tile dq
+    const int seg = lane >> 3, off = 4 * (lane & 7);
+    const float* src = seg == 0   ? bqkv + D + 32 * dq + off
+                       : seg == 1 ? bqkv + 2 * D + 32 * dq + off
+                       : seg == 2 ? bqkv + HD * hq + off
+                       : seg == 3 ? bqkv + HD * hq + (HD > 32 ? 32 : 0) + off
+                       : seg == 4 ? bo + 32 * dq + off
+                       : seg == 5 ? g2 + 32 * dq + off
+                       : seg == 6 ? be2 + 32 * dq + off
+                                  : bo + off;
+    dma16(src, rP + 1024);
   }
-  // W_k / W_v rows of d-tile w: lane -> row 32w + li, columns 16kk + 8g .. +8 (the A
-  // operand of K^T = W_k h^T and the B operand of V = h W_v^T).
-  const int dq = w < NNT ? w : 0;
-  f16x8 wk[KD], wv[KD];
-  {
-    const f16* wr = wqkv + (int64_t)(D + 32 * dq + li) * D + 8 * g;
+  // W_k rows 32dq .. 32dq+31, then the W_v rows.
+  dma_rows<D, P::N_A>(rWkv, lane, [&](int r) {
+    return wqkv + (int64_t)((r < 32 ? D : 2 * D - 32) + 32 * dq + r) * D;
+  });
+  // W_q rows of head hq.
+  dma_rows<D, P::N_Q>(rWq, lane, [&](int r) { return wqkv + (int64_t)(HD * hq + r) * D; });
+  // Residual block: queries 32s .. 32s+31, columns 32dq .. 32dq+31, as [32 rows][4 chunks]
+  // with chunk c of row r at c ^ ((r >> 2) & 3).
 #pragma unroll
-    for (int kk = 0; kk < KD; ++kk) {
-      wk[kk] = *reinterpret_cast<const f16x8*>(wr + 16 * kk);
-      wv[kk] = *reinterpret_cast<const f16x8*>(wr + (int64_t)D * D + 16 * kk);
-    }
-  }
-  // W_q rows of head w (A operand of Q^T = W_q h^T): row 32(w*NDT + dt) + li.
-  const int hq = w < H ? w : 0;
-  f16x8 wq[NDT][KD];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int kk = 0; kk < KD; ++kk)
-      wq[dt][kk] = *reinterpret_cast<const f16x8*>(wqkv + (int64_t)(32 * (hq * NDT + dt) + li) * D + 16 * kk + 8 * g);
-  // W_o rows of output tile w (A operand of out^T = W_o ctx^T), in the k order of the
-  // attention output: columns 16ks + 4g + {0..3, 8..11}; the halves are joined where used.
-  f16x4 wlo[KD], whi[KD];
-#pragma unroll
-  for (int ks = 0; ks < KD; ++ks) {
-    const f16* p = wo + (int64_t)(32 * dq + li) * D + 16 * ks + 4 * g;
-    wlo[ks] = *reinterpret_cast<const f16x4*>(p);
-    whi[ks] = *reinterpret_cast<const f16x4*>(p + 8);
-  }
-  // Residual: query qtok, columns 32w + 8qd + 4g + e (rows past S are never stored).
-  Raw4 xres[4];
-  {
-    const TX* xr = xs + (int64_t)(q_ok ? qtok : 0) * D + 32 * dq + 4 * g;
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) xres[qd] = *reinterpret_cast<const Raw4*>(xr + 8 * qd);
+  for (int i = 0; i < P::N_R; ++i) {
+    const int o = 1024 * i + 16 * lane;
+    const int r = o / 64, pos = (o % 64) / 16;
+    const int qr = 32 * s + r < S ? 32 * s + r : 0;
+    dma16(xs + (int64_t)qr * D + 32 * dq + 8 * (pos ^ ((r >> 2) & 3)), rR + 1024 * i);
   }
 
-  // ---- LN1 of token tok (columns 16kk + 8g + e) into the token tile's LDS rows --------
-  Pw[w * 64 + lane] = __builtin_bit_cast(f16x8, pv);
+  // ---- LN1 of token 32w + li (columns 16kk + 8g + e): its tile and parameters are in.
+  wait_vmcnt<1 + P::N_A + P::N_Q + P::N_R>();
   {
     float xv[KD][8];
     float sum = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < KD; ++kk)
+    for (int kk = 0; kk < KD; ++kk) {
+      const f16x8 c = tile_chunk<D>(rTok, li, 2 * kk + g);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        xv[kk][e] = tok_ok ? (float)xin[kk][e] : 0.f;
+        xv[kk][e] = tok_ok ? (float)c[e] : 0.f;
         sum += xv[kk][e];
       }
+    }
     const float mean = (sum + __shfl_xor(sum, 32)) * (1.0f / D);
     float q = 0.f;
 #pragma unroll
@@ -167,48 +204,81 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         q += t * t;
       }
     const float rstd = rsqrtf((q + __shfl_xor(q, 32)) * (1.0f / D) + eps);
-    const float* pw = reinterpret_cast<const float*>(Pw + w * 64);  // written by this wave
+    const float* pg = reinterpret_cast<const float*>(rP);
+    // The output fragments overwrite the token tile in place: every read of it above
+    // feeds the mean, so all of them precede the first write.
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) {
       float gv[8], bv[8];
-      load8(pw + 16 * kk + 8 * g, gv);
-      load8(pw + D + 16 * kk + 8 * g, bv);
+      load8(pg + 16 * kk + 8 * g, gv);
+      load8(pg + D + 16 * kk + 8 * g, bv);
       f16x8 h;
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[kk][e] - mean) * rstd * gv[e] + bv[e]);
       Hb[(w * KD + kk) * 64 + lane] = h;
     }
   }
-  __syncthreads();  // LN1 output of every token tile is in LDS
 
-  // ---- 2. K^T and V of d-tile w for every token tile; Q^T of the slice for head w ---
+  // ---- operand fragments of this wave's weights -------------------------------------------
+  wait_vmcnt<P::N_Q + P::N_R>();
+  f16x8 wk[KD], wv[KD];  // A operand of K^T = W_k h^T; B operand of V = h W_v^T
+#pragma unroll
+  for (int kk = 0; kk < KD; ++kk) {
+    wk[kk] = tile_chunk<D>(rWkv, li, 2 * kk + g);
+    wv[kk] = tile_chunk<D>(rWkv + P::TILEB, li, 2 * kk + g);
+  }
+  wait_vmcnt<P::N_R>();
+  f16x8 wq[NDT][KD];  // A operand of Q^T = W_q h^T
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int kk = 0; kk < KD; ++kk) wq[dt][kk] = tile_chunk<D>(rWq, 32 * dt + li, 2 * kk + g);
+  const float* pp = reinterpret_cast<const float*>(rP + 1024);  // the 32-float segments above
+  lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
+
+  // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.
+  dma_rows<D, P::N_O>(rWo, lane, [&](int r) { return wo + (int64_t)(32 * dq + r) * D; });
+
+  // ---- K^T and V of d-tile w for every token tile; Q^T of the slice for head w ---------
   if (w < NNT) {
     float bk[16], bv[16];
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(bqkv + D + 32 * w + 8 * qd + 4 * g);
+      const f32x4 t = *reinterpret_cast<const f32x4*>(pp + 8 * qd + 4 * g);
 #pragma unroll
       for (int e = 0; e < 4; ++e) bk[4 * qd + e] = t[e];
     }
-    const float bvl = bqkv[2 * D + 32 * w + li];
+    const float bvl = pp[32 + li];
 #pragma unroll
     for (int r = 0; r < 16; ++r) bv[r] = bvl;
     const int h = (32 * w) / HD, t2 = w % NDT;  // head and d tile within the head
-#pragma unroll
-    for (int t = 0; t < kSplitTiles; ++t) {
-      f32x16 ka = zero16(), va = zero16();
+    // Two accumulator pairs: the products of token tile t run on the matrix
+    // cores while tile t-1 is biased, converted and stored.
+    f32x16 ka[2], va[2];
+    auto products = [&](int t) {
+      ka[t & 1] = zero16();
+      va[t & 1] = zero16();
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
         const f16x8 hb = Hb[(t * KD + kk) * 64 + lane];
-        ka = mfma32x32x16(wk[kk], hb, ka);
-        va = mfma32x32x16(hb, wv[kk], va);
+        ka[t & 1] = mfma32x32x16(wk[kk], hb, ka[t & 1]);
+        va[t & 1] = mfma32x32x16(hb, wv[kk], va[t & 1]);
       }
+    };
+    auto store = [&](int t) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = half_to_f16(ka, half, bk);
-        Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = half_to_f16(va, half, bv);
+        Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = half_to_f16(ka[t & 1], half, bk);
+        Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = half_to_f16(va[t & 1], half, bv);
       }
+    };
+    products(0);
+#pragma unroll
+    for (int t = 1; t < kSplitTiles; ++t) {
+      products(t);
+      store(t - 1);
     }
+    store(kSplitTiles - 1);
   }
   f16x8 qB[KSH];
   if (w < H) {
@@ -220,7 +290,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       float bq[16];
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 t = *reinterpret_cast<const f32x4*>(bqkv + 32 * (w * NDT + dt) + 8 * qd + 4 * g);
+        const f32x4 t = *reinterpret_cast<const f32x4*>(pp + 64 + 32 * dt + 8 * qd + 4 * g);
 #pragma unroll
         for (int e = 0; e < 4; ++e) bq[4 * qd + e] = t[e];
       }
@@ -228,9 +298,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       for (int half = 0; half < 2; ++half) qB[2 * dt + half] = half_to_f16(qa, half, bq);
     }
   }
-  __syncthreads();  // K, V of every token tile and head are in LDS
+  lds_barrier();  // K, V of every token tile and head are in LDS
 
-  // ---- 3b. attention of head w: S^T = K Q^T over two blocks of two key tiles, exact
+  // ---- attention of head w: S^T = K Q^T over two blocks of two key tiles, exact
   // softmax with one rescale between the blocks, O^T = V^T P^T.
   if (w < H) {
     const int h = w;
@@ -301,31 +371,38 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int half = 0; half < 2; ++half) Cx[(h * KSH + 2 * dt + half) * 64 + lane] = scaled_f16(ot[dt], half, inv);
   }
-  __syncthreads();  // attention output of every head is in LDS
+  wait_vmcnt<0>();  // W_o rows and the residual block
+  lds_barrier();    // attention output of every head is in LDS
 
-  // ---- 4. out^T tile w = W_o[32w..32w+31] ctx^T, + b_o + x, then LN2 ------------------------
+  // ---- out^T tile w = W_o[32w..32w+31] ctx^T, + b_o + x, then LN2 ----------------------
   float v[4][4];  // query qtok, column 32w + 8qd + 4g + e
   float sum = 0.f;
   if (w < NNT) {
     f32x16 oacc = zero16();
 #pragma unroll
     for (int ks = 0; ks < KD; ++ks) {
-      const f16x8 a = {wlo[ks][0], wlo[ks][1], wlo[ks][2], wlo[ks][3], whi[ks][0], whi[ks][1], whi[ks][2], whi[ks][3]};
+      // Row li of the W_o tile at the k order of the attention output: columns
+      // 16ks + 4g + {0..3} (chunk 2ks) and 16ks + 8 + 4g + {0..3} (chunk 2ks + 1).
+      const char* row = rWo + li * 2 * D + 8 * g;
+      const f16x4 lo = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks) ^ row_swz<D>(li)));
+      const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks + 1) ^ row_swz<D>(li)));
+      const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       oacc = mfma32x32x16(a, Cx[ks * 64 + lane], oacc);
     }
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(bo + 32 * w + 8 * qd + 4 * g);
+      const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 128 + 8 * qd + 4 * g);
+      const f16x4 xr = *reinterpret_cast<const f16x4*>(rR + li * 64 + 16 * (qd ^ ((li >> 2) & 3)) + 8 * g);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[qd][e] = oacc[4 * qd + e] + bb[e] + (float)xres[qd][e];
+        v[qd][e] = oacc[4 * qd + e] + bb[e] + (float)xr[e];
         sum += v[qd][e];
       }
     }
     sum += __shfl_xor(sum, 32);
     if (g == 0) Stat[w * 32 + li] = sum;
   }
-  __syncthreads();
+  lds_barrier();
   float mean = 0.f;
 #pragma unroll
   for (int n = 0; n < NNT; ++n) mean += Stat[n * 32 + li];
@@ -342,7 +419,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     q += __shfl_xor(q, 32);
     if (g == 0) Stat[(kSplitWaves + w) * 32 + li] = q;
   }
-  __syncthreads();
+  lds_barrier();
   if (w < NNT) {
     float var = 0.f;
 #pragma unroll
@@ -353,8 +430,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         const int n0 = 32 * w + 8 * qd + 4 * g;
-        const f32x4 gg = *reinterpret_cast<const f32x4*>(g2 + n0);
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(be2 + n0);
+        const f32x4 gg = *reinterpret_cast<const f32x4*>(pp + 160 + 8 * qd + 4 * g);
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 192 + 8 * qd + 4 * g);
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = (v[qd][e] - mean) * rstd * gg[e] + bb[e];
@@ -365,45 +442,35 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   }
 }
 
-bool layer_split_pays(int64_t batch, int64_t seq_len) {
-  // Up to two rounds of workgroups; beyond that the persistent kernel, which
-  // projects K and V once per sequence, does less work per output.
+bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dtype) {
+  // fp16 activations at d_model 64 / 128, and at most two rounds of workgroups;
+  // beyond that the persistent kernel, which projects K and V once per
+  // sequence, does less work per output.
+  if (x_dtype != kF16 || (d_model != 64 && d_model != 128)) return false;
   const int64_t items = batch * ((seq_len + 31) / 32);
   return items <= 2 * (int64_t)compute_units();
 }
 
-template <int D, int HD, bool CAUSAL, typename TX>
+template <int D, int HD, bool CAUSAL>
 static hipError_t launch_split(const SmallLayerArgs& a, float c2) {
   const int ns = (int)((a.seq_len + 31) / 32);
   const int64_t grid = a.batch * ns;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((layer_split_kernel<D, HD, CAUSAL, TX>), dim3((unsigned)grid), dim3(64 * kSplitWaves), 0,
-                     a.stream, static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
+  hipLaunchKernelGGL((layer_split_kernel<D, HD, CAUSAL>), dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream,
+                     static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
                      static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
-                     static_cast<TX*>(a.y), a.resid_out, (int)a.seq_len, ns, c2, a.eps);
+                     static_cast<f16*>(a.y), a.resid_out, (int)a.seq_len, ns, c2, a.eps);
   return hipGetLastError();
-}
-
-template <int D, int HD, bool CAUSAL>
-static hipError_t split_dtype(const SmallLayerArgs& a, float c2) {
-  return a.x_dtype == kF16 ? launch_split<D, HD, CAUSAL, f16>(a, c2) : launch_split<D, HD, CAUSAL, float>(a, c2);
 }
 
 template <bool CAUSAL>
 static hipError_t split_shape(const SmallLayerArgs& a, float c2) {
   const int64_t hd = a.d_model / a.heads;
-  if (a.d_model == 128) {
-    if (hd == 32) return split_dtype<128, 32, CAUSAL>(a, c2);
-    return split_dtype<128, 64, CAUSAL>(a, c2);
-  }
-  if (a.d_model == 64) {
-    if (hd == 32) return split_dtype<64, 32, CAUSAL>(a, c2);
-    return split_dtype<64, 64, CAUSAL>(a, c2);
-  }
-  return split_dtype<96, 32, CAUSAL>(a, c2);
+  if (a.d_model == 128) return hd == 32 ? launch_split<128, 32, CAUSAL>(a, c2) : launch_split<128, 64, CAUSAL>(a, c2);
+  return hd == 32 ? launch_split<64, 32, CAUSAL>(a, c2) : launch_split<64, 64, CAUSAL>(a, c2);
 }
 
-// Shape and dtype checks are the caller's (run_layer_small).
+// Shape and dtype checks are the caller's (run_layer_small, layer_split_pays).
 hipError_t run_layer_split(const SmallLayerArgs& a, float c2) {
   return a.causal ? split_shape<true>(a, c2) : split_shape<false>(a, c2);
 }

@@ -18,10 +18,13 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
 }
 
 // s_waitcnt vmcnt(n), leaving the other counters unconstrained (gfx9 encoding).
+// The empty asm statement keeps the compiler from hoisting reads of the DMA'd
+// LDS above the wait.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
 }
 
 // Workgroup barrier without the memory fence of __syncthreads(): that fence
@@ -31,6 +34,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // accesses across.
 __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Workgroup barrier that publishes this wave's LDS writes (lgkmcnt(0)) but,
+// unlike __syncthreads(), does not wait for outstanding global loads or DMA.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
