@@ -47,7 +47,15 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """The device's current stream handle.  The raw query costs ~0.1 us; building
+    a Stream object (torch.cuda.current_stream) costs ~3 us, a quarter of a
+    small forward's launch budget."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -127,8 +127,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   f16x8* const Cx = reinterpret_cast<f16x8*>(smem + P::OFF_CX);
   float* const Stat = reinterpret_cast<float*>(smem + P::OFF_STAT);
 
-  const int b = blockIdx.x / NS;
-  const int s = blockIdx.x - b * NS;  // query slice
+  // The S/32 slices of a sequence run on one XCD, so its L2 serves the token
+  // tiles they all read.
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int b = item / NS;
+  const int s = item - b * NS;  // query slice
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 31, g = lane >> 5;
