@@ -21,9 +21,13 @@
 //     the V^T operand is read in exactly that key order with two
 //     ds_read_b64_tr_b16 (a 4x4 transpose within each 16-lane group);
 //   * K and V tiles are row-major in LDS, 16-byte chunks XOR-swizzled by row
-//     (no padding, conflict-free operand reads), double-buffered: the next key
-//     block is prefetched into registers during the matrix work and stored to
-//     the other buffer, one barrier per block;
+//     (no padding, conflict-free operand reads), filled by coalesced LDS-DMA
+//     (global_load_lds_dwordx4, 1 KB per wave instruction) 3-4 key blocks ahead:
+//     each wave waits for its own transfers (vmcnt), one barrier per block
+//     publishes them and retires the stage the next DMA refills;
+//   * the Q tile arrives the same way (its own LDS region in short-sequence
+//     launches, so it overlaps the first K/V stages), and the output tile leaves
+//     through LDS so that the stores to ctx are whole coalesced rows;
 //   * the Q fragments are pre-scaled by scale * log2(e) and each score tile's
 //     accumulator starts at -m (the query's running max), so the matrix cores
 //     deliver s - m in the exp2 domain and p = exp2 of the accumulator;
@@ -36,6 +40,7 @@
 //     exchange with lane ^ 32 uses v_permlane32_swap.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 
 namespace cobra {
 
@@ -89,20 +94,33 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 
 }  // namespace
 
-template <int HD, int NW, int BN, bool CAUSAL>
+template <int HD, int NW, int BN, int ST, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict__ qkv, f16* __restrict__ ctx,
                                                            int S, int H, int hd, float c2, int nqb) {
   constexpr int BM = 32 * NW;          // queries per workgroup
   constexpr int KS = HD / 16;          // k-steps of the QK^T product
   constexpr int ND = (HD + 31) / 32;   // 32-row blocks of d in O^T
   constexpr int NT = NW * 64;
-  constexpr int CPR = HD / 8;          // 16-byte chunks per key row
-  constexpr int CH = BN * CPR;         // chunks per tile
-  constexpr int IT = (CH + NT - 1) / NT;
+  constexpr int CPR = HD / 8;          // 16-byte chunks per row
+  constexpr int TB = BN * HD * 2;      // bytes of one K (or V) tile
+  constexpr int SB = 2 * TB;           // bytes of one stage: K tile, then V tile
+  constexpr int NI = SB / 1024;        // 1 KB DMA spans per stage
+  constexpr int LPT = NI / NW;         // spans per wave per stage
+  constexpr int QPT = BM * HD * 2 / 1024 / NW;  // Q-tile spans per wave
   static_assert(HD % 16 == 0 && BN % 32 == 0, "tile geometry");
+  static_assert(NI % NW == 0 && LPT >= 1 && (NI / 2) % 1 == 0, "every wave DMAs whole spans of each stage");
+  // Short-sequence launches (<= 4 waves) give the Q tile its own LDS region, so its
+  // DMA overlaps the first K/V stages instead of preceding them; 8-wave launches
+  // (long sequences) stage it through the K/V stages to keep LDS small.
+  constexpr bool QSEP = NW <= 4;
+  constexpr int QB = BM * HD * 2;
+  constexpr int LDSB = ST * SB + (QSEP ? QB : 0);
+  static_assert(BM * HD * 2 <= ST * SB, "the output tile passes through the K/V stages");
+  static_assert(ST >= 2 && (ST - 1) * LPT < 64, "vmcnt range");
+  static_assert(LDSB <= 163840, "LDS budget");
 
-  __shared__ __attribute__((aligned(16))) f16 Ks[2][BN * HD];
-  __shared__ __attribute__((aligned(16))) f16 Vs[2][BN * HD];
+  __shared__ __attribute__((aligned(1024))) char smem[LDSB];
+  char* const qtile = smem + (QSEP ? ST * SB : 0);
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = id % nqb;
@@ -122,63 +140,31 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   const int q0w = qb * BM + w * 32;  // this wave's first query
   const int qi = q0w + li;           // this lane's query
 
-  // Q^T fragments: B operand of S^T = K . Q^T (k = d), pre-scaled by
-  // scale * log2(e) so that the products come out in the exp2 domain.
-  f16x8 qf[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    const int d0 = kk * 16 + g * 8;
-    if (qi < S && d0 < hd) {
-      const f16x8 q = *reinterpret_cast<const f16x8*>(qbase + qi * ld + d0);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[kk][e] = (f16)((float)q[e] * c2);
-    } else {
-      qf[kk] = zero8();
-    }
-  }
-
-  // K/V tile loads: a wave-uniform block base plus a fixed per-thread offset;
-  // only a block reaching past S needs the per-row predicate.  (256-wide heads
-  // keep the single predicated path: their registers are full, and a second
-  // copy of the loads costs them accumulator moves.)
-  unsigned voff[IT];
-  bool vok[IT];
-#pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int c = tid + i * NT;
-    vok[i] = (CH % NT == 0 || c < CH) && (c % CPR) * 8 < hd;
-    voff[i] = vok[i] ? (unsigned)((c / CPR) * ld + (c % CPR) * 8) : 0u;
-  }
-  f16x8 rk[IT], rv[IT];
-  auto gload = [&](int kb) {
-    const f16* kblk = kbase + (int64_t)kb * ld;
-    const f16* vblk = vbase + (int64_t)kb * ld;
-    if (HD <= 128 && kb + BN <= S) {
-#pragma unroll
-      for (int i = 0; i < IT; ++i) {
-        rk[i] = vok[i] ? *reinterpret_cast<const f16x8*>(kblk + voff[i]) : zero8();
-        rv[i] = vok[i] ? *reinterpret_cast<const f16x8*>(vblk + voff[i]) : zero8();
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < IT; ++i) {
-        const int c = tid + i * NT;
-        const bool ok = vok[i] && kb + c / CPR < S;
-        rk[i] = ok ? *reinterpret_cast<const f16x8*>(kblk + voff[i]) : zero8();
-        rv[i] = ok ? *reinterpret_cast<const f16x8*>(vblk + voff[i]) : zero8();
-      }
-    }
+  // Row-major [rows][HD] tiles in LDS, chunk c of row r at c ^ swz(r), filled by
+  // coalesced LDS-DMA: 1 KB span `sp` of a tile holds rows sp*1024/(2HD) ..; each lane
+  // fetches the global chunk that belongs in its slot.  Rows past S fetch row S-1 and
+  // chunks past hd fetch chunk 0 (finite values; masked, zero-weighted or not stored).
+  auto dma_tile = [&](char* tile, int sp, const f16* base, int row0) {
+    const int o = sp * 1024 + 16 * lane;
+    const int row = o / (2 * HD), pos = (o % (2 * HD)) / 16;
+    const int r = min(row0 + row, S - 1);
+    const int d0 = 8 * (pos ^ swz<HD>(row));
+    dma16(base + (int64_t)r * ld + (d0 < hd ? d0 : 0), tile + sp * 1024);
   };
-  auto sstore = [&](int buf) {
+
+  // Q^T fragments: B operand of S^T = K . Q^T (k = d), staged through LDS and
+  // pre-scaled by scale * log2(e) so that the products come out in the exp2 domain.
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-      const int c = tid + i * NT;
-      if (CH % NT == 0 || c < CH) {
-        const int row = c / CPR;
-        const int off = row * HD + (((c % CPR) ^ swz<HD>(row)) * 8);
-        *reinterpret_cast<f16x8*>(&Ks[buf][off]) = rk[i];
-        *reinterpret_cast<f16x8*>(&Vs[buf][off]) = rv[i];
-      }
+  for (int i = 0; i < QPT; ++i) dma_tile(qtile, w + NW * i, qbase, qb * BM);
+
+  // K/V stages: ST tiles deep, one barrier per key block.
+  auto issue = [&](int stage, int kb) {
+    char* sbase = smem + stage * SB;
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int span = w + NW * i;
+      const bool v = span >= NI / 2;
+      dma_tile(sbase + (v ? TB : 0), v ? span - NI / 2 : span, v ? vbase : kbase, kb);
     }
   };
 
@@ -196,17 +182,70 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
 
   const int kend = CAUSAL ? min(S, (qb + 1) * BM) : S;
   const int nblk = (kend + BN - 1) / BN;
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  const int pre = min(ST - 1, nblk);  // key blocks in flight before the loop
+  if constexpr (QSEP) {
+#pragma unroll
+    for (int s = 0; s < ST - 1; ++s)
+      if (s < nblk) issue(s, s * BN);
+    // The Q tile is the oldest transfer: wait for it alone.
+    if constexpr (ST >= 4) {
+      if (pre >= 3) {
+        wait_vmcnt<3 * LPT>();
+      } else if (pre == 2) {
+        wait_vmcnt<2 * LPT>();
+      } else {
+        wait_vmcnt<LPT>();
+      }
+    } else {
+      if (pre >= 2) {
+        wait_vmcnt<2 * LPT>();
+      } else {
+        wait_vmcnt<LPT>();
+      }
+    }
+  } else {
+    wait_vmcnt<0>();
+  }
+  stage_barrier();
+  f16x8 qf[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const int row = w * 32 + li, d0 = kk * 16 + g * 8;
+    const f16x8 q = *reinterpret_cast<const f16x8*>(qtile + row * 2 * HD + 16 * ((2 * kk + g) ^ swz<HD>(row)));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[kk][e] = d0 < hd ? (f16)((float)q[e] * c2) : (f16)0.0f;
+  }
+  if constexpr (!QSEP) {
+    lds_barrier();  // every wave has its Q fragments before the stages are refilled
+#pragma unroll
+    for (int s = 0; s < ST - 1; ++s)
+      if (s < nblk) issue(s, s * BN);
+  }
   for (int n = 0; n < nblk; ++n) {
     const int kb = n * BN;
-    const int cur = n & 1;
-    const bool more = n + 1 < nblk;
-    if (more) gload(kb + BN);
-    const f16* Kc = Ks[cur];
-    const f16* Vc = Vs[cur];
-
+    // Blocks n+1 .. n+ST-2 may still be in flight; block n must have landed.
+    const int ahead = min(ST - 2, nblk - 1 - n);
+    if constexpr (ST >= 4) {
+      if (ahead >= 2) {
+        wait_vmcnt<2 * LPT>();
+      } else if (ahead == 1) {
+        wait_vmcnt<LPT>();
+      } else {
+        wait_vmcnt<0>();
+      }
+    } else if constexpr (ST == 3) {
+      if (ahead >= 1) {
+        wait_vmcnt<LPT>();
+      } else {
+        wait_vmcnt<0>();
+      }
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();  // block n visible to all waves; every wave is done with block n-1
+    if (n + ST - 1 < nblk) issue((n + ST - 1) % ST, (n + ST - 1) * BN);
+    const f16* Kc = reinterpret_cast<const f16*>(smem + (n % ST) * SB);
+    const f16* Vc = reinterpret_cast<const f16*>(smem + (n % ST) * SB + TB);
     // s = scores in the exp2 domain minus the running max: the accumulator
     // starts at -m_run (every register of a lane belongs to the lane's query).
     f32x16 s[BN / 32];
@@ -289,36 +328,43 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
         o[j] = mfma32x32x16(a, pf[ks], o[j]);
       }
 
-    if (more) sstore(cur ^ 1);
-    __syncthreads();
   }
 
+  // Output through LDS: O^T quads into [BM][HD] rows, then whole 16-byte chunks per
+  // lane, so the stores to ctx are row-contiguous.
   const float l_tot = sum_xor32(l_run);
   const float inv = 1.0f / l_tot;
-  if (qi < S) {
-    f16* out = ctx + (b * S + qi) * (int64_t)D + h * hd;
+  lds_barrier();  // every wave is done with the last stage
 #pragma unroll
-    for (int j = 0; j < ND; ++j)
+  for (int j = 0; j < ND; ++j)
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = j * 32 + 8 * q4 + 4 * g;
-        if (d < hd) {
-          f16x4 v;
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = j * 32 + 8 * q4 + 4 * g;
+      if (HD >= 32 || d < HD) {
+        const int row = w * 32 + li;
+        f16x4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (f16)(o[j][q4 * 4 + e] * inv);
-          *reinterpret_cast<f16x4*>(out + d) = v;
-        }
+        for (int e = 0; e < 4; ++e) v[e] = (f16)(o[j][q4 * 4 + e] * inv);
+        *reinterpret_cast<f16x4*>(smem + row * 2 * HD + 16 * ((d >> 3) ^ swz<HD>(row)) + 8 * g) = v;
       }
+    }
+  lds_barrier();
+  for (int idx = tid; idx < BM * CPR; idx += NT) {
+    const int row = idx / CPR, c = idx % CPR;
+    const int q = qb * BM + row, d0 = 8 * c;
+    if (q < S && d0 < hd)
+      *reinterpret_cast<f16x8*>(ctx + (b * S + q) * (int64_t)D + h * hd + d0) =
+          *reinterpret_cast<const f16x8*>(smem + row * 2 * HD + 16 * (c ^ swz<HD>(row)));
   }
 }
 
-template <int HD, int NW, int BN, bool CAUSAL>
+template <int HD, int NW, int BN, int ST, bool CAUSAL>
 static hipError_t launch_attn(const AttnArgs& a, float c2) {
   constexpr int BM = 32 * NW;
   const int nqb = (a.seq_len + BM - 1) / BM;
   const int64_t grid = (int64_t)nqb * a.heads * a.batch;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, CAUSAL>), dim3((unsigned)grid), dim3(NW * 64), 0, a.stream,
+  hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL>), dim3((unsigned)grid), dim3(NW * 64), 0, a.stream,
                      static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads, a.head_dim, c2,
                      nqb);
   return hipGetLastError();
@@ -329,17 +375,19 @@ static hipError_t dispatch_waves(const AttnArgs& a, float c2) {
   // Waves per workgroup follow the sequence length: every K/V tile a
   // workgroup stages is shared by all of its waves, so long sequences take 8
   // (256 queries), short ones fewer so that no wave idles past S.  Wide heads
-  // keep 4: their per-thread share of the K/V prefetch and the O accumulator
-  // already fill the register file.
+  // keep 4: the O accumulator already fills the register file.  Key blocks of
+  // BN keys (one 1 KB DMA span per wave at least), ST stages deep.
   constexpr int BN = HD >= 256 ? 32 : 64;
+  constexpr int BN8 = HD <= 16 ? 128 : BN;  // 8 waves x one 1 KB span per stage
+  constexpr int ST = HD >= 128 ? 3 : 4;
   if constexpr (HD <= 64) {
-    if (a.seq_len <= 32) return launch_attn<HD, 1, BN, CAUSAL>(a, c2);
-    if (a.seq_len <= 64) return launch_attn<HD, 2, BN, CAUSAL>(a, c2);
+    if (a.seq_len <= 32) return launch_attn<HD, 1, BN, ST, CAUSAL>(a, c2);
+    if (a.seq_len <= 64) return launch_attn<HD, 2, BN, ST, CAUSAL>(a, c2);
   }
   if constexpr (HD <= 128) {
-    if (a.seq_len > 128) return launch_attn<HD, 8, BN, CAUSAL>(a, c2);
+    if (a.seq_len > 128) return launch_attn<HD, 8, BN8, ST, CAUSAL>(a, c2);
   }
-  return launch_attn<HD, 4, BN, CAUSAL>(a, c2);
+  return launch_attn<HD, 4, BN, ST, CAUSAL>(a, c2);
 }
 
 template <bool CAUSAL>
