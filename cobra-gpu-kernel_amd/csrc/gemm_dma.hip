@@ -240,24 +240,25 @@ static hipError_t launch_dma(const GemmArgs& a) {
   return hipGetLastError();
 }
 
-// Tile choice (measured on MI355X): 256 x 256 tiles (128 x 128 per wave, two
-// stages) once there are several rounds of them -- the least LDS traffic per
-// MFMA; otherwise 256 x 128 tiles with three stages, tile ids grouped by eight
-// row blocks.
+// Tile choice (measured on MI355X): 128 x 128 tiles with two stages (64 KB of
+// LDS, 169 VGPRs) run two workgroups per CU, whose barriers and DMA waits
+// interleave -- the best choice for every shape measured except very large
+// fp16-output products (>= 4 rounds of 256 x 256 tiles), where 256 x 256 tiles
+// (128 x 128 per wave, the least LDS traffic per MFMA) are ~5-8 % faster.
 template <typename TR, typename TC>
 static hipError_t dispatch_dma(const GemmArgs& a) {
   const int64_t big = ((a.M + 255) / 256) * (int64_t)((a.N + 255) / 256);
-  if (big >= 4 * (int64_t)compute_units()) return launch_dma<256, 256, 2, 2, 2, 4, TR, TC>(a);
-  return launch_dma<256, 128, 2, 2, 3, 8, TR, TC>(a);
+  if (sizeof(TC) == 2 && big >= 4 * (int64_t)compute_units()) return launch_dma<256, 256, 2, 2, 2, 4, TR, TC>(a);
+  return launch_dma<128, 128, 2, 2, 2, 8, TR, TC>(a);
 }
 
 bool gemm_dma_ok(const GemmArgs& a) {
   // K in whole 64-wide k-tiles; N in 8-column groups; a per-block byte offset
-  // (rows x K) that fits 32 bits; enough tiles to cover the chip.
+  // (rows x K) that fits 32 bits; at least half a round of 128 x 128 tiles.
   if (a.ln_gamma || a.K % 64 != 0 || a.N % 8 != 0 || a.M <= 0) return false;
-  if ((int64_t)256 * a.K * 2 >= ((int64_t)1 << 32) || (int64_t)128 * a.K * 2 >= ((int64_t)1 << 32)) return false;
-  const int64_t tiles = ((a.M + 255) / 256) * (int64_t)((a.N + 127) / 128);
-  return tiles >= 256;
+  if ((int64_t)256 * a.K * 2 >= ((int64_t)1 << 32)) return false;
+  const int64_t tiles = ((a.M + 127) / 128) * (int64_t)((a.N + 127) / 128);
+  return 2 * tiles >= compute_units();
 }
 
 hipError_t run_gemm_dma(const GemmArgs& a) {

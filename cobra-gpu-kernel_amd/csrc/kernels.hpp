@@ -61,8 +61,8 @@ inline int compute_units() {
 }
 
 hipError_t run_gemm(const GemmArgs& a);
-// Large plain-epilogue GEMMs through LDS-DMA tiles (K % 64 == 0, N % 8 == 0,
-// >= 256 tiles); run_gemm routes eligible shapes there.
+// Plain-epilogue GEMMs through LDS-DMA tiles (K % 64 == 0, N % 8 == 0, at
+// least half a round of 128 x 128 tiles); run_gemm routes eligible shapes there.
 bool gemm_dma_ok(const GemmArgs& a);
 hipError_t run_gemm_dma(const GemmArgs& a);
 

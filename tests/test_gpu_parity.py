@@ -253,6 +253,8 @@ def test_linear_op():
     (65536, 128, 128, "f16"),       # two k-tiles, a single column block
     (32768, 2048, 256, "f32"),      # enough tiles for the 256 x 256 variant
     (40000, 1544, 128, None),       # 256 x 256 variant, ragged M and N
+    (8192, 384, 128, None),         # the d128 QKV projection: half a round of 128 x 128 tiles
+    (6000, 264, 64, "f16"),         # ragged M and N at the tile-count threshold
 ])
 def test_linear_large_tiles(M, N, K, resid):
     """Shapes large enough (>= 256 tiles of 256 x 128, K % 64 == 0) for the
