@@ -15,12 +15,17 @@ from typing import Optional
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcobra_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F16 = 0
 F32 = 1
 PLAN_FUSED = 0
 PLAN_STAGED = 1
+# Epilogue / row-mask flags (COBRA_EPI_* in include/cobra_amd.h).
+EPI_GELU = 1
+EPI_MASK_BRANCH = 2
+EPI_MASK_RESID = 4
+EPI_MASK_OUT = 8
 
 _c_int = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -31,18 +36,24 @@ _vp = ctypes.c_void_p
 SIGNATURES = {
     "cobra_version": (_c_int, []),
     "cobra_error_string": (ctypes.c_char_p, [_c_int]),
-    "cobra_ln_fwd": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _c_f32, _vp]),
-    "cobra_linear_fwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp]),
+    "cobra_ln_fwd": (
+        _c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _c_i64, _c_i64, _c_f32, _vp],
+    ),
+    "cobra_linear_fwd": (
+        _c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp],
+    ),
     "cobra_linear_ln_fwd": (
         _c_int,
-        [_vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_f32, _vp],
+        [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_f32,
+         _vp],
     ),
-    "cobra_attn_fwd": (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp]),
-    "cobra_layer_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64]),
-    "cobra_layer_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "cobra_mask_bits": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+    "cobra_attn_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp]),
+    "cobra_layer_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "cobra_layer_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
     "cobra_layer_fwd": (
         _c_int,
-        [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64,
+        [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_f32, _vp],
     ),
 }

@@ -24,7 +24,12 @@ mirrors the reference's orchestration (TTB:857-1541):
   fused plan is one direct launch, because replaying a one-node graph costs
   about four times a direct launch on this runtime (``graph=True`` forces it);
 * inputs that do not fit one device pass are streamed in batch chunks sized
-  from ``hipMemGetInfo`` with halve-on-OOM (``streaming``, TTB:1364-1508).
+  from ``hipMemGetInfo`` with halve-on-OOM (``streaming``, TTB:1364-1508);
+* ``valid_token_mask`` ([B, S] bool) masks padded keys and zeroes the padded
+  rows' attention output, as ``BaselineSelfAttention`` does (TTB:106-109,
+  121-122), for any mask (not only left-aligned padding).  It is applied
+  whenever given, without a host-side ``.all()`` test; the graph path copies
+  it into a static buffer like the reference (TTB:1338, 1353-1354).
 """
 
 from __future__ import annotations
@@ -105,6 +110,7 @@ class CobraAttentionSublayer(nn.Module):
         self._static_x: Optional[torch.Tensor] = None
         self._static_y: Optional[torch.Tensor] = None
         self._static_r: Optional[torch.Tensor] = None
+        self._static_m: Optional[torch.Tensor] = None
 
     # -- parameters ---------------------------------------------------------
 
@@ -139,24 +145,24 @@ class CobraAttentionSublayer(nn.Module):
         return_residual: bool = False,
     ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
         causal = self.causal if causal is None else bool(causal)
-        if valid_token_mask is not None and not bool(valid_token_mask.all()):
-            raise NotImplementedError("padded sequences (valid_token_mask with False entries) are not supported yet")
         pack = self._packed()
         # Free memory moves between calls, so big or host-resident inputs are
         # re-checked every time (TTB:1402-1406); small ones never pay for it.
         if not x.is_cuda or x.numel() * x.element_size() >= streaming.STREAM_MIN_BYTES:
             self._validate(x)
             if self._stream_needed(x):
-                return self._run_streamed(x, causal, return_residual)
-        sig = (x.shape, x.dtype, x.device, causal, return_residual)
+                return self._run_streamed(x, valid_token_mask, causal, return_residual)
+        masked = valid_token_mask is not None
+        sig = (x.shape, x.dtype, x.device, causal, return_residual, masked)
         if sig != self._sig:
             self._validate(x)
-            self._prepare(sig, x)
+            self._prepare(sig, x, masked)
         if not x.is_contiguous():
             x = x.contiguous()
+        m = self._mask_bytes(valid_token_mask, x) if masked else None
         if self._graph_ok:
-            return self._run_graphed(x, pack, causal, return_residual)
-        return self._run_eager(x, pack, causal, return_residual)
+            return self._run_graphed(x, m, pack, causal, return_residual)
+        return self._run_eager(x, m, pack, causal, return_residual)
 
     # -- planning -------------------------------------------------------------
 
@@ -166,46 +172,68 @@ class CobraAttentionSublayer(nn.Module):
         if x.dtype not in (torch.float16, torch.float32):
             raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
 
-    def _prepare(self, sig, x: torch.Tensor) -> None:
+    @staticmethod
+    def _mask_bytes(mask: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """The [B, S] token mask as contiguous device bytes (0 = padded).
+
+        A bool mask is reinterpreted, not converted (TTB:1203-1205).  The mask
+        is always applied -- there is no ``.all()`` test, which would cost a
+        device synchronisation per call.
+        """
+        if tuple(mask.shape) != tuple(x.shape[:2]):
+            raise ValueError(f"valid_token_mask must be {tuple(x.shape[:2])}, got {tuple(mask.shape)}")
+        if mask.dtype not in (torch.bool, torch.uint8):
+            raise TypeError(f"valid_token_mask must be bool or uint8, got {mask.dtype}")
+        if mask.device != x.device:
+            mask = mask.to(x.device, non_blocking=True)
+        mask = mask.contiguous()
+        return mask.view(torch.uint8) if mask.dtype == torch.bool else mask
+
+    def _prepare(self, sig, x: torch.Tensor, masked: bool) -> None:
         """Per-signature set-up (the reference's _prepare, TTB:948-1081): plan,
         workspace, graph gate.  Never runs on the steady-state path."""
         B, S, D = x.shape
         H = self.attention.num_heads
-        self.plan = ops.layer_plan(B, S, D, H)
-        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H), dtype=torch.uint8, device=x.device)
+        self.plan = ops.layer_plan(B, S, D, H, masked)
+        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H, masked), dtype=torch.uint8, device=x.device)
         small = x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
         if self.graph is None:
             self._graph_ok = small and self.plan != ops.PLAN_FUSED
         else:
             self._graph_ok = bool(self.graph) and small
         self._graph = None
-        self._static_x = self._static_y = self._static_r = None
+        self._static_x = self._static_y = self._static_r = self._static_m = None
         self._sig = sig
 
-    def _launch(self, x, y, r, pack: _Pack, ws: torch.Tensor, causal: bool) -> None:
+    def _launch(self, x, m, y, r, pack: _Pack, ws: torch.Tensor, causal: bool) -> None:
         ops.layer_fwd(x, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w, pack.ln1_b, pack.ln2_w,
-                      pack.ln2_b, y, ws, self.attention.num_heads, causal, self.norm1.eps, resid_out=r)
+                      pack.ln2_b, y, ws, self.attention.num_heads, causal, self.norm1.eps, resid_out=r,
+                      valid_mask=m)
 
-    def _run_eager(self, x, pack, causal, return_residual, ws=None):
+    def _run_eager(self, x, m, pack, causal, return_residual, ws=None):
         y = torch.empty_like(x)
         r = torch.empty(x.shape, dtype=torch.float32, device=x.device) if return_residual else None
-        self._launch(x, y, r, pack, self._ws if ws is None else ws, causal)
+        self._launch(x, m, y, r, pack, self._ws if ws is None else ws, causal)
         return (r, y) if return_residual else y
 
-    def _run_graphed(self, x, pack, causal, return_residual):
+    def _run_graphed(self, x, m, pack, causal, return_residual):
         if self._graph is None:
             self._static_x = x.clone()
+            self._static_m = None if m is None else m.clone()
             self._static_y = torch.empty_like(x)
             self._static_r = (torch.empty(x.shape, dtype=torch.float32, device=x.device)
                               if return_residual else None)
             # One eager pass first: loads the code objects outside the capture.
-            self._launch(self._static_x, self._static_y, self._static_r, pack, self._ws, causal)
+            self._launch(self._static_x, self._static_m, self._static_y, self._static_r, pack, self._ws, causal)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                self._launch(self._static_x, self._static_y, self._static_r, pack, self._ws, causal)
+                self._launch(self._static_x, self._static_m, self._static_y, self._static_r, pack, self._ws,
+                             causal)
             self._graph = graph
         if x.data_ptr() != self._static_x.data_ptr():
             self._static_x.copy_(x)
+        if m is not None and m.data_ptr() != self._static_m.data_ptr():
+            self._static_m.copy_(m)
         self._graph.replay()
         return (self._static_r, self._static_y) if return_residual else self._static_y
 
@@ -218,7 +246,7 @@ class CobraAttentionSublayer(nn.Module):
 
     def _per_seq_bytes(self, x: torch.Tensor, return_residual: bool) -> int:
         B, S, D = x.shape
-        ws = ops.layer_workspace_bytes(1, S, D, self.attention.num_heads)
+        ws = ops.layer_workspace_bytes(1, S, D, self.attention.num_heads, True)
         return streaming.live_bytes_per_sequence(ws, S, D, x.element_size(), return_residual)
 
     def _stream_needed(self, x: torch.Tensor) -> bool:
@@ -230,11 +258,17 @@ class CobraAttentionSublayer(nn.Module):
         live = self._per_seq_bytes(x, False) * x.shape[0]
         return streaming.should_stream(x.is_cuda, nbytes, x.shape[0], live, free)
 
-    def _run_streamed(self, x, causal, return_residual):
+    def _run_streamed(self, x, valid_token_mask, causal, return_residual):
         dev = self.norm1.weight.device
         pack = self._packed()
         B, S, D = x.shape
         host = not x.is_cuda
+        masked = valid_token_mask is not None
+        if masked:
+            if tuple(valid_token_mask.shape) != (B, S):
+                raise ValueError(f"valid_token_mask must be {(B, S)}, got {tuple(valid_token_mask.shape)}")
+            if valid_token_mask.dtype not in (torch.bool, torch.uint8):
+                raise TypeError(f"valid_token_mask must be bool or uint8, got {valid_token_mask.dtype}")
         free, _ = torch.cuda.mem_get_info(dev)
         step = streaming.plan_chunk(B, self._per_seq_bytes(x, return_residual), free)
         y_all = torch.empty_like(x)
@@ -245,11 +279,12 @@ class CobraAttentionSublayer(nn.Module):
             xc = x[b0:b1]
             xc = xc.to(dev, non_blocking=True) if host else xc.contiguous()
             n = b1 - b0
+            mc = self._mask_bytes(valid_token_mask[b0:b1], xc) if masked else None
             if n not in ws_cache:
                 ws_cache.clear()
-                ws_cache[n] = torch.empty(ops.layer_workspace_bytes(n, S, D, self.attention.num_heads),
+                ws_cache[n] = torch.empty(ops.layer_workspace_bytes(n, S, D, self.attention.num_heads, masked),
                                           dtype=torch.uint8, device=dev)
-            out = self._run_eager(xc, pack, causal, return_residual, ws=ws_cache[n])
+            out = self._run_eager(xc, mc, pack, causal, return_residual, ws=ws_cache[n])
             if return_residual:
                 r_all[b0:b1].copy_(out[0])
                 y_all[b0:b1].copy_(out[1])

@@ -7,10 +7,13 @@ on ``torch.cuda.current_stream()`` and never synchronises.  Differences:
 
 * weights are nn.Linear's ``[N, K]`` layout; the reference passed a
   transposed ``[K, N]`` copy to its GEMMs (TTB:895-904).  No copy is needed here;
-* attention takes ``causal`` (the reference kernel was causal-only);
-* row masks (``mask_row`` / ``rmask`` / ``mask_out``) and the GELU epilogue
-  belong to padding support and the FFN, which are not on this path: passing
-  them raises ``NotImplementedError`` rather than silently ignoring them.
+* attention takes ``causal`` (the reference kernel was causal-only) and an
+  optional ``key_mask`` (the reference routed masked attention to SDPA with an
+  additive -inf bias, TTB:1207-1213, 1240-1253);
+* row masks (``mask_row`` / ``rmask``) are ``[M]`` bool or uint8 tensors
+  (0 = padded row), applied with the reference kernels' MASK_RESID / MASK_OUT
+  rules; ``mask_branch=True`` additionally offers the attention sublayer's own
+  rule, zeroing the product rows *before* the residual add (TTB:121-122).
 
 Argument errors raise ``ValueError``/``TypeError`` before anything is
 enqueued; a non-zero code from the library raises ``CobraError``.
@@ -65,10 +68,17 @@ def _f32_param(t: torch.Tensor, n: int, what: str) -> torch.Tensor:
     return t.to(dtype=torch.float32).contiguous()
 
 
-def _no_masks(**kw) -> None:
-    for k, v in kw.items():
-        if v not in (None, False):
-            raise NotImplementedError(f"{k}: row masks / padding are not supported on this path yet")
+def _row_mask(m: Optional[torch.Tensor], rows: int, what: str) -> Optional[torch.Tensor]:
+    """A [rows] (or [B, S] with B*S == rows) bool/uint8 device mask as a uint8 view."""
+    if m is None:
+        return None
+    _dev(m, what)
+    if m.dtype not in (torch.bool, torch.uint8):
+        raise TypeError(f"{what} must be bool or uint8, got {m.dtype}")
+    if m.numel() != rows:
+        raise ValueError(f"{what} must hold {rows} rows, got shape {tuple(m.shape)}")
+    # bool -> uint8 is a reinterpretation of the same bytes (0x00 / 0x01), not a copy.
+    return m.reshape(rows).view(torch.uint8)
 
 
 def add_ln(
@@ -84,13 +94,22 @@ def add_ln(
 ) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
     """``(resid + branch)`` then LayerNorm -> ``(new_resid | None, normed)``.
 
-    Mirrors ``_tl_add_ln`` (TTB:539-569).  The stored residual is always fp32.
+    Mirrors ``_tl_add_ln`` (TTB:539-569), including its mask rule: with a
+    ``mask_row``, the residual is multiplied by the mask whenever it is stored
+    or the output is masked, and ``mask_out`` also masks the normalised output.
+    The stored residual is always fp32.
     """
-    _no_masks(mask_row=mask_row, mask_out=mask_out)
     _dev(resid, "resid")
     if resid.dim() != 2:
         raise ValueError("resid must be [M, N]")
     M, N = resid.shape
+    mrow = _row_mask(mask_row, M, "mask_row")
+    flags = 0
+    if mrow is not None:
+        if store_resid or mask_out:
+            flags |= _lib.EPI_MASK_RESID
+        if mask_out:
+            flags |= _lib.EPI_MASK_OUT
     if branch is not None:
         _dev(branch, "branch")
         if branch.shape != resid.shape:
@@ -100,8 +119,8 @@ def add_ln(
     out_n = torch.empty((M, N), device=resid.device, dtype=torch.float16 if cast_fp16 else torch.float32)
     call(
         "cobra_ln_fwd", resid.data_ptr(), _dtype_code(resid, "resid"), _ptr(branch),
-        _dtype_code(branch, "branch") if branch is not None else 0, gw.data_ptr(), gb.data_ptr(),
-        _ptr(out_r), out_n.data_ptr(), _dtype_code(out_n, "normed"), M, N, float(eps), _stream(resid),
+        _dtype_code(branch, "branch") if branch is not None else 0, gw.data_ptr(), gb.data_ptr(), _ptr(mrow),
+        flags, _ptr(out_r), out_n.data_ptr(), _dtype_code(out_n, "normed"), M, N, float(eps), _stream(resid),
     )
     return out_r, out_n
 
@@ -114,14 +133,17 @@ def linear(
     out_fp32: bool = False,
     resid: Optional[torch.Tensor] = None,
     rmask: Optional[torch.Tensor] = None,
+    mask_branch: bool = False,
 ) -> torch.Tensor:
-    """``a @ w.T + bias (+ resid)`` with fp32 accumulate.  Mirrors ``_tl_linear`` (TTB:355-381).
+    """``a @ w.T + bias`` (GELU) ``(+ resid)`` with fp32 accumulate.  Mirrors ``_tl_linear`` (TTB:355-381).
 
     a: [M, K] fp16; w: [N, K] fp16; bias: [N]; resid: [M, N] fp16/fp32.
+    ``gelu`` is the exact erf GELU after the bias (TTB:326-328).  ``rmask``
+    multiplies ``(product + resid)`` of padded rows by 0 when there is a
+    residual (the reference kernel applies it only then, TTB:343-348); with
+    ``mask_branch=True`` it instead zeroes the padded rows' product before the
+    residual add, so those rows come out equal to ``resid``.
     """
-    if gelu:
-        raise NotImplementedError("the GELU epilogue belongs to the FFN sublayer, not on this path")
-    _no_masks(rmask=rmask)
     _dev(a, "a")
     _dev(w, "w")
     if a.dtype != torch.float16 or w.dtype != torch.float16:
@@ -135,11 +157,20 @@ def linear(
         _dev(resid, "resid")
         if resid.shape != (M, N):
             raise ValueError("resid must be [M, N]")
+    mrow = _row_mask(rmask, M, "rmask")
+    epi = _lib.EPI_GELU if gelu else 0
+    if mrow is not None:
+        if mask_branch:
+            epi |= _lib.EPI_MASK_BRANCH
+        elif resid is not None:
+            epi |= _lib.EPI_MASK_RESID
+        else:
+            mrow = None
     out = torch.empty((M, N), device=a.device, dtype=torch.float32 if out_fp32 else torch.float16)
     call(
         "cobra_linear_fwd", a.data_ptr(), w.data_ptr(), _ptr(b32), _ptr(resid),
-        _dtype_code(resid, "resid") if resid is not None else 0, out.data_ptr(), _dtype_code(out, "out"),
-        M, N, K, _stream(a),
+        _dtype_code(resid, "resid") if resid is not None else 0, _ptr(mrow), epi, out.data_ptr(),
+        _dtype_code(out, "out"), M, N, K, _stream(a),
     )
     return out
 
@@ -155,12 +186,15 @@ def linear_ln(
     norm_fp16: bool = True,
     mask_out: bool = False,
     eps: float = 1e-5,
+    mask_branch: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """``r = a @ w.T + bias + resid``; ``(r fp32, LayerNorm(r))``.  Mirrors ``_tl_linear_ln`` (TTB:465-488).
 
-    Requires N <= 128, like the reference (TTB:471).
+    Requires N <= 128, like the reference (TTB:471).  ``rmask`` multiplies the
+    padded rows of ``r`` by 0 and, with ``mask_out``, of the normalised output
+    (TTB:436-458); ``mask_branch=True`` zeroes the padded rows' product before
+    the residual add instead (the attention sublayer's rule, TTB:121-122).
     """
-    _no_masks(rmask=rmask, mask_out=mask_out)
     _dev(a, "a")
     _dev(w, "w")
     _dev(resid, "resid")
@@ -174,14 +208,31 @@ def linear_ln(
         raise ValueError("fused-LN GEMM requires N <= 128 (one workgroup owns a whole row)")
     b32 = _f32_param(bias, N, "bias")
     gw, gb = _f32_param(nw, N, "nw"), _f32_param(nb, N, "nb")
+    mrow = _row_mask(rmask, M, "rmask")
+    epi = 0
+    if mrow is not None:
+        epi |= _lib.EPI_MASK_BRANCH if mask_branch else _lib.EPI_MASK_RESID
+        if mask_out:
+            epi |= _lib.EPI_MASK_OUT
     out = torch.empty((M, N), device=a.device, dtype=torch.float32)
     normed = torch.empty((M, N), device=a.device, dtype=torch.float16 if norm_fp16 else torch.float32)
     call(
         "cobra_linear_ln_fwd", a.data_ptr(), w.data_ptr(), b32.data_ptr(), resid.data_ptr(),
-        _dtype_code(resid, "resid"), out.data_ptr(), gw.data_ptr(), gb.data_ptr(), normed.data_ptr(),
-        _dtype_code(normed, "normed"), M, N, K, float(eps), _stream(a),
+        _dtype_code(resid, "resid"), _ptr(mrow), epi, out.data_ptr(), gw.data_ptr(), gb.data_ptr(),
+        normed.data_ptr(), _dtype_code(normed, "normed"), M, N, K, float(eps), _stream(a),
     )
     return out, normed
+
+
+def mask_bits(mask: torch.Tensor) -> torch.Tensor:
+    """[B, S] bool/uint8 token mask -> packed key bits ``[B, ceil(S/64)]`` (int64 storage of u64 words)."""
+    if mask.dim() != 2:
+        raise ValueError(f"mask must be [B, S], got {tuple(mask.shape)}")
+    B, S = mask.shape
+    m = _row_mask(mask, B * S, "mask")
+    bits = torch.empty((B, (S + 63) // 64), device=mask.device, dtype=torch.int64)
+    call("cobra_mask_bits", m.data_ptr(), bits.data_ptr(), B, S, _stream(mask))
+    return bits
 
 
 def attn(
@@ -194,11 +245,14 @@ def attn(
     out_dtype: torch.dtype = torch.float16,
     cfgs=None,
     causal: bool = True,
+    key_mask: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention on packed ``qkv [B*S, 3*H*hd]`` -> ``ctx [B*S, H*hd]``.  Mirrors ``_tl_attn`` (TTB:828-854).
 
     ``cfgs`` (the reference's tile ladder) is accepted and ignored: tiles are
-    chosen inside the library from (seq_len, head_dim).
+    chosen inside the library from (seq_len, head_dim).  ``key_mask`` ([B, S]
+    bool/uint8, 0 = padded) masks keys like TTB:106-109; a query with no valid
+    key gets a zero row.
     """
     _dev(qkv, "qkv")
     if qkv.dtype != torch.float16 or out_dtype != torch.float16:
@@ -206,10 +260,15 @@ def attn(
     D = heads * head_dim
     if qkv.shape != (batch * seq_len, 3 * D):
         raise ValueError(f"qkv must be [{batch * seq_len}, {3 * D}], got {tuple(qkv.shape)}")
+    bits = None
+    if key_mask is not None:
+        if tuple(key_mask.shape) != (batch, seq_len):
+            raise ValueError(f"key_mask must be [{batch}, {seq_len}], got {tuple(key_mask.shape)}")
+        bits = mask_bits(key_mask)
     out = torch.empty((batch * seq_len, D), device=qkv.device, dtype=torch.float16)
     call(
-        "cobra_attn_fwd", qkv.data_ptr(), out.data_ptr(), batch, seq_len, heads, head_dim, float(scale),
-        1 if causal else 0, _stream(qkv),
+        "cobra_attn_fwd", qkv.data_ptr(), out.data_ptr(), _ptr(bits), batch, seq_len, heads, head_dim,
+        float(scale), 1 if causal else 0, _stream(qkv),
     )
     return out
 
@@ -218,16 +277,16 @@ PLAN_FUSED = _lib.PLAN_FUSED
 PLAN_STAGED = _lib.PLAN_STAGED
 
 
-def layer_plan(batch: int, seq_len: int, d_model: int, heads: int) -> int:
+def layer_plan(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False) -> int:
     """PLAN_FUSED (one kernel) or PLAN_STAGED for this shape (host-only query)."""
-    p = _lib.lib().cobra_layer_plan(batch, seq_len, d_model, heads)
+    p = _lib.lib().cobra_layer_plan(batch, seq_len, d_model, heads, 1 if masked else 0)
     if p < 0:
         raise ValueError(f"unsupported sublayer shape B={batch} S={seq_len} D={d_model} H={heads}")
     return int(p)
 
 
-def layer_workspace_bytes(batch: int, seq_len: int, d_model: int, heads: int) -> int:
-    n = _lib.lib().cobra_layer_workspace_bytes(batch, seq_len, d_model, heads)
+def layer_workspace_bytes(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False) -> int:
+    n = _lib.lib().cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, 1 if masked else 0)
     if n < 0:
         raise ValueError(f"unsupported sublayer shape B={batch} S={seq_len} D={d_model} H={heads}")
     return int(n)
@@ -249,14 +308,17 @@ def layer_fwd(
     causal: bool,
     eps: float = 1e-5,
     resid_out: Optional[torch.Tensor] = None,
+    valid_mask: Optional[torch.Tensor] = None,
 ) -> None:
     """Enqueue the whole sublayer into caller-provided buffers (no allocation).
 
-    x, y: [B, S, D] (same dtype); packed weights as produced by ``CobraAttentionSublayer``.
+    x, y: [B, S, D] (same dtype); packed weights as produced by ``CobraAttentionSublayer``;
+    valid_mask: optional [B, S] uint8 (0 = padded token) -- the workspace must then be
+    sized with ``masked=True``.
     """
     B, S, D = x.shape
     call(
-        "cobra_layer_fwd", x.data_ptr(), _dtype_code(x, "x"), w_qkv.data_ptr(), b_qkv.data_ptr(),
+        "cobra_layer_fwd", x.data_ptr(), _dtype_code(x, "x"), _ptr(valid_mask), w_qkv.data_ptr(), b_qkv.data_ptr(),
         w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(), ln2_w.data_ptr(),
         ln2_b.data_ptr(), y.data_ptr(), _ptr(resid_out), workspace.data_ptr(), workspace.numel(),
         B, S, D, heads, 1 if causal else 0, float(eps), _stream(x),

@@ -7,7 +7,10 @@
 // keys (j > i under causality, j >= S) are -inf, p = softmax(s) in fp32,
 // ctx_i = sum_j p_j v_j.  The [S, S] score matrix is never formed: keys are
 // visited in blocks with an online (running max / running sum) softmax in the
-// exp2 domain, normalised once at the end.
+// exp2 domain, normalised once at the end.  An optional key mask (the
+// reference's valid_token_mask, TTB:106-109) arrives as packed bits, one
+// 64-bit word per 64 keys of a sequence, produced from the [B, S] byte mask by
+// mask_bits_kernel; a query with no valid key gets a zero context row.
 //
 // CDNA4 mapping (one wave = 32 queries, v_mfma_f32_32x32x16_f16):
 //   * scores are computed transposed, S^T = K . Q^T, so the C layout gives
@@ -37,7 +40,11 @@
 //     lane needs it;
 //   * the running sum adds the fp16 probabilities the P.V product consumes
 //     (v_dot2_f32_f16 against ones, fp32 accumulation), and the max/sum
-//     exchange with lane ^ 32 uses v_permlane32_swap.
+//     exchange with lane ^ 32 uses v_permlane32_swap;
+//   * key masks: the block's validity word is a scalar load (it waits in
+//     lgkmcnt, never behind the K/V transfers in vmcnt); a block without a
+//     valid key is skipped by the whole workgroup, a fully valid one costs a
+//     compare, and only partly valid blocks mask per key.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "lds_dma.hpp"
@@ -94,9 +101,10 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 
 }  // namespace
 
-template <int HD, int NW, int BN, int ST, bool CAUSAL>
+template <int HD, int NW, int BN, int ST, bool CAUSAL, bool MASKED>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict__ qkv, f16* __restrict__ ctx,
-                                                           int S, int H, int hd, float c2, int nqb) {
+                                                           int S, int H, int hd, float c2, int nqb,
+                                                           const uint64_t* __restrict__ key_bits, int nwords) {
   constexpr int BM = 32 * NW;          // queries per workgroup
   constexpr int KS = HD / 16;          // k-steps of the QK^T product
   constexpr int ND = (HD + 31) / 32;   // 32-row blocks of d in O^T
@@ -108,6 +116,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   constexpr int LPT = NI / NW;         // spans per wave per stage
   constexpr int QPT = BM * HD * 2 / 1024 / NW;  // Q-tile spans per wave
   static_assert(HD % 16 == 0 && BN % 32 == 0, "tile geometry");
+  static_assert(BN == 32 || BN == 64 || BN == 128, "key-mask words");
+  constexpr int KW = BN > 64 ? 2 : 1;  // validity words per key block
   static_assert(NI % NW == 0 && LPT >= 1 && (NI / 2) % 1 == 0, "every wave DMAs whole spans of each stage");
   // Short-sequence launches (<= 4 waves) give the Q tile its own LDS region, so its
   // DMA overlaps the first K/V stages instead of preceding them; 8-wave launches
@@ -173,6 +183,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   for (int j = 0; j < ND; ++j) o[j] = zero16();
   float m_run = 0.f;  // running max in the exp2 domain, set by block 0
   float l_run = 0.f;  // this lane's share of the running sum
+  bool started = false;  // key masks: the running max is set by the first block with a valid key
+  const uint64_t* krow = MASKED ? key_bits + b * nwords : nullptr;
   const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 
   // Per-lane V^T read geometry (see the header): row within a 16-key step,
@@ -223,6 +235,21 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   }
   for (int n = 0; n < nblk; ++n) {
     const int kb = n * BN;
+    // Key-validity bits of keys kb .. kb+BN-1 (bit j = key kb + j); the scalar
+    // load completes under the barrier's lgkmcnt wait below.
+    uint64_t kw[KW];
+    if constexpr (MASKED) {
+      const int w0 = kb >> 6;
+      if constexpr (BN == 128) {
+        kw[0] = krow[w0];
+        kw[1] = krow[min(w0 + 1, nwords - 1)];
+        if (w0 + 1 >= nwords) kw[1] = 0;
+      } else if constexpr (BN == 64) {
+        kw[0] = krow[w0];
+      } else {
+        kw[0] = (krow[w0] >> (kb & 32)) & 0xffffffffull;
+      }
+    }
     // Blocks n+1 .. n+ST-2 may still be in flight; block n must have landed.
     const int ahead = min(ST - 2, nblk - 1 - n);
     if constexpr (ST >= 4) {
@@ -244,6 +271,18 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     }
     lds_barrier();  // block n visible to all waves; every wave is done with block n-1
     if (n + ST - 1 < nblk) issue((n + ST - 1) % ST, (n + ST - 1) * BN);
+    bool kpart = false;  // some key of the block is padded
+    if constexpr (MASKED) {
+      constexpr uint64_t kFull = BN == 32 ? 0xffffffffull : ~0ull;
+      uint64_t any = 0, all = kFull;
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        any |= kw[k];
+        all &= kw[k];
+      }
+      if (any == 0) continue;  // no valid key: the block adds nothing (uniform over the workgroup)
+      kpart = all != kFull;
+    }
     const f16* Kc = reinterpret_cast<const f16*>(smem + (n % ST) * SB);
     const f16* Vc = reinterpret_cast<const f16*>(smem + (n % ST) * SB + TB);
     // s = scores in the exp2 domain minus the running max: the accumulator
@@ -262,14 +301,20 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
       }
     }
 
-    // Masks only where a block reaches past S or, causally, past this wave's first query.
-    if (kb + BN > S || (CAUSAL && kb + BN > q0w + 1)) {
+    // Masks only where a block reaches past S, causally past this wave's first
+    // query, or holds a padded key.
+    if (kb + BN > S || (CAUSAL && kb + BN > q0w + 1) || kpart) {
+      uint64_t lw[KW];  // this lane's view: bit c = key kb + 32*(word half) + 4g + c
+#pragma unroll
+      for (int k = 0; k < KW; ++k) lw[k] = MASKED ? kw[k] >> (4 * g) : 0;
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kb + t * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= S || (CAUSAL && key > qi)) s[t][r] = kNegInf;
+          bool dead = key >= S || (CAUSAL && key > qi);
+          if constexpr (MASKED) dead = dead || !((lw[t >> 1] >> ((t & 1) * 32 + 8 * (r >> 2) + (r & 3))) & 1);
+          if (dead) s[t][r] = kNegInf;
         }
     }
     float mx = kNegInf;
@@ -278,9 +323,28 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
     mx = max_xor32(mx);  // this block's max relative to m_run
-    // Block 0 sets the running max (it holds key 0, valid for every query, so
-    // mx is finite); later blocks raise it only past the lazy threshold.
-    if (n == 0 || __builtin_amdgcn_ballot_w64(mx > kLazyRescale)) {
+    if constexpr (MASKED) {
+      // The first block with a valid key for the query sets its running max
+      // (until then the accumulators start at 0 and every probability is 0).
+      const bool live = mx != kNegInf;
+      if (__builtin_amdgcn_ballot_w64(started ? mx > kLazyRescale : live)) {
+        const float inc = started ? fmaxf(mx, 0.f) : (live ? mx : 0.f);
+        const float alpha = started ? __builtin_amdgcn_exp2f(-inc) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[t][r] -= inc;
+        m_run += inc;
+        started = started || live;
+      }
+    } else if (n == 0 || __builtin_amdgcn_ballot_w64(mx > kLazyRescale)) {
+      // Block 0 sets the running max (it holds key 0, valid for every query, so
+      // mx is finite); later blocks raise it only past the lazy threshold.
       const float inc = n == 0 ? mx : fmaxf(mx, 0.f);
       if (n != 0) {
         const float alpha = __builtin_amdgcn_exp2f(-inc);
@@ -333,7 +397,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   // Output through LDS: O^T quads into [BM][HD] rows, then whole 16-byte chunks per
   // lane, so the stores to ctx are row-contiguous.
   const float l_tot = sum_xor32(l_run);
-  const float inv = 1.0f / l_tot;
+  const float inv = MASKED ? (l_tot > 0.f ? 1.0f / l_tot : 0.f) : 1.0f / l_tot;
   lds_barrier();  // every wave is done with the last stage
 #pragma unroll
   for (int j = 0; j < ND; ++j)
@@ -364,9 +428,15 @@ static hipError_t launch_attn(const AttnArgs& a, float c2) {
   const int nqb = (a.seq_len + BM - 1) / BM;
   const int64_t grid = (int64_t)nqb * a.heads * a.batch;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL>), dim3((unsigned)grid), dim3(NW * 64), 0, a.stream,
-                     static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads, a.head_dim, c2,
-                     nqb);
+  const int nwords = (int)mask_words(a.seq_len);
+  if (a.key_bits)
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL, true>), dim3((unsigned)grid), dim3(NW * 64), 0,
+                       a.stream, static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads,
+                       a.head_dim, c2, nqb, a.key_bits, nwords);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL, false>), dim3((unsigned)grid), dim3(NW * 64), 0,
+                       a.stream, static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads,
+                       a.head_dim, c2, nqb, nullptr, nwords);
   return hipGetLastError();
 }
 
@@ -398,6 +468,31 @@ static hipError_t dispatch_hd(const AttnArgs& a, float c2) {
   if (hd <= 64) return dispatch_waves<64, CAUSAL>(a, c2);
   if (hd <= 128) return dispatch_waves<128, CAUSAL>(a, c2);
   return dispatch_waves<256, CAUSAL>(a, c2);
+}
+
+// One wave per 64-bit word: lane j reads the byte of key 64w + j (coalesced)
+// and the ballot of "valid" is the word.
+__global__ __launch_bounds__(256) void mask_bits_kernel(const uint8_t* __restrict__ mask, uint64_t* __restrict__ bits,
+                                                        int64_t total_words, int S, int nw) {
+  const int64_t word = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (word >= total_words) return;  // whole waves only
+  const int lane = threadIdx.x & 63;
+  const int64_t b = word / nw;
+  const int key = (int)(word - b * nw) * 64 + lane;
+  const bool valid = key < S && mask[b * S + key] != 0;
+  const uint64_t v = __builtin_amdgcn_ballot_w64(valid);
+  if (lane == 0) bits[word] = v;
+}
+
+hipError_t run_mask_bits(const uint8_t* mask, uint64_t* bits, int64_t batch, int seq_len, hipStream_t stream) {
+  if (!mask || !bits || batch < 0 || seq_len < 0) return hipErrorInvalidValue;
+  const int nw = (int)mask_words(seq_len);
+  const int64_t total = batch * nw;
+  if (total == 0) return hipSuccess;
+  const int64_t blocks = (total + 3) / 4;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mask_bits_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, mask, bits, total, seq_len, nw);
+  return hipGetLastError();
 }
 
 hipError_t run_attn(const AttnArgs& a) {

@@ -17,19 +17,27 @@ int64_t round256(int64_t n) { return (n + 255) & ~int64_t(255); }
 int code(hipError_t e) { return static_cast<int>(e); }
 constexpr int kBad = static_cast<int>(hipErrorInvalidValue);
 
+constexpr int kEpiAll = COBRA_EPI_GELU | COBRA_EPI_MASK_BRANCH | COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT;
+static_assert(COBRA_EPI_GELU == cobra::kEpiGelu && COBRA_EPI_MASK_BRANCH == cobra::kEpiMaskBranch &&
+                  COBRA_EPI_MASK_RESID == cobra::kEpiMaskResid && COBRA_EPI_MASK_OUT == cobra::kEpiMaskOut,
+              "ABI flag values are the kernels' own");
+
 struct LayerBuffers {
-  int64_t h_off, qkv_off, r_off, total;
+  int64_t h_off, qkv_off, r_off, bits_off, total;
 };
 
 // Workspace layout of cobra_layer_fwd: h (fp16 [T, D], later reused for the
-// attention context), qkv (fp16 [T, 3D]), and for D > 128 the fp32 residual
-// that feeds the separate LayerNorm pass.
-LayerBuffers layer_buffers(int64_t tokens, int64_t d) {
+// attention context), qkv (fp16 [T, 3D]), for D > 128 the fp32 residual that
+// feeds the separate LayerNorm pass, and with a token mask the packed key
+// bits ([B][ceil(S/64)] u64).
+LayerBuffers layer_buffers(int64_t batch, int64_t seq_len, int64_t d, bool masked) {
+  const int64_t tokens = batch * seq_len;
   LayerBuffers b{};
   b.h_off = 0;
   b.qkv_off = round256(tokens * d * 2);
   b.r_off = b.qkv_off + round256(tokens * 3 * d * 2);
-  b.total = b.r_off + (d > 128 ? round256(tokens * d * 4) : 0);
+  b.bits_off = b.r_off + (d > 128 ? round256(tokens * d * 4) : 0);
+  b.total = b.bits_off + (masked ? round256(batch * cobra::mask_words(seq_len) * 8) : 0);
   return b;
 }
 
@@ -48,9 +56,10 @@ int cobra_version(void) { return COBRA_ABI_VERSION; }
 const char* cobra_error_string(int c) { return hipGetErrorString(static_cast<hipError_t>(c)); }
 
 int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtype, const float* gamma,
-                 const float* beta, float* resid_out, void* y, int y_dtype, int64_t rows, int64_t d, float eps,
-                 void* stream) {
+                 const float* beta, const uint8_t* row_mask, int mask_flags, float* resid_out, void* y, int y_dtype,
+                 int64_t rows, int64_t d, float eps, void* stream) {
   if (!x || !y || !gamma || !beta || !is_dtype(x_dtype) || !is_dtype(y_dtype)) return kBad;
+  if ((mask_flags & ~(COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT)) != 0 || (mask_flags && !row_mask)) return kBad;
   if (branch && !is_dtype(branch_dtype)) return kBad;
   if (!aligned16(x) || !aligned16(y) || !aligned16(gamma) || !aligned16(beta) || !opt_aligned16(branch) ||
       !opt_aligned16(resid_out))
@@ -58,24 +67,32 @@ int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtyp
   if (d <= 0 || d > cobra::kLnMaxD || d % 8 != 0 || rows < 0) return kBad;
   cobra::LnArgs a{x,        x_dtype, branch, branch_dtype == kF32 ? 1 : 0, gamma, beta, resid_out, y, y_dtype,
                   rows,     (int)d,  eps,    static_cast<hipStream_t>(stream)};
+  a.row_mask = row_mask;
+  a.mask_resid = (mask_flags & COBRA_EPI_MASK_RESID) != 0;
+  a.mask_out = (mask_flags & COBRA_EPI_MASK_OUT) != 0;
   return code(cobra::run_ln(a));
 }
 
-int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype, void* c,
-                     int c_dtype, int64_t M, int64_t N, int64_t K, void* stream) {
+int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
+                     const uint8_t* row_mask, int epi, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
+                     void* stream) {
   if (!a || !w || !c || !is_dtype(c_dtype) || (resid && !is_dtype(resid_dtype))) return kBad;
+  if ((epi & ~kEpiAll) != 0 || (epi & COBRA_EPI_MASK_OUT) || ((epi & ~COBRA_EPI_GELU) && !row_mask)) return kBad;
   if (!aligned16(a) || !aligned16(w) || !aligned16(c) || !opt_aligned16(resid) || !opt_aligned16(bias)) return kBad;
   if (M < 0 || N <= 0 || K <= 0 || N > 0x7fffffff || K > 0x7fffffff) return kBad;
   cobra::GemmArgs g{a,       w,       bias,    resid,   resid_dtype, c,   c_dtype,
                     M,       (int)N,  (int)K,  nullptr, nullptr,     nullptr, kF16,
                     1e-5f,   static_cast<hipStream_t>(stream)};
+  g.row_mask = row_mask;
+  g.epi = epi;
   return code(cobra::run_gemm(g));
 }
 
 int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
-                        float* resid_out, const float* gamma, const float* beta, void* y, int y_dtype, int64_t M,
-                        int64_t N, int64_t K, float eps, void* stream) {
+                        const uint8_t* row_mask, int epi, float* resid_out, const float* gamma, const float* beta,
+                        void* y, int y_dtype, int64_t M, int64_t N, int64_t K, float eps, void* stream) {
   if (!a || !w || !gamma || !beta || !y || !is_dtype(y_dtype) || (resid && !is_dtype(resid_dtype))) return kBad;
+  if ((epi & ~kEpiAll) != 0 || ((epi & ~COBRA_EPI_GELU) && !row_mask)) return kBad;
   if (!aligned16(a) || !aligned16(w) || !aligned16(y) || !opt_aligned16(resid) || !opt_aligned16(resid_out) ||
       !opt_aligned16(bias))
     return kBad;
@@ -83,37 +100,48 @@ int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const v
   cobra::GemmArgs g{a,     w,      bias,   resid, resid_dtype, resid_out, kF32,
                     M,     (int)N, (int)K, gamma, beta,        y,         y_dtype,
                     eps,   static_cast<hipStream_t>(stream)};
+  g.row_mask = row_mask;
+  g.epi = epi;
   return code(cobra::run_gemm(g));
 }
 
-int cobra_attn_fwd(const void* qkv, void* ctx, int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim,
-                   float scale, int causal, void* stream) {
+int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int64_t seq_len, void* stream) {
+  if (!mask || !key_bits || (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
+  if (batch < 0 || seq_len < 0 || seq_len > 0x7fffffff) return kBad;
+  return code(cobra::run_mask_bits(mask, key_bits, batch, (int)seq_len, static_cast<hipStream_t>(stream)));
+}
+
+int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t batch, int64_t seq_len,
+                   int64_t heads, int64_t head_dim, float scale, int causal, void* stream) {
   if (!qkv || !ctx || !aligned16(qkv) || !aligned16(ctx)) return kBad;
+  if (key_bits && (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
   if (batch < 0 || seq_len < 0 || seq_len > 0x7fffffff || heads <= 0 || heads > 0x7fffffff || head_dim <= 0 ||
       head_dim > 256 || !(scale > 0.f))
     return kBad;
   cobra::AttnArgs a{qkv, ctx, batch, (int)seq_len, (int)heads, (int)head_dim, scale, causal ? 1 : 0,
                     static_cast<hipStream_t>(stream)};
+  a.key_bits = key_bits;
   return code(cobra::run_attn(a));
 }
 
-int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads) {
+int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked) {
   if (!layer_shape_ok(batch, seq_len, d_model, heads)) return -1;
-  return cobra::layer_small_ok(seq_len, d_model, heads) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
+  return !masked && cobra::layer_small_ok(seq_len, d_model, heads) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
 }
 
-int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads) {
-  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads);
+int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked) {
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked);
   if (plan < 0) return -1;
-  return plan == COBRA_PLAN_FUSED ? 0 : layer_buffers(batch * seq_len, d_model).total;
+  return plan == COBRA_PLAN_FUSED ? 0 : layer_buffers(batch, seq_len, d_model, masked != 0).total;
 }
 
-int cobra_layer_fwd(const void* x, int x_dtype, const void* w_qkv, const float* b_qkv, const void* w_o,
-                    const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
+int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const void* w_qkv, const float* b_qkv,
+                    const void* w_o, const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
                     const float* ln2_b, void* y, float* resid_out, void* workspace, int64_t workspace_bytes,
                     int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
                     void* stream) {
-  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads);
+  const bool masked = valid_mask != nullptr;
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked);
   if (plan < 0 || !is_dtype(x_dtype)) return kBad;
   const void* must[] = {x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y};
   for (const void* p : must)
@@ -128,17 +156,19 @@ int cobra_layer_fwd(const void* x, int x_dtype, const void* w_qkv, const float* 
                             y,     resid_out, batch, seq_len, d_model, heads, causal ? 1 : 0, eps, s};
     return code(cobra::run_layer_small(a));
   }
-  const LayerBuffers lb = layer_buffers(T, D);
+  const LayerBuffers lb = layer_buffers(batch, seq_len, D, masked);
   if (!workspace || workspace_bytes < lb.total) return kBad;
   if (T == 0) return 0;
   char* ws = static_cast<char*>(workspace);
   void* h = ws + lb.h_off;
   void* qkv = ws + lb.qkv_off;
   void* ctx = h;  // h is dead once the QKV projection has read it
+  uint64_t* bits = masked ? reinterpret_cast<uint64_t*>(ws + lb.bits_off) : nullptr;
 
   cobra::LnArgs ln1{x, x_dtype, nullptr, 0, ln1_w, ln1_b, nullptr, h, kF16, T, (int)D, eps, s};
   hipError_t e = cobra::run_ln(ln1);
   if (e != hipSuccess) return code(e);
+  if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
 
   cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kF16, qkv, kF16, T, (int)(3 * D), (int)D,
                        nullptr, nullptr, nullptr, kF16, eps, s};
@@ -146,16 +176,23 @@ int cobra_layer_fwd(const void* x, int x_dtype, const void* w_qkv, const float* 
 
   cobra::AttnArgs at{qkv, ctx, batch, (int)seq_len, (int)heads, (int)(D / heads),
                      (float)(1.0 / sqrt((double)(D / heads))), causal ? 1 : 0, s};
+  at.key_bits = bits;
   if ((e = cobra::run_attn(at)) != hipSuccess) return code(e);
 
+  // Padded query rows: the attention output is zeroed before the residual add
+  // (TTB:121-122), so r = x there.
   if (D <= 128) {
     cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, resid_out, kF32, T, (int)D, (int)D,
                         ln2_w, ln2_b, y, x_dtype, eps, s};
+    out.row_mask = valid_mask;
+    out.epi = masked ? cobra::kEpiMaskBranch : 0;
     return code(cobra::run_gemm(out));
   }
   float* r = resid_out ? resid_out : reinterpret_cast<float*>(ws + lb.r_off);
   cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, r, kF32, T, (int)D, (int)D,
                       nullptr, nullptr, nullptr, kF16, eps, s};
+  out.row_mask = valid_mask;
+  out.epi = masked ? cobra::kEpiMaskBranch : 0;
   if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
   cobra::LnArgs ln2{r, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
   return code(cobra::run_ln(ln2));

@@ -88,6 +88,10 @@ __device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
   *reinterpret_cast<f32x4*>(p + 4) = b;
 }
 
+// Exact (erf) GELU, F.gelu(approximate="none"), in the reference epilogue's
+// operation order: v * 0.5 * (1 + erf(v / sqrt(2))) (TTB:326-328).
+__device__ __forceinline__ float gelu_erf(float v) { return v * 0.5f * (1.0f + erff(v * 0.7071067811865476f)); }
+
 // Workgroup-id remap so that consecutive logical tiles land on the same XCD
 // (the hardware deals workgroups round-robin over 8 XCDs, each with its own
 // L2).  A bijection on [0, n) for any n.

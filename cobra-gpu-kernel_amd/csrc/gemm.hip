@@ -3,7 +3,11 @@
 //
 // Replaces the reference's _gemm_kernel/_tl_linear (torch_transformer_benchmark.py:283-381)
 // for the projections and _gemm_ln_kernel/_tl_linear_ln (TTB:394-488) for
-// out_proj + bias + residual -> fp32 residual -> LayerNorm.  Same ownership
+// out_proj + bias + residual -> fp32 residual -> LayerNorm.  Epilogue options
+// (kEpi* flags, in this order): exact GELU, padded rows' branch set to 0
+// (masked_fill before the residual add), residual add, padded rows' sum
+// multiplied by 0 (the reference's MASK_RESID), and in the LayerNorm epilogue
+// the padded rows' output multiplied by 0 (MASK_OUT).  Same ownership
 // invariant as the reference: every output element belongs to exactly one
 // workgroup, there is no split-K and no atomics, so results are bit-repeatable.
 //
@@ -39,13 +43,25 @@ __device__ __forceinline__ float to_f32(T v) {
   return (float)v;
 }
 
+// 1 for a valid row, 0 for a padded one.
+__device__ __forceinline__ float row_valid(const uint8_t* __restrict__ mask, int64_t m) {
+  return mask[m] != 0 ? 1.f : 0.f;
+}
+
+// The epilogue steps between the bias and the residual add.
+__device__ __forceinline__ float epi_pre_resid(float v, int epi, const uint8_t* __restrict__ mask, int64_t m) {
+  if (epi & kEpiGelu) v = gelu_erf(v);
+  if ((epi & kEpiMaskBranch) && mask[m] == 0) v = 0.f;
+  return v;
+}
+
 template <int BM, int BN, int WM, int WN, typename TR, typename TC, bool LN_EPI, typename TY>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict__ A, const f16* __restrict__ W,
                                                           const float* __restrict__ bias, const TR* __restrict__ resid,
                                                           TC* __restrict__ C, int64_t M, int N, int K,
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, TY* __restrict__ Y,
-                                                          float eps) {
+                                                          float eps, const uint8_t* __restrict__ row_mask, int epi) {
   using T = GemmTile<BM, BN, WM, WN>;
   constexpr int BK = T::BK, LDK = T::LDK, NT = T::NT;
   constexpr int GEMM_LDS = (BM + BN) * LDK * 2;
@@ -141,7 +157,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict
           const int64_t m = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
           if (m < M && n < N) {
             float v = acc[i][j][r] + bn;
+            if (epi) v = epi_pre_resid(v, epi, row_mask, m);
             if (resid) v += to_f32(resid[m * N + n]);
+            if (epi & kEpiMaskResid) v *= row_valid(row_mask, m);
             C[m * N + n] = (TC)v;
           }
         }
@@ -162,7 +180,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict
           const int row = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
           const int64_t m = m0 + row;
           float v = acc[i][j][r] + bn;
-          if (resid && m < M && col < N) v += to_f32(resid[m * N + col]);
+          if (m < M && col < N) {
+            if (epi) v = epi_pre_resid(v, epi, row_mask, m);
+            if (resid) v += to_f32(resid[m * N + col]);
+            if (epi & kEpiMaskResid) v *= row_valid(row_mask, m);
+          }
           Cs[row * LDC + col] = v;
         }
       }
@@ -203,6 +225,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict
           float o[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[e] = (v[c][e] - mean) * rstd * gamma[ch * 8 + e] + beta[ch * 8 + e];
+          if (epi & kEpiMaskOut) {
+            const float mv = row_valid(row_mask, m);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] *= mv;
+          }
           store8(Y + m * N + ch * 8, o);
         }
       }
@@ -217,7 +244,7 @@ static hipError_t launch_gemm(const GemmArgs& a) {
   hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, TR, TC, LN_EPI, TY>), dim3((unsigned)tiles), dim3(WM * WN * 64), 0,
                      a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
                      static_cast<const TR*>(a.resid), static_cast<TC*>(a.c), a.M, a.N, a.K, a.ln_gamma, a.ln_beta,
-                     static_cast<TY*>(a.ln_y), a.eps);
+                     static_cast<TY*>(a.ln_y), a.eps, a.row_mask, a.epi);
   return hipGetLastError();
 }
 
@@ -240,6 +267,9 @@ static hipError_t dispatch_ln(const GemmArgs& a) {
 hipError_t run_gemm(const GemmArgs& a) {
   if (a.M < 0 || a.N <= 0 || a.K <= 0 || a.K % 8 != 0) return hipErrorInvalidValue;
   if (!a.a || !a.w) return hipErrorInvalidValue;
+  if ((a.epi & ~(kEpiGelu | kEpiMaskBranch | kEpiMaskResid | kEpiMaskOut)) != 0) return hipErrorInvalidValue;
+  if ((a.epi & (kEpiMaskBranch | kEpiMaskResid | kEpiMaskOut)) && !a.row_mask) return hipErrorInvalidValue;
+  if ((a.epi & kEpiMaskOut) && !a.ln_gamma) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;
   const bool has_resid = a.resid != nullptr;
   if (has_resid && a.resid_dtype != kF16 && a.resid_dtype != kF32) return hipErrorInvalidValue;

@@ -20,7 +20,8 @@
 //     accumulator holds C^T: each lane owns one output row and 4 consecutive
 //     columns per register quad;
 //   * epilogue through LDS: the fp32 tile (+ bias) is staged, then written in
-//     whole-row, 16-byte-per-lane passes with the residual added on the way.
+//     whole-row, 16-byte-per-lane passes with the kEpi* options (GELU, row
+//     masks) and the residual applied on the way.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "lds_dma.hpp"
@@ -65,7 +66,8 @@ template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename 
 __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __restrict__ A, const f16* __restrict__ W,
                                                               const float* __restrict__ bias,
                                                               const TR* __restrict__ resid, TC* __restrict__ C,
-                                                              int64_t M, int N, int K) {
+                                                              int64_t M, int N, int K,
+                                                              const uint8_t* __restrict__ row_mask, int epi) {
   using T = DmaTile<BM, BN, WM, WN, ST>;
   constexpr int BK = T::BK, NT = T::NT, NW = T::NW, LPT = T::LPT;
   __shared__ __attribute__((aligned(1024))) char smem[T::LDS];
@@ -210,10 +212,23 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __rest
         const int64_t m = m0 + r;
         if (m >= M) break;
         f32x4 v = *reinterpret_cast<const f32x4*>(Cs + r * T::LDC + c4);
+        float mv = 1.f;
+        if (epi) {
+          if (epi & (kEpiMaskBranch | kEpiMaskResid)) mv = row_mask[m] != 0 ? 1.f : 0.f;
+          if (epi & kEpiGelu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+          }
+          if ((epi & kEpiMaskBranch) && mv == 0.f) v = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
         if (resid) {
           const TR* rp = resid + m * N + n;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] += to_float(rp[e]);
+        }
+        if (epi & kEpiMaskResid) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] *= mv;
         }
         TC* cp = C + m * N + n;
         if constexpr (sizeof(TC) == 4) {
@@ -236,7 +251,7 @@ static hipError_t launch_dma(const GemmArgs& a) {
   if (tiles > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WM, WN, ST, GM, TR, TC>), dim3((unsigned)tiles), dim3(WM * WN * 64), 0,
                      a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
-                     static_cast<const TR*>(a.resid), static_cast<TC*>(a.c), a.M, a.N, a.K);
+                     static_cast<const TR*>(a.resid), static_cast<TC*>(a.c), a.M, a.N, a.K, a.row_mask, a.epi);
   return hipGetLastError();
 }
 

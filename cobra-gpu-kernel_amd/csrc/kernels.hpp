@@ -11,6 +11,15 @@ namespace cobra {
 
 constexpr int kLnMaxD = 4096;  // widest row the LayerNorm kernels hold in registers
 
+// Row-mask and activation options of the GEMM epilogues (bit flags, applied
+// in this order; mask byte 0 = padded row, any other value = valid row).
+enum : int {
+  kEpiGelu = 1,        // v = gelu(v) with the exact erf form, after the bias
+  kEpiMaskBranch = 2,  // padded rows: v = 0 before the residual add (masked_fill of the branch)
+  kEpiMaskResid = 4,   // padded rows: (v + resid) * 0 -- the reference epilogue's MASK_RESID
+  kEpiMaskOut = 8,     // LayerNorm epilogue: padded rows' normalised output * 0 (MASK_OUT)
+};
+
 struct LnArgs {
   const void* x;           // [rows, d], x_dtype
   int x_dtype;
@@ -25,6 +34,9 @@ struct LnArgs {
   int d;
   float eps;
   hipStream_t stream;
+  const uint8_t* row_mask = nullptr;  // optional [rows]; 0 = padded row
+  int mask_resid = 0;      // r *= mask before the store and the statistics
+  int mask_out = 0;        // y *= mask
 };
 hipError_t run_ln(const LnArgs& a);
 
@@ -45,6 +57,8 @@ struct GemmArgs {
   int ln_y_dtype;
   float eps;
   hipStream_t stream;
+  const uint8_t* row_mask = nullptr;  // [M] when a kEpiMask* flag is set
+  int epi = 0;             // kEpi* flags
 };
 // Compute units of the current device (cached after the first call).
 inline int compute_units() {
@@ -76,8 +90,13 @@ struct AttnArgs {
   float scale;             // softmax scale (head_dim ** -0.5 in the layer)
   int causal;
   hipStream_t stream;
+  const uint64_t* key_bits = nullptr;  // optional [batch][ceil(S/64)]: bit j of word w = key 64w+j valid
 };
 hipError_t run_attn(const AttnArgs& a);
+
+// mask [batch, S] bytes (0 = padded) -> key_bits [batch][ceil(S/64)] (attn.hip).
+hipError_t run_mask_bits(const uint8_t* mask, uint64_t* bits, int64_t batch, int seq_len, hipStream_t stream);
+inline int64_t mask_words(int64_t seq_len) { return (seq_len + 63) / 64; }
 
 // Whole sublayer in one kernel (layer_small.hip).
 struct SmallLayerArgs {

@@ -1,9 +1,12 @@
-// Row LayerNorm with optional residual branch:  r = x (+ branch);  y = LN(r).
+// Row LayerNorm with optional residual branch and row mask:
+//   r = (x (+ branch)) (* m);  y = LN(r) (* m)
 //
 // Replaces the reference's _add_ln_kernel / _tl_add_ln
 // (torch_transformer_benchmark.py:491-569): two-pass fp32 statistics over the
 // row held in registers (mean, then centred biased variance, /N), eps inside
-// the square root, affine, cast on store.
+// the square root, affine, cast on store.  The row mask m (0 for a padded row,
+// 1 otherwise) multiplies the residual (MASK_RESID) and/or the output
+// (MASK_OUT) as the reference kernel does (TTB:511-534).
 //
 // Layout: LPR lanes own one row, each lane holds NCH chunks of 8 consecutive
 // elements (16 B of fp16, 32 B of fp32), so every global access is a full
@@ -17,7 +20,9 @@ template <typename TX, typename TY, int LPR, int NCH>
 __global__ __launch_bounds__(256) void ln_rows_kernel(const TX* __restrict__ x, const void* __restrict__ branch,
                                                       int branch_f32, const float* __restrict__ gamma,
                                                       const float* __restrict__ beta, float* __restrict__ resid_out,
-                                                      TY* __restrict__ y, int64_t rows, int d, float eps) {
+                                                      TY* __restrict__ y, int64_t rows, int d, float eps,
+                                                      const uint8_t* __restrict__ row_mask, int mask_resid,
+                                                      int mask_out) {
   constexpr int RPW = 64 / LPR;  // rows per wave
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -26,6 +31,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const TX* __restrict__ x, 
   const bool active = row < rows;
   const int nch = d >> 3;
   const int64_t base = row * d;
+  const float mv = (row_mask && active) ? (row_mask[row] != 0 ? 1.f : 0.f) : 1.f;
 
   float v[NCH][8];
   float s = 0.f;
@@ -42,6 +48,10 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const TX* __restrict__ x, 
           load8(static_cast<const f16*>(branch) + base + ch * 8, bv);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[c][i] += bv[i];
+      }
+      if (mask_resid) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[c][i] *= mv;
       }
     } else {
 #pragma unroll
@@ -80,6 +90,10 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const TX* __restrict__ x, 
       o[i] = (v[c][i] - mean) * rstd * g0[i] + b0[i];
       o[i + 4] = (v[c][i + 4] - mean) * rstd * g1[i] + b1[i];
     }
+    if (mask_out) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] *= mv;
+    }
     store8(y + base + ch * 8, o);
   }
 }
@@ -90,7 +104,8 @@ static hipError_t launch_ln(const LnArgs& a) {
   const int64_t blocks = (a.rows + RPB - 1) / RPB;
   hipLaunchKernelGGL((ln_rows_kernel<TX, TY, LPR, NCH>), dim3((unsigned)blocks), dim3(256), 0, a.stream,
                      static_cast<const TX*>(a.x), a.branch, a.branch_f32, a.gamma, a.beta, a.resid_out,
-                     static_cast<TY*>(a.y), a.rows, a.d, a.eps);
+                     static_cast<TY*>(a.y), a.rows, a.d, a.eps, a.row_mask, a.row_mask ? a.mask_resid : 0,
+                     a.row_mask ? a.mask_out : 0);
   return hipGetLastError();
 }
 

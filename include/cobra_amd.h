@@ -27,9 +27,27 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 1
+#define COBRA_ABI_VERSION 2
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
+
+/*
+ * Epilogue / row-mask flags (bit set), applied in this order.  A row mask is
+ * one byte per row: 0 = padded row, any other value = valid row.
+ *   COBRA_EPI_GELU        v = gelu(v), exact erf form, after the bias
+ *                         (the reference GEMM's GELU, TTB:326-328);
+ *   COBRA_EPI_MASK_BRANCH padded rows: v = 0 before the residual add (the
+ *                         attention output's masked_fill, TTB:121-122);
+ *   COBRA_EPI_MASK_RESID  padded rows: (v + resid) * 0, also the stored
+ *                         residual (the reference's MASK_RESID, TTB:346-348, 511-516);
+ *   COBRA_EPI_MASK_OUT    padded rows: LayerNorm output * 0 (MASK_OUT, TTB:533-534).
+ */
+enum {
+  COBRA_EPI_GELU = 1,
+  COBRA_EPI_MASK_BRANCH = 2,
+  COBRA_EPI_MASK_RESID = 4,
+  COBRA_EPI_MASK_OUT = 8
+};
 
 /* ABI version of the loaded library (COBRA_ABI_VERSION it was built with). */
 int cobra_version(void);
@@ -38,50 +56,69 @@ int cobra_version(void);
 const char* cobra_error_string(int code);
 
 /*
- * Row LayerNorm with optional residual branch:
- *     r = x + branch (branch optional);  resid_out = r (optional, fp32);
+ * Row LayerNorm with optional residual branch and row mask:
+ *     r = x + branch (branch optional);  r *= m (COBRA_EPI_MASK_RESID);
+ *     resid_out = r (optional, fp32);
  *     y = (r - mean(r)) * rsqrt(var(r) + eps) * gamma + beta     (biased var)
- * x, branch, y: [rows, d]; gamma, beta: [d] fp32.  d % 8 == 0, d <= 4096.
- * Replaces _tl_add_ln / _add_ln_kernel (TTB:539-569, 491-535); row masks of
- * the reference (MASK_RESID / MASK_OUT) are not part of this entry point.
+ *     y *= m (COBRA_EPI_MASK_OUT)
+ * x, branch, y: [rows, d]; gamma, beta: [d] fp32; row_mask: [rows] bytes
+ * (required when mask_flags != 0; only the two flags above are accepted).
+ * d % 8 == 0, d <= 4096.  Replaces _tl_add_ln / _add_ln_kernel
+ * (TTB:539-569, 491-535).
  */
 int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtype, const float* gamma,
-                 const float* beta, float* resid_out, void* y, int y_dtype, int64_t rows, int64_t d, float eps,
-                 void* stream);
+                 const float* beta, const uint8_t* row_mask, int mask_flags, float* resid_out, void* y, int y_dtype,
+                 int64_t rows, int64_t d, float eps, void* stream);
 
 /*
  * Projection GEMM with fused epilogue:
- *     c = a . w^T + bias (+ resid)
+ *     v = a . w^T + bias;  then the epi flags GELU, MASK_BRANCH;  v += resid;
+ *     then MASK_RESID;  c = v
  * a: [M, K] fp16, w: [N, K] fp16 (nn.Linear weight layout), bias: [N] fp32
- * (optional), resid: [M, N] (optional), c: [M, N] in c_dtype.  fp32 accumulate.
- * K % 8 == 0.  Replaces _tl_linear / _gemm_kernel (TTB:355-381, 283-353)
- * without the GELU and row-mask options (FFN and padding are not on this path).
+ * (optional), resid: [M, N] (optional), row_mask: [M] bytes (required by the
+ * mask flags), c: [M, N] in c_dtype.  fp32 accumulate and epilogue.
+ * K % 8 == 0; COBRA_EPI_MASK_OUT is rejected (no LayerNorm here).  Replaces
+ * _tl_linear / _gemm_kernel (TTB:355-381, 283-353).
  */
-int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype, void* c,
-                     int c_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
+                     const uint8_t* row_mask, int epi, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
+                     void* stream);
 
 /*
  * Projection GEMM + residual + LayerNorm over whole rows:
- *     r = a . w^T + bias + resid;  resid_out = r (optional, fp32);
- *     y = LayerNorm(r) * gamma + beta
+ *     r = a . w^T + bias (GELU, MASK_BRANCH) + resid (MASK_RESID);
+ *     resid_out = r (optional, fp32);  y = LayerNorm(r) * gamma + beta (MASK_OUT)
  * Shapes as cobra_linear_fwd; requires N <= 128 (one workgroup owns a row) and
  * N % 8 == 0.  Replaces _tl_linear_ln / _gemm_ln_kernel (TTB:465-488, 394-463).
  */
 int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
-                        float* resid_out, const float* gamma, const float* beta, void* y, int y_dtype, int64_t M,
-                        int64_t N, int64_t K, float eps, void* stream);
+                        const uint8_t* row_mask, int epi, float* resid_out, const float* gamma, const float* beta,
+                        void* y, int y_dtype, int64_t M, int64_t N, int64_t K, float eps, void* stream);
+
+/*
+ * Token mask -> packed key bits for cobra_attn_fwd:
+ *     mask: [batch, seq_len] bytes (0 = padded token);
+ *     key_bits: [batch][ceil(seq_len / 64)] uint64, 8-byte aligned; bit j of
+ *     word w is set iff token 64 w + j exists and is valid.
+ * The reference builds an additive -inf bias from the mask for SDPA instead
+ * (TTB:1207-1213); the bits are 1/32 of that tensor's size.
+ */
+int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int64_t seq_len, void* stream);
 
 /*
  * Multi-head attention on a packed projection buffer:
  *     qkv: [batch*seq_len, 3*D] fp16 with column blocks q | k | v, each split
  *          into `heads` contiguous slices of head_dim (D = heads*head_dim);
  *     ctx: [batch*seq_len, D] fp16, ctx_i = softmax((q_i k^T) * scale) v per head.
- * causal != 0 masks keys j > i.  head_dim % 8 == 0, head_dim <= 256.
+ * causal != 0 masks keys j > i; key_bits (optional, from cobra_mask_bits)
+ * masks padded keys (TTB:106-109).  A query left with no valid key gets a
+ * zero row (the reference's softmax would give NaN there; the sublayer zeroes
+ * such rows anyway).  head_dim % 8 == 0, head_dim <= 256.
  * Replaces _tl_attn / _attn_kernel (TTB:828-854, 572-649; causal only there)
- * and the SDPA call used for non-causal attention (TTB:1240-1253).
+ * and the SDPA call used for non-causal and masked attention (TTB:1240-1253).
  */
-int cobra_attn_fwd(const void* qkv, void* ctx, int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim,
-                   float scale, int causal, void* stream);
+int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t batch, int64_t seq_len,
+                   int64_t heads, int64_t head_dim, float scale, int causal, void* stream);
 
 /* Execution plans of cobra_layer_fwd. */
 enum {
@@ -91,20 +128,25 @@ enum {
 
 /*
  * Which plan cobra_layer_fwd runs for this shape, or -1 if the shape is not
- * supported.  FUSED covers seq_len <= 128 with d_model 128 (head_dim 32 or
- * 64), 64 (32, 64) or 96 (32).  Host-only: no device work.  The reference's
+ * supported.  FUSED covers unmasked calls with seq_len <= 128 and d_model 128
+ * (head_dim 32 or 64), 64 (32, 64) or 96 (32); masked != 0 (a token mask will
+ * be passed) selects STAGED.  Host-only: no device work.  The reference's
  * counterpart is the gate set of UserOptimizedTransformer._prepare
  * (TTB:1030-1071).
  */
-int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads);
+int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked);
 
 /* Device workspace (bytes) cobra_layer_fwd needs for this shape (0 for FUSED). */
-int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads);
+int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked);
 
 /*
  * The whole attention sublayer (TTB:141-142 with TTB:88-123):
  *     h = LN1(x);  [q|k|v] = h . w_qkv^T + b_qkv;  c = MHA(q, k, v)
  *     r = x + (c . w_o^T + b_o);   y = LN2(r)
+ * valid_mask (optional): [batch, seq_len] bytes, 0 = padded token.  Padded
+ * keys are masked in the attention (TTB:106-109) and padded rows get a zero
+ * attention output, r = x (TTB:121-122); the workspace must then be sized
+ * with masked = 1.
  * x, y: [batch*seq_len, d_model] in x_dtype; w_qkv: [3*d_model, d_model] fp16
  * (rows: q_proj, k_proj, v_proj weights, in that order); b_qkv: [3*d_model]
  * fp32; w_o: [d_model, d_model] fp16; b_o and the LayerNorm parameters fp32.
@@ -113,8 +155,8 @@ int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_mo
  * Replaces the attention half of UserOptimizedTransformer._run_fused
  * (TTB:1216-1268), which is what its CUDA graph replays (TTB:1331-1360).
  */
-int cobra_layer_fwd(const void* x, int x_dtype, const void* w_qkv, const float* b_qkv, const void* w_o,
-                    const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
+int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const void* w_qkv, const float* b_qkv,
+                    const void* w_o, const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
                     const float* ln2_b, void* y, float* resid_out, void* workspace, int64_t workspace_bytes,
                     int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
                     void* stream);

@@ -125,12 +125,15 @@ def oracle_forward(
     causal: bool = False,
     block_q: Optional[int] = None,
     return_residual: bool = False,
+    valid_token_mask: Optional[torch.Tensor] = None,
 ):
     """fp32 oracle output for ``x`` (any dtype / device); TF32 disabled."""
     prev = torch.backends.cuda.matmul.allow_tf32
     torch.backends.cuda.matmul.allow_tf32 = False
+    if valid_token_mask is not None:
+        valid_token_mask = valid_token_mask.to(x.device, torch.bool)
     try:
         with torch.inference_mode():
-            return layer(x.float(), None, causal, return_residual, block_q)
+            return layer(x.float(), valid_token_mask, causal, return_residual, block_q)
     finally:
         torch.backends.cuda.matmul.allow_tf32 = prev

@@ -30,11 +30,12 @@ def build_pair(d_model: int, heads: int, seed: int = 0, dtype: torch.dtype = tor
     return ref, mod
 
 
-def oracle_on(ref, x: torch.Tensor, causal: bool, device, block_q=None, return_residual=False):
+def oracle_on(ref, x: torch.Tensor, causal: bool, device, block_q=None, return_residual=False, mask=None):
     """Run the fp32 oracle on ``device`` (CPU for small cases, the GPU for big ones)."""
     layer = ref.to(device)
     try:
-        out = oracle_forward(layer, x.to(device), causal=causal, block_q=block_q, return_residual=return_residual)
+        out = oracle_forward(layer, x.to(device), causal=causal, block_q=block_q, return_residual=return_residual,
+                             valid_token_mask=mask)
     finally:
         ref.to("cpu")
     if return_residual:

@@ -340,9 +340,9 @@ def test_invalid_shapes_raise():
     qkv = torch.zeros(16, 3 * 3 * 264, device=DEV, dtype=torch.float16)
     with pytest.raises(CobraError):
         ops.attn(qkv, 1, 16, 3, 264, 0.1)  # head_dim > 256
-    with pytest.raises(NotImplementedError):
-        _, mod = build_pair(128, 4)
-        x = torch.zeros(1, 8, 128, device=DEV, dtype=torch.float16)
-        m = torch.ones(1, 8, dtype=torch.bool, device=DEV)
-        m[0, 5:] = False
-        mod(x, m)
+    _, mod = build_pair(128, 4)
+    x = torch.zeros(2, 8, 128, device=DEV, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        mod(x, torch.ones(2, 7, dtype=torch.bool, device=DEV))  # mask shape
+    with pytest.raises(TypeError):
+        mod(x, torch.ones(2, 8, dtype=torch.float32, device=DEV))  # mask dtype

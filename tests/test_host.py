@@ -37,12 +37,21 @@ def test_argument_validation_rejects_before_any_launch():
     from cobra_amd import _lib
 
     lib = _lib.lib()
-    bad = lib.cobra_ln_fwd(None, 0, None, 0, None, None, None, None, 0, 8, 128, 1e-5, None)
+    bad = lib.cobra_ln_fwd(None, 0, None, 0, None, None, None, 0, None, None, 0, 8, 128, 1e-5, None)
     assert bad != 0
-    assert lib.cobra_attn_fwd(16, 16, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
-    assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10) == -1      # head_dim 12
-    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16) > 0     # staged plan (head_dim 8)
-    assert lib.cobra_layer_plan(2, 16, 128, 4) == _lib.PLAN_FUSED
+    # a mask flag without a mask, an unknown flag
+    assert lib.cobra_ln_fwd(256, 0, None, 0, 256, 256, None, _lib.EPI_MASK_OUT, None, 256, 0, 8, 128, 1e-5,
+                            None) != 0
+    assert lib.cobra_linear_fwd(256, 256, None, None, 0, 256, 64, 256, 0, 8, 8, 8, None) != 0
+    assert lib.cobra_linear_fwd(256, 256, None, None, 0, 256, _lib.EPI_MASK_OUT, 256, 0, 8, 8, 8, None) != 0
+    assert lib.cobra_linear_fwd(256, 256, None, None, 0, None, _lib.EPI_MASK_RESID, 256, 0, 8, 8, 8, None) != 0
+    assert lib.cobra_attn_fwd(16, 16, None, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
+    assert lib.cobra_attn_fwd(256, 256, 12, 1, 4, 1, 16, 0.1, 0, None) != 0  # misaligned key bits
+    assert lib.cobra_mask_bits(256, 12, 1, 4, None) != 0                   # misaligned key bits
+    assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10, 0) == -1      # head_dim 12
+    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0) > 0     # staged plan (head_dim 8)
+    assert lib.cobra_layer_plan(2, 16, 128, 4, 0) == _lib.PLAN_FUSED
+    assert lib.cobra_layer_plan(2, 16, 128, 4, 1) == _lib.PLAN_STAGED  # token masks run staged
 
 
 def test_workspace_size_formula():
@@ -54,6 +63,10 @@ def test_workspace_size_formula():
     assert ops.layer_workspace_bytes(64, 128, 128, 16) == 8192 * 128 * 2 + 8192 * 384 * 2
     t, d = 32 * 100000, 1024
     assert ops.layer_workspace_bytes(32, 100000, 1024, 16) == t * d * 2 + t * 3 * d * 2 + t * d * 4
+    # a token mask adds the packed key bits, [B][ceil(S/64)] u64, 256-B aligned
+    bits = -(-(32 * 1563 * 8) // 256) * 256
+    assert ops.layer_workspace_bytes(32, 100000, 1024, 16, masked=True) == t * d * 2 + t * 3 * d * 2 + t * d * 4 + bits
+    assert ops.layer_workspace_bytes(64, 128, 128, 4, masked=True) == 8192 * 128 * 2 + 8192 * 384 * 2 + 1024
 
 
 def test_plan_selection_per_config():
@@ -98,8 +111,10 @@ def test_ops_reject_host_tensors():
 
     with pytest.raises(ValueError, match="device"):
         ops.linear(torch.zeros(4, 8, dtype=torch.float16), torch.zeros(8, 8, dtype=torch.float16), None)
-    with pytest.raises(NotImplementedError):
-        ops.linear(torch.zeros(4, 8), torch.zeros(8, 8), None, gelu=True)
+    with pytest.raises(ValueError, match="device"):
+        ops.linear(torch.zeros(4, 8, dtype=torch.float16), torch.zeros(8, 8, dtype=torch.float16), None, gelu=True)
+    with pytest.raises(ValueError, match="device"):
+        ops.mask_bits(torch.ones(2, 8, dtype=torch.bool))
 
 
 def test_product_never_imports_the_oracle():

@@ -235,9 +235,92 @@ def test_plumbing_config_runs_on_cpu():
     assert abs(y.mean().item()) < 1e-5
 
 
+def _ragged_mask(b, s, seed=0, left_aligned=False):
+    """[b, s] bool: each sequence has 1..s valid tokens, left-aligned (the
+    reference harness's padding, TTB:1602-1612) or scattered."""
+    g = torch.Generator().manual_seed(seed)
+    if left_aligned:
+        lengths = torch.randint(1, s + 1, (b,), generator=g)
+        return torch.arange(s)[None, :] < lengths[:, None]
+    m = torch.rand(b, s, generator=g) < 0.6
+    m[:, 0] = True  # at least one valid token per sequence
+    return m
+
+
+def _key_mask_mismatch(layer, x, mask, causal):
+    """Oracle attention under a token mask vs torch's multi-head attention with
+    key_padding_mask (an independent implementation), on the valid query rows;
+    plus the largest magnitude on the padded rows, which must be exactly 0."""
+    att = layer.attention
+    b, s, d = x.shape
+    with torch.no_grad():
+        h_in = layer.norm1(x)
+        ours = att(h_in, mask, causal)
+        w_in = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight])
+        b_in = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias])
+        t = h_in.transpose(0, 1)
+        ref, _ = F.multi_head_attention_forward(
+            t, t, t, d, att.num_heads, w_in, b_in, None, None, False, 0.0,
+            att.out_proj.weight, att.out_proj.bias, training=False, need_weights=False,
+            key_padding_mask=~mask, attn_mask=torch.ones(s, s, dtype=torch.bool).triu(1) if causal else None,
+        )
+        ref = ref.transpose(0, 1)
+    valid_err = (ours - ref)[mask].abs().max().item()
+    padded = ours[~mask].abs().max().item() if (~mask).any() else 0.0
+    return valid_err, padded
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("left_aligned", [False, True])
+def test_key_mask_matches_library_mha(causal, left_aligned):
+    """Padded keys get -inf (TTB:106-109), padded rows a zero output (TTB:121-122)."""
+    layer = _layer64(16, 4)
+    x = torch.randn(4, 9, 16, dtype=torch.float64)
+    mask = _ragged_mask(4, 9, seed=1, left_aligned=left_aligned)
+    valid_err, padded = _key_mask_mismatch(layer, x, mask, causal)
+    assert valid_err < SOFTMAX_TOL
+    assert padded == 0.0
+
+
+def _compaction_mismatch(layer, x, mask):
+    """Non-causal: a sequence's valid rows equal the sublayer run on its valid
+    tokens alone (padded keys are as good as absent); padded rows equal
+    LN2(x), since their attention output is zero."""
+    worst = 0.0
+    with torch.no_grad():
+        y = layer(x, mask)
+        for bi in range(x.shape[0]):
+            keep = mask[bi]
+            alone = layer(x[bi : bi + 1, keep])
+            worst = max(worst, (y[bi, keep] - alone[0]).abs().max().item())
+            if (~keep).any():
+                worst = max(worst, (y[bi, ~keep] - layer.norm2(x[bi, ~keep])).abs().max().item())
+    return worst
+
+
+def test_key_mask_equals_dropping_padded_tokens():
+    layer = _layer64(16, 4)
+    x = torch.randn(5, 11, 16, dtype=torch.float64)
+    assert _compaction_mismatch(layer, x, _ragged_mask(5, 11, seed=2)) < SOFTMAX_TOL
+
+
+def test_left_padding_is_a_no_op_for_valid_rows_under_causality():
+    """The reference's elision argument (TTB:1110-1115): with left-aligned
+    padding a valid causal query only sees valid keys, so its row equals the
+    unmasked causal row."""
+    layer = _layer64(16, 4)
+    x = torch.randn(4, 10, 16, dtype=torch.float64)
+    mask = _ragged_mask(4, 10, seed=3, left_aligned=True)
+    with torch.no_grad():
+        masked = layer(x, mask, causal=True)
+        plain = layer(x, None, causal=True)
+    assert (masked - plain)[mask].abs().max().item() < SOFTMAX_TOL
+
+
 @pytest.mark.parametrize(
     "mistake",
-    ["no_v_bias", "scale_sqrt_d", "heads_interleaved", "softmax_axis", "causal_lower", "no_residual", "unbiased_var"],
+    ["no_v_bias", "scale_sqrt_d", "heads_interleaved", "softmax_axis", "causal_lower", "no_residual", "unbiased_var",
+     "mask_on_queries", "no_output_zeroing"],
 )
 def test_planted_mistakes_are_caught(mistake, monkeypatch):
     """Each mistake is planted in the oracle (CPU only); some check above must fail."""
@@ -276,8 +359,30 @@ def test_planted_mistakes_are_caught(mistake, monkeypatch):
                 )
             ),
         )
+    elif mistake == "mask_on_queries":
+        orig_pv = L.OracleSelfAttention._probs_times_v
+
+        def rows_masked(self, q, k, v, q0, m, causal, od):
+            # masks score rows (queries) instead of columns (keys)
+            if m is None:
+                return orig_pv(self, q, k, v, q0, m, causal, od)
+            out = orig_pv(self, q, k, v, q0, None, causal, od)
+            return out.masked_fill(~m[:, None, q0 : q0 + q.shape[-2], None], 0)
+
+        monkeypatch.setattr(L.OracleSelfAttention, "_probs_times_v", rows_masked)
+    elif mistake == "no_output_zeroing":
+        orig_fwd = L.OracleSelfAttention.forward
+        monkeypatch.setattr(
+            L.OracleSelfAttention, "forward",
+            lambda self, x, m=None, causal=False, block_q=None: orig_fwd(self, x, m, causal, block_q)
+            + (0.0 if m is None else (~m[..., None]).to(x.dtype) * self.out_proj.bias),
+        )
     caught = False
-    if mistake in ("no_v_bias", "scale_sqrt_d", "heads_interleaved", "softmax_axis"):
+    if mistake in ("mask_on_queries", "no_output_zeroing"):
+        mask = _ragged_mask(2, 6, seed=4)
+        valid_err, padded = _key_mask_mismatch(layer, x, mask, False)
+        caught = valid_err > 1e-3 or padded > 1e-3
+    elif mistake in ("no_v_bias", "scale_sqrt_d", "heads_interleaved", "softmax_axis"):
         caught = _mha_mismatch(layer, x, False) > 1e-3
     elif mistake == "causal_lower":
         caught = _mha_mismatch(layer, x, True) > 1e-3
