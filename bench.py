@@ -126,21 +126,30 @@ def roofline(name, flops, nbytes, ms, peak_tflops=PEAK_FP16_TFLOPS, peak_gbs=PEA
 
 
 def measured_peaks(dev):
+    """Sustained fp16 GEMM and copy rates of this box, for the "% of measured peak" figures.
+
+    The GEMM is 8192^3 through torch (hipBLASLt) in the layout every projection
+    on the path uses (A [M, K] row-major times W^T, W [N, K] row-major), on
+    N(0,1) data, after ~0.2 s of warm-up; median of five 20-launch runs.  A cold
+    10-launch NN measurement reads ~30 % lower on MI355X (clocks ramp, NN is a
+    slower layout), which would flatter every fraction derived from it.
+    """
     a = torch.randn(8192, 8192, device=dev, dtype=torch.float16)
-    b = torch.randn(8192, 8192, device=dev, dtype=torch.float16)
-    for _ in range(3):
-        a @ b
-    ms = event_ms(lambda: a @ b, 10)
+    w = torch.randn(8192, 8192, device=dev, dtype=torch.float16)
+    fn = lambda: torch.matmul(a, w.t())  # noqa: E731
+    event_ms(fn, 150)
+    ms = statistics.median([event_ms(fn, 20) for _ in range(5)])
     gemm = 2 * 8192 ** 3 / (ms / 1e3) / 1e12
-    del a, b
+    del a, w
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
-    dst.copy_(src)
-    ms = event_ms(lambda: dst.copy_(src), 10)
+    event_ms(lambda: dst.copy_(src), 10)
+    ms = statistics.median([event_ms(lambda: dst.copy_(src), 10) for _ in range(3)])
     bw = 2 * (1 << 30) / (ms / 1e3) / 1e9
     del src, dst
     torch.cuda.empty_cache()
-    return {"fp16_gemm_8192_tflops": gemm, "device_copy_gbs": bw}
+    return {"fp16_gemm_8192_tflops": gemm, "device_copy_gbs": bw,
+            "method": "torch.matmul(A, W.t()) 8192^3 fp16 N(0,1), warm, median of 5x20; 1 GiB device copy, median of 3x10"}
 
 
 def graph_floor_us(iters=500):
@@ -346,12 +355,18 @@ def main() -> int:
     }
     log(f"[bench] base: {ms * 1e3:.2f} us/forward, {tflops:.2f} TFLOP/s; kernel {k_ms * 1e3:.2f} us; "
         f"graph replay {g_ms * 1e3:.2f} us")
-    line["measured_peaks"] = measured_peaks(dev)
+    peaks = line["measured_peaks"] = measured_peaks(dev)
+    line["measured_mfma_frac"] = tflops / peaks["fp16_gemm_8192_tflops"]
+    line["measured_hbm_frac"] = line["hbm_gbs"] / peaks["device_copy_gbs"]
     if not args.no_sweep:
         line["sweep"] = sweep(dev)
+        for v in line["sweep"].values():
+            v["measured_mfma_frac"] = v["tflops_in_graph"] / peaks["fp16_gemm_8192_tflops"]
+            v["measured_hbm_frac"] = v["hbm_gbs_in_graph"] / peaks["device_copy_gbs"]
     if not args.no_long:
         try:
             line["long"] = bench_long(dev)
+            line["long"]["measured_mfma_frac"] = line["long"]["tflops"] / peaks["fp16_gemm_8192_tflops"]
             log(f"[bench] long: {line['long']['ms_per_step']:.1f} ms/forward")
         except torch.cuda.OutOfMemoryError as e:
             line["long"] = {"error": f"OOM: {e}"}

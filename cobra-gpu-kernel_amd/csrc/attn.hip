@@ -81,17 +81,6 @@ __device__ __forceinline__ int swz(int row) {
 
 constexpr float kLazyRescale = 8.0f;  // log2 units
 
-// max(v, v of lane ^ 32): v_permlane32_swap exchanges the two 32-lane halves
-// on the vector ALU (no LDS round trip, unlike a bpermute shuffle).
-__device__ __forceinline__ float max_xor32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float sum_xor32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 __device__ __forceinline__ f32x16 splat16(float v) {
   f32x16 r;
 #pragma unroll

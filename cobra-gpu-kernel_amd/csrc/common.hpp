@@ -47,12 +47,45 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// Cross-lane exchanges on the vector ALU (no LDS round trip, unlike the
+// ds_bpermute behind __shfl_xor).  v_permlane32_swap / v_permlane16_swap
+// exchange 32- / 16-lane halves of two registers; passing the same register
+// twice yields, in the two results, the value of this lane and of lane ^ 32
+// (^ 16), in an order that depends on the half -- so the sum or max below is
+// the same bitwise in both lanes of a pair.
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// v of another lane of the same 16-lane row, chosen by a DPP control word.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 // Sum over aligned groups of W lanes (W a power of two <= 64); every lane of
-// the group receives the group total.  All 64 lanes must execute it.
+// the group receives the same group total.  All 64 lanes must execute it.
+// Butterfly on DPP lane swizzles: lane ^ 1 and lane ^ 2 (quad_perm), the
+// other quad of an 8-lane group (row_half_mirror), the other half of a 16-lane
+// row (row_mirror), then lane ^ 16 and lane ^ 32.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  if constexpr (W >= 2) v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
+  if constexpr (W >= 16) v += dpp_f32<0x140>(v); // row_mirror
+  if constexpr (W >= 32) v = sum_xor16(v);
+  if constexpr (W >= 64) v = sum_xor32(v);
   return v;
 }
 

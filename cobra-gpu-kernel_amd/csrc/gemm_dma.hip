@@ -255,16 +255,51 @@ static hipError_t launch_dma(const GemmArgs& a) {
   return hipGetLastError();
 }
 
-// Tile choice (measured on MI355X): 128 x 128 tiles with two stages (64 KB of
-// LDS, 169 VGPRs) run two workgroups per CU, whose barriers and DMA waits
-// interleave -- the best choice for every shape measured except very large
-// fp16-output products (>= 4 rounds of 256 x 256 tiles), where 256 x 256 tiles
-// (128 x 128 per wave, the least LDS traffic per MFMA) are ~5-8 % faster.
+// Tile choice.  Candidates (measured on MI355X, TFLOP/s at 8192^3 in brackets):
+//   256 x 256, 8 waves of 64 x 128   [1096]  one workgroup per CU
+//   256 x 192, 8 waves of 64 x 96    [ 980]
+//   256 x 128, 8 waves of 64 x 64    [ 951]
+//   128 x 128, 4 waves of 64 x 64    [ 932]  two workgroups per CU
+// Bigger tiles move fewer bytes through LDS and L2 per MFMA, but a grid that
+// ends in a partly filled round wastes CUs.  The estimate below is the number
+// of rounds of tiles times the time of one round (tile area / relative
+// efficiency); it picks 256 x 192 for 8192 x 3072 x 1024 (2 full rounds; +10 %
+// over 128 x 128), 256 x 128 for 8192 x 1024 x 1024 (+6 %) and 256 x 256 for
+// the 3.2 M-row projections (+13-16 %).
+struct TileCand {
+  int bm, bn, per_cu;  // tile and workgroups resident per CU
+  double eff;          // relative throughput of a full round
+};
+constexpr TileCand kTiles[] = {{256, 256, 1, 1.00}, {256, 192, 1, 0.90}, {256, 128, 1, 0.87}, {128, 128, 2, 0.85}};
+
+static int pick_tile(int64_t M, int N) {
+  const int64_t cus = compute_units();
+  int best = 0;
+  double best_t = 1e300;
+  for (int i = 0; i < (int)(sizeof(kTiles) / sizeof(kTiles[0])); ++i) {
+    const TileCand& c = kTiles[i];
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * (int64_t)((N + c.bn - 1) / c.bn);
+    const int64_t slots = cus * c.per_cu;
+    const int64_t rounds = (tiles + slots - 1) / slots;
+    // a round with more tiles than CUs shares each CU between per_cu workgroups
+    const double per_round = (double)c.bm * c.bn / c.eff * (tiles > cus ? c.per_cu : 1);
+    const double t = (double)rounds * per_round;
+    if (t < best_t * 0.999) {
+      best_t = t;
+      best = i;
+    }
+  }
+  return best;
+}
+
 template <typename TR, typename TC>
 static hipError_t dispatch_dma(const GemmArgs& a) {
-  const int64_t big = ((a.M + 255) / 256) * (int64_t)((a.N + 255) / 256);
-  if (sizeof(TC) == 2 && big >= 4 * (int64_t)compute_units()) return launch_dma<256, 256, 2, 2, 2, 4, TR, TC>(a);
-  return launch_dma<128, 128, 2, 2, 2, 8, TR, TC>(a);
+  switch (pick_tile(a.M, a.N)) {
+    case 0: return launch_dma<256, 256, 4, 2, 2, 4, TR, TC>(a);
+    case 1: return launch_dma<256, 192, 4, 2, 2, 4, TR, TC>(a);
+    case 2: return launch_dma<256, 128, 4, 2, 2, 4, TR, TC>(a);
+    default: return launch_dma<128, 128, 2, 2, 2, 8, TR, TC>(a);
+  }
 }
 
 bool gemm_dma_ok(const GemmArgs& a) {

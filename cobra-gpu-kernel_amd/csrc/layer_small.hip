@@ -190,7 +190,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
           s += xv[kk][e];
         }
       }
-      const float mean = (s + __shfl_xor(s, 32)) * (1.0f / D);
+      const float mean = sum_xor32(s) * (1.0f / D);
       float q = 0.f;
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk)
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
           const float t = xv[kk][e] - mean;
           q += t * t;
         }
-      const float rstd = rsqrtf((q + __shfl_xor(q, 32)) * (1.0f / D) + eps);
+      const float rstd = rsqrtf(sum_xor32(q) * (1.0f / D) + eps);
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
         float gv[8], bv[8];
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max_xor32(mx);
         const float m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);  // block 0 always holds key 0
         const float alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
             for (int dt = 0; dt < NDT; ++dt)
               ot[dt] = mfma32x32x16(Vl[(((2 * blk + u) * NDT + dt) * 2 + half) * 64 + lane], pB[u][half], ot[dt]);
       }
-      l += __shfl_xor(l, 32);
+      l = sum_xor32(l);
       const float inv = __builtin_amdgcn_rcpf(l);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
           s += v[nt][qd][e];
         }
       }
-    const float mean = (s + __shfl_xor(s, 32)) * (1.0f / D);
+    const float mean = sum_xor32(s) * (1.0f / D);
     float q = 0.f;
 #pragma unroll
     for (int nt = 0; nt < NNT; ++nt)
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
           const float t = v[nt][qd][e] - mean;
           q += t * t;
         }
-    const float rstd = rsqrtf((q + __shfl_xor(q, 32)) * (1.0f / D) + eps);
+    const float rstd = rsqrtf(sum_xor32(q) * (1.0f / D) + eps);
     if (tok_ok) {
       TX* yrow = y + row * D;
 #pragma unroll

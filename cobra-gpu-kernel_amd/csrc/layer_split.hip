@@ -197,7 +197,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         sum += xv[kk][e];
       }
     }
-    const float mean = (sum + __shfl_xor(sum, 32)) * (1.0f / D);
+    const float mean = sum_xor32(sum) * (1.0f / D);
     float q = 0.f;
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk)
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         const float t = xv[kk][e] - mean;
         q += t * t;
       }
-    const float rstd = rsqrtf((q + __shfl_xor(q, 32)) * (1.0f / D) + eps);
+    const float rstd = rsqrtf(sum_xor32(q) * (1.0f / D) + eps);
     const float* pg = reinterpret_cast<const float*>(rP);
     // The output fragments overwrite the token tile in place: every read of it above
     // feeds the mean, so all of them precede the first write.
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = max_xor32(mx);
       // Block 0 holds key 0, valid for every query, so its max is finite; a fully
       // masked later block leaves the running max as it is.
       const float m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
             ot[dt] = mfma32x32x16(Vl[(((h * kSplitTiles + 2 * blk + u) * NDT + dt) * 2 + half) * 64 + lane],
                                   pB[u][half], ot[dt]);
     }
-    l += __shfl_xor(l, 32);
+    l = sum_xor32(l);
     const float inv = __builtin_amdgcn_rcpf(l);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         sum += v[qd][e];
       }
     }
-    sum += __shfl_xor(sum, 32);
+    sum = sum_xor32(sum);
     if (g == 0) Stat[w * 32 + li] = sum;
   }
   lds_barrier();
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         const float t = v[qd][e] - mean;
         q += t * t;
       }
-    q += __shfl_xor(q, 32);
+    q = sum_xor32(q);
     if (g == 0) Stat[(kSplitWaves + w) * 32 + li] = q;
   }
   lds_barrier();

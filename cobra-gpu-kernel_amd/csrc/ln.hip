@@ -16,8 +16,11 @@
 
 namespace cobra {
 
+// Rows up to 1024 wide: eight waves per SIMD (<= 64 VGPRs), so that 8192 rows
+// of 1024 -- one row per wave -- are all in flight at once on 256 CUs instead
+// of in two rounds.  Wider rows hold more registers and keep the default.
 template <typename TX, typename TY, int LPR, int NCH>
-__global__ __launch_bounds__(256) void ln_rows_kernel(const TX* __restrict__ x, const void* __restrict__ branch,
+__global__ __launch_bounds__(256, NCH <= 2 ? 8 : 1) void ln_rows_kernel(const TX* __restrict__ x, const void* __restrict__ branch,
                                                       int branch_f32, const float* __restrict__ gamma,
                                                       const float* __restrict__ beta, float* __restrict__ resid_out,
                                                       TY* __restrict__ y, int64_t rows, int d, float eps,
