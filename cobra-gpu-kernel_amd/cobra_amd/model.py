@@ -1,0 +1,288 @@
+"""Drop-in transformer stack: ``CobraTransformer`` for the reference's model.
+
+``CobraTransformer(config)`` has the parameters, construction order and
+``forward(x, valid_token_mask=None)`` surface of ``BaselineTransformer`` /
+``UserOptimizedTransformer`` (torch_transformer_benchmark.py:149-173,
+917-1541, "TTB"): ``layers[i].{norm1, attention.{q,k,v,out}_proj, norm2,
+ffn_in, ffn_out}`` and ``final_norm``, so a reference state_dict loads with
+``strict=True`` and a seeded construction draws the reference's weights.
+
+Every op runs on this library's HIP kernels through ``ops`` (no PyTorch
+compute fallback).  Per block, with the residual stream ``r`` kept in fp32
+and GEMM operands in fp16 (the reference's fused policy, TTB:1170-1290):
+
+    h    = LN1(r)                       layer 0: LayerNorm kernel; later layers:
+                                        the previous block's FFN epilogue
+    qkv  = h Wqkv^T + b                 one [3D, D] GEMM, q|k|v order (TTB:876-883)
+    ctx  = attention(qkv)               flash attention, causal per config,
+                                        padded keys masked (TTB:98-113)
+    r    = r + (ctx Wo^T + bo)          fp32 epilogue; padded rows' branch = 0
+    h2   = LN2(r)                       same kernel for d_model <= 128, else a
+                                        LayerNorm pass (TTB:1255-1283)
+    f    = gelu(h2 W1^T + b1)           exact erf GELU in the GEMM epilogue
+    r    = (r + f W2^T + b2) * mask     block row mask (TTB:144-145)
+    h    = LN1'(r)                      the NEXT block's norm1, or final_norm with
+                                        the output row mask on the last block
+
+The op order and roundings are the reference's; the output is x.dtype.
+Small inputs (<= 64 MiB, TTB:1077-1079) replay a captured hipGraph of the
+whole forward with static input / mask buffers (TTB:1331-1360); inputs that
+do not fit one device pass stream in batch chunks (TTB:1364-1508).
+"""
+
+from __future__ import annotations
+
+import gc
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+
+from . import ops, streaming
+from .layer import CobraSelfAttention
+
+GRAPH_MAX_INPUT_BYTES = 64 * 1024 * 1024
+
+
+@dataclass(frozen=True)
+class TransformerConfig:
+    """Fields and validation of the reference's ``TransformerConfig`` (TTB:28-57)."""
+
+    batch_size: int
+    seq_len: int
+    d_model: int
+    num_heads: int
+    ffn_dim: int
+    num_layers: int
+    causal: bool
+
+    def validate(self) -> None:
+        for name in ("batch_size", "seq_len", "d_model", "num_heads", "ffn_dim", "num_layers"):
+            if getattr(self, name) <= 0:
+                raise ValueError(f"{name} must be positive")
+        if self.d_model % self.num_heads != 0:
+            raise ValueError(f"d_model ({self.d_model}) must be divisible by num_heads ({self.num_heads})")
+
+
+class CobraTransformerBlock(nn.Module):
+    """Parameters of ``BaselineTransformerBlock`` (TTB:126-133), same names and draw order."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attention = CobraSelfAttention(d_model, num_heads)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn_in = nn.Linear(d_model, ffn_dim)
+        self.ffn_out = nn.Linear(ffn_dim, d_model)
+
+
+class _BlockPack:
+    """Kernel-ready copies of one block's parameters (plain attributes, so the
+    state_dict is unchanged; TTB:857-914)."""
+
+    __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "w1", "b1", "w2", "b2", "ln1_w", "ln1_b", "ln2_w", "ln2_b")
+
+    def __init__(self, blk: CobraTransformerBlock) -> None:
+        att = blk.attention
+        with torch.no_grad():
+            self.w_qkv = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(
+                torch.float16).contiguous()
+            self.b_qkv = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).float().contiguous()
+            self.w_o = att.out_proj.weight.to(torch.float16).contiguous()
+            self.b_o = att.out_proj.bias.float().contiguous()
+            self.w1 = blk.ffn_in.weight.to(torch.float16).contiguous()
+            self.b1 = blk.ffn_in.bias.float().contiguous()
+            self.w2 = blk.ffn_out.weight.to(torch.float16).contiguous()
+            self.b2 = blk.ffn_out.bias.float().contiguous()
+            self.ln1_w = blk.norm1.weight.float().contiguous()
+            self.ln1_b = blk.norm1.bias.float().contiguous()
+            self.ln2_w = blk.norm2.weight.float().contiguous()
+            self.ln2_b = blk.norm2.bias.float().contiguous()
+
+
+class CobraTransformer(nn.Module):
+    def __init__(self, config: TransformerConfig, graph: Optional[bool] = None) -> None:
+        super().__init__()
+        config.validate()
+        self.config = config
+        # Construction order = BaselineTransformer's (TTB:153-161).
+        self.layers = nn.ModuleList(
+            [CobraTransformerBlock(config.d_model, config.num_heads, config.ffn_dim)
+             for _ in range(config.num_layers)]
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+        # hipGraph replay: None = automatic (inputs <= 64 MiB), True / False force it.
+        self.graph = graph
+        self._params = list(self.parameters())
+        self._versioned = [not p.is_inference() for p in self._params]
+        self._packs: Optional[List[_BlockPack]] = None
+        self._final = None
+        self._versions = None
+        self._sig = None
+        self._graph_ok = False
+        self._graph = None
+        self._static_x = self._static_m = self._static_out = None
+
+    # -- parameters -----------------------------------------------------------
+
+    def _apply(self, fn, *args, **kwargs):
+        out = super()._apply(fn, *args, **kwargs)
+        self._params = list(self.parameters())
+        self._versioned = [not p.is_inference() for p in self._params]
+        self._packs = None
+        self._sig = None
+        return out
+
+    def _packed(self) -> List[_BlockPack]:
+        versions = tuple([p._version if v else p.data_ptr() for p, v in zip(self._params, self._versioned)])
+        if self._packs is None or self._versions != versions:
+            if not self.final_norm.weight.is_cuda:
+                raise RuntimeError("CobraTransformer runs on the GPU only: move it with .to('cuda')")
+            self._packs = [_BlockPack(blk) for blk in self.layers]
+            with torch.no_grad():
+                self._final = (self.final_norm.weight.float().contiguous(), self.final_norm.bias.float().contiguous())
+            self._versions = versions
+            self._graph = None
+        return self._packs
+
+    # -- entry point ----------------------------------------------------------
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        self._validate(x)
+        packs = self._packed()
+        if not x.is_cuda or x.numel() * x.element_size() >= streaming.STREAM_MIN_BYTES:
+            if self._stream_needed(x):
+                return self._run_streamed(x, valid_token_mask)
+        masked = valid_token_mask is not None
+        sig = (tuple(x.shape), x.dtype, x.device, masked)
+        if sig != self._sig:
+            self._graph_ok = (self.graph if self.graph is not None else True) and \
+                x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
+            self._graph = None
+            self._static_x = self._static_m = self._static_out = None
+            self._sig = sig
+        x = x.contiguous()
+        m = self._mask_bytes(valid_token_mask, x) if masked else None
+        if self._graph_ok:
+            return self._run_graphed(x, m, packs)
+        return self._run(x, m, packs)
+
+    def _validate(self, x: torch.Tensor) -> None:
+        if x.dim() != 3 or x.shape[-1] != self.config.d_model:
+            raise ValueError(f"x must be [B, S, {self.config.d_model}], got {tuple(x.shape)}")
+        if x.dtype not in (torch.float16, torch.float32):
+            raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
+        d, f = self.config.d_model, self.config.ffn_dim
+        hd = d // self.config.num_heads
+        if d % 8 or f % 8 or hd % 8 or hd > 256 or d > 4096:
+            raise ValueError("the HIP kernels need d_model, ffn_dim and head_dim multiples of 8, "
+                             "head_dim <= 256 and d_model <= 4096")
+
+    @staticmethod
+    def _mask_bytes(mask: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """[B, S] token mask as contiguous device bytes (0 = padded); applied whenever given."""
+        if tuple(mask.shape) != tuple(x.shape[:2]):
+            raise ValueError(f"valid_token_mask must be {tuple(x.shape[:2])}, got {tuple(mask.shape)}")
+        if mask.dtype not in (torch.bool, torch.uint8):
+            raise TypeError(f"valid_token_mask must be bool or uint8, got {mask.dtype}")
+        mask = mask.to(x.device, non_blocking=True).contiguous()
+        return mask.view(torch.uint8) if mask.dtype == torch.bool else mask
+
+    # -- the forward, as a sequence of kernel launches ---------------------------
+
+    def _run(self, x: torch.Tensor, m: Optional[torch.Tensor], packs: List[_BlockPack]) -> torch.Tensor:
+        cfg = self.config
+        B, S, D = x.shape
+        T = B * S
+        H = cfg.num_heads
+        hd = D // H
+        scale = hd ** -0.5
+        eps = self.final_norm.eps
+        xf = x.view(T, D)
+        mrow = None if m is None else m.view(T)
+        bits = None if m is None else ops.mask_bits(m.view(B, S))
+        out16 = x.dtype == torch.float16
+        n = len(packs)
+
+        _, h = ops.add_ln(xf, None, None, packs[0].ln1_w, packs[0].ln1_b, cast_fp16=True, eps=eps,
+                          store_resid=False)
+        r = xf
+        for i, p in enumerate(packs):
+            last = i == n - 1
+            nw, nb = self._final if last else (packs[i + 1].ln1_w, packs[i + 1].ln1_b)
+            qkv = ops.linear(h, p.w_qkv, p.b_qkv)
+            ctx = ops.attn(qkv, B, S, H, hd, scale, causal=cfg.causal, key_bits=bits)
+            if D <= 128:
+                r, h2 = ops.linear_ln(ctx, p.w_o, p.b_o, r, p.ln2_w, p.ln2_b, rmask=mrow, eps=eps, mask_branch=True)
+            else:
+                r = ops.linear(ctx, p.w_o, p.b_o, out_fp32=True, resid=r, rmask=mrow, mask_branch=True)
+                _, h2 = ops.add_ln(r, None, None, p.ln2_w, p.ln2_b, cast_fp16=True, eps=eps, store_resid=False)
+            hid = ops.linear(h2, p.w1, p.b1, gelu=True)
+            norm16 = out16 or not last
+            if D <= 128:
+                r, h = ops.linear_ln(hid, p.w2, p.b2, r, nw, nb, rmask=mrow, norm_fp16=norm16, mask_out=last,
+                                     eps=eps)
+            else:
+                r = ops.linear(hid, p.w2, p.b2, out_fp32=True, resid=r, rmask=mrow)
+                _, h = ops.add_ln(r, None, mrow, nw, nb, cast_fp16=norm16, eps=eps, store_resid=False,
+                                  mask_out=last)
+        return h.view(B, S, D)
+
+    def _run_graphed(self, x, m, packs):
+        if self._graph is None:
+            self._static_x = x.clone()
+            self._static_m = None if m is None else m.clone()
+            self._run(self._static_x, self._static_m, packs)  # loads every code object outside the capture
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._static_out = self._run(self._static_x, self._static_m, packs)
+            self._graph = graph
+        if x.data_ptr() != self._static_x.data_ptr():
+            self._static_x.copy_(x)
+        if m is not None and m.data_ptr() != self._static_m.data_ptr():
+            self._static_m.copy_(m)
+        self._graph.replay()
+        # Returned without a clone, as the reference does (TTB:1356-1360).
+        return self._static_out
+
+    # -- streaming -----------------------------------------------------------------
+
+    def _per_seq_bytes(self, x: torch.Tensor) -> int:
+        """Device bytes one sequence holds at the peak of a block (this build's model):
+        fp32 residual, fp16 h / qkv / ctx / h2 / FFN hidden, the input and the output."""
+        S, D, F = x.shape[1], self.config.d_model, self.config.ffn_dim
+        per_tok = 4 * D + 2 * D + 6 * D + 2 * D + 2 * D + 2 * F + 2 * D * x.element_size() + 4 * D
+        return S * per_tok
+
+    def _stream_needed(self, x: torch.Tensor) -> bool:
+        nbytes = x.numel() * x.element_size()
+        if x.is_cuda and nbytes < streaming.STREAM_MIN_BYTES:
+            return False
+        free, _ = torch.cuda.mem_get_info(self.final_norm.weight.device)
+        return streaming.should_stream(x.is_cuda, nbytes, x.shape[0], self._per_seq_bytes(x) * x.shape[0], free)
+
+    def _run_streamed(self, x, valid_token_mask):
+        dev = self.final_norm.weight.device
+        packs = self._packed()
+        B = x.shape[0]
+        host = not x.is_cuda
+        free, _ = torch.cuda.mem_get_info(dev)
+        step = streaming.plan_chunk(B, self._per_seq_bytes(x), free)
+        out = torch.empty_like(x)
+
+        def run_chunk(b0: int, b1: int) -> None:
+            xc = x[b0:b1]
+            xc = xc.to(dev, non_blocking=True) if host else xc.contiguous()
+            mc = None
+            if valid_token_mask is not None:
+                mc = self._mask_bytes(valid_token_mask[b0:b1], xc)
+            out[b0:b1].copy_(self._run(xc, mc, packs))
+
+        def on_oom() -> None:
+            gc.collect()
+            torch.cuda.empty_cache()
+
+        streaming.run_chunked(B, step, run_chunk, on_oom, lambda e: isinstance(e, torch.cuda.OutOfMemoryError))
+        return out

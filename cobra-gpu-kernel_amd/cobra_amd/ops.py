@@ -246,13 +246,15 @@ def attn(
     cfgs=None,
     causal: bool = True,
     key_mask: Optional[torch.Tensor] = None,
+    key_bits: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention on packed ``qkv [B*S, 3*H*hd]`` -> ``ctx [B*S, H*hd]``.  Mirrors ``_tl_attn`` (TTB:828-854).
 
     ``cfgs`` (the reference's tile ladder) is accepted and ignored: tiles are
     chosen inside the library from (seq_len, head_dim).  ``key_mask`` ([B, S]
     bool/uint8, 0 = padded) masks keys like TTB:106-109; a query with no valid
-    key gets a zero row.
+    key gets a zero row.  ``key_bits`` passes the packed form (``mask_bits``)
+    instead, so a caller with several attention calls per mask packs it once.
     """
     _dev(qkv, "qkv")
     if qkv.dtype != torch.float16 or out_dtype != torch.float16:
@@ -260,11 +262,17 @@ def attn(
     D = heads * head_dim
     if qkv.shape != (batch * seq_len, 3 * D):
         raise ValueError(f"qkv must be [{batch * seq_len}, {3 * D}], got {tuple(qkv.shape)}")
-    bits = None
+    bits = key_bits
     if key_mask is not None:
+        if key_bits is not None:
+            raise ValueError("pass key_mask or key_bits, not both")
         if tuple(key_mask.shape) != (batch, seq_len):
             raise ValueError(f"key_mask must be [{batch}, {seq_len}], got {tuple(key_mask.shape)}")
         bits = mask_bits(key_mask)
+    elif bits is not None:
+        _dev(bits, "key_bits")
+        if bits.dtype != torch.int64 or tuple(bits.shape) != (batch, (seq_len + 63) // 64):
+            raise ValueError(f"key_bits must be int64 [{batch}, {(seq_len + 63) // 64}]")
     out = torch.empty((batch * seq_len, D), device=qkv.device, dtype=torch.float16)
     call(
         "cobra_attn_fwd", qkv.data_ptr(), out.data_ptr(), _ptr(bits), batch, seq_len, heads, head_dim,

@@ -15,6 +15,9 @@ reference checkout; ``TTB`` = ``torch_transformer_benchmark.py``):
   cannot be materialised.
 * ``gate``    -- ``compare_outputs`` (TTB:1616-1697): per element
   ``finite and (abs <= atol or abs <= rtol*|ref|)``.
+* ``model``   -- ``OracleTransformerConfig`` / ``OracleTransformerBlock`` /
+  ``OracleTransformer``: the whole stack (TTB:28-57, 126-173) -- attention
+  half, exact-GELU FFN half, block and output row masks, ``final_norm``.
 * ``cases``   -- seeded construction (TTB:2024-2031), input generation
   (TTB:1575-1593 semantics on a CPU generator) and the configuration matrix of
   the benchmark (tools/sweep.py:31-47, attention sublayer only).
@@ -36,3 +39,10 @@ from .cases import (  # noqa: F401
 )
 from .gate import AccuracyResult, compare_outputs  # noqa: F401
 from .layer import OracleAttentionSublayer, OracleSelfAttention  # noqa: F401
+from .model import (  # noqa: F401
+    OracleTransformer,
+    OracleTransformerBlock,
+    OracleTransformerConfig,
+    make_model,
+    model_forward,
+)

@@ -1,0 +1,157 @@
+"""GPU parity of the whole stack (``CobraTransformer``) against the fp32 oracle model.
+
+The cases are the reference's own causal matrix (tools/sweep.py:31-47: batch,
+d_model, heads, seq_len, layers, ffn_dim) at full size where the oracle
+finishes in seconds -- on the CPU, or on the GPU in fp32 with TF32 off for the
+larger ones -- plus non-causal and padded variants (tools/validate.py:74-80).
+Gate: the reference's (abs <= 2e-3 or rel <= 2e-2, zero failing elements).
+fp16 cases compare against the oracle on the same fp16-rounded inputs and
+weights; the fp32 case (the reference's scored setting, fp16 operands inside)
+against the unrounded fp32 oracle.
+"""
+
+import pytest
+import torch
+
+from oracle import OracleTransformerConfig, compare_outputs, make_input, make_model, model_forward, quantize_like
+
+from _gpu_util import DEV, log
+
+pytestmark = pytest.mark.gpu
+
+
+def build(cfg, dtype=torch.float16, seed=0, graph=None):
+    from cobra_amd import CobraTransformer, TransformerConfig
+
+    ref = make_model(OracleTransformerConfig(*cfg), seed=seed)
+    if dtype == torch.float16:
+        quantize_like(ref, torch.float16)
+    mod = CobraTransformer(TransformerConfig(*cfg), graph=graph)
+    mod.load_state_dict(ref.state_dict(), strict=True)
+    return ref, mod.to(device=DEV, dtype=dtype).eval()
+
+
+def run_case(cfg, dtype=torch.float16, mask=None, oracle_device="cpu", subset=None, seed=0):
+    B, S, D = cfg[0], cfg[1], cfg[2]
+    log(f"[model] B{B} S{S} D{D} H{cfg[3]} F{cfg[4]} L{cfg[5]} causal={cfg[6]} dtype={dtype} "
+        f"mask={'yes' if mask is not None else 'no'}")
+    ref, mod = build(cfg, dtype, seed=seed)
+    x = make_input(B, S, D, seed=seed + 1).to(dtype)
+    if mask is not None:
+        x = x.masked_fill(~mask[..., None], 0)
+    with torch.inference_mode():
+        y = mod(x.to(DEV), None if mask is None else mask.to(DEV))
+        y = y.float().cpu()
+        torch.cuda.synchronize()
+    rows = list(range(B)) if subset is None else subset
+    layer = ref.to(oracle_device)
+    try:
+        want = model_forward(layer, x[rows].to(oracle_device), None if mask is None else mask[rows]).cpu()
+    finally:
+        ref.to("cpu")
+    res = compare_outputs(want, y[rows])
+    log(f"[model] max_abs={res.max_abs_error:.3e} max_rel={res.max_relative_error:.3e} "
+        f"failed={res.failed_elements}/{res.total_elements}")
+    return res
+
+
+# (#, batch, d_model, heads, seq_len, layers, ffn_dim) from tools/sweep.py, as config tuples
+SWEEP = {
+    1: (64, 128, 128, 4, 128, 4, True), 2: (1, 128, 128, 4, 128, 4, True), 3: (4, 128, 128, 4, 128, 4, True),
+    4: (16, 128, 128, 4, 128, 4, True), 5: (128, 128, 128, 4, 128, 4, True), 7: (64, 128, 32, 4, 32, 4, True),
+    9: (64, 128, 128, 1, 128, 4, True), 10: (64, 128, 128, 2, 128, 4, True), 11: (64, 128, 128, 16, 128, 4, True),
+    12: (64, 32, 128, 4, 128, 4, True),
+}
+
+
+@pytest.mark.parametrize("case", sorted(SWEEP))
+def test_sweep_case_cpu_oracle(case):
+    res = run_case(SWEEP[case])
+    assert res.passed, res
+
+
+@pytest.mark.parametrize("cfg", [(64, 128, 1024, 4, 1024, 4, True), (64, 1024, 128, 4, 128, 4, True)])
+def test_sweep_case_gpu_oracle(cfg):
+    """Cases 8 (d_model 1024, head_dim 256) and 13 (S = 1024)."""
+    res = run_case(cfg, oracle_device=DEV)
+    assert res.passed, res
+
+
+def test_sweep_case_6_sampled():
+    """Case 6 (B = 10000): the full batch on the GPU, sampled sequences on the CPU."""
+    res = run_case((10000, 128, 128, 4, 128, 4, True), subset=[0, 1, 4321, 9999])
+    assert res.passed, res
+
+
+def test_long_sequence_sampled():
+    """Case 14's geometry (d_model 1024, 16 heads, 2 layers) at S = 8192: GPU oracle with blocked queries."""
+    cfg = (2, 8192, 1024, 16, 1024, 2, True)
+    ref, mod = build(cfg)
+    x = make_input(2, 8192, 1024, seed=3).half()
+    with torch.inference_mode():
+        y = mod(x.to(DEV)).float()
+        torch.cuda.synchronize()
+    layer = ref.to(DEV)
+    try:
+        want = model_forward(layer, x.to(DEV), block_q=2048)
+    finally:
+        ref.to("cpu")
+    res = compare_outputs(want.cpu(), y.cpu())
+    log(f"[model S8192] max_abs={res.max_abs_error:.3e} failed={res.failed_elements}")
+    assert res.passed, res
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("pad", [0.3, 0.9])
+def test_padded(causal, pad):
+    """tools/validate.py:74-80: left-aligned padding, causal and not."""
+    B, S = 8, 128
+    g = torch.Generator().manual_seed(int(pad * 10) + causal)
+    lengths = torch.randint(max(1, round(S * (1 - pad))), S + 1, (B,), generator=g)
+    mask = torch.arange(S)[None, :] < lengths[:, None]
+    res = run_case((B, S, 128, 4, 128, 4, causal), mask=mask)
+    assert res.passed, res
+
+
+def test_padded_wide_model():
+    """d_model > 128 (separate LayerNorm passes) with a scattered mask, non-causal."""
+    B, S = 4, 96
+    mask = torch.rand(B, S, generator=torch.Generator().manual_seed(5)) < 0.7
+    mask[:, 0] = True
+    res = run_case((B, S, 256, 4, 512, 2, False), mask=mask)
+    assert res.passed, res
+
+
+def test_fp32_io_against_unrounded_oracle():
+    """The reference's scored setting: fp32 model and input, fp16 operands inside (TTB:960-1004)."""
+    res = run_case((16, 128, 128, 4, 128, 4, False), dtype=torch.float32)
+    assert res.passed, res
+
+
+def test_graph_replay_matches_eager_and_new_inputs():
+    cfg = (8, 128, 128, 4, 256, 2, True)
+    _, mod = build(cfg, graph=True)
+    _, eager = build(cfg, graph=False)
+    for seed in range(3):
+        x = make_input(8, 128, 128, seed=10 + seed).half().to(DEV)
+        with torch.inference_mode():
+            a = mod(x).clone()
+            b = eager(x)
+            torch.cuda.synchronize()
+        assert torch.equal(a, b), seed
+    assert mod._graph is not None
+
+
+def test_state_dict_and_reload():
+    """A reference-layout state_dict loads strictly; changing a weight in place is picked up."""
+    cfg = (2, 16, 128, 4, 128, 2, False)
+    ref, mod = build(cfg, graph=False)
+    x = make_input(2, 16, 128, seed=4).half().to(DEV)
+    with torch.inference_mode():
+        a = mod(x).clone()
+    with torch.no_grad():
+        mod.layers[1].ffn_out.bias.add_(1.0)
+    with torch.inference_mode():
+        b = mod(x)
+    assert (a - b).abs().max().item() > 1e-3
+    assert set(mod.state_dict()) == set(ref.state_dict())

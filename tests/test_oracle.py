@@ -407,3 +407,141 @@ def test_planted_mistakes_are_caught(mistake, monkeypatch):
         except AssertionError:
             caught = True
     assert caught, f"planted mistake '{mistake}' went unnoticed"
+
+
+# ---------------------------------------------------------------------------
+# The whole stack (oracle/model.py, TTB:126-173)
+# ---------------------------------------------------------------------------
+
+from oracle import OracleTransformerConfig, make_model  # noqa: E402
+
+
+def _model64(b, s, d, h, f, n, causal, seed=0):
+    cfg = OracleTransformerConfig(b, s, d, h, f, n, causal)
+    model = make_model(cfg, seed=seed).double()
+    with torch.no_grad():  # non-trivial LayerNorm affine so gamma/beta are exercised
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.uniform_(0.5, 1.5) if name.endswith("weight") else p.uniform_(-0.5, 0.5)
+    return model
+
+
+def _np_gelu_erf(t):
+    return 0.5 * t * (1.0 + np.vectorize(math.erf)(t / math.sqrt(2.0)))
+
+
+def _np_block_s1(blk, x):
+    """One block at S = 1 in fp64 numpy: attention reduces to the value path (ctx = v)."""
+    h = _np_layernorm(blk.norm1, x)
+    att = blk.attention
+    x1 = x + _np_linear(att.out_proj, _np_linear(att.v_proj, h))
+    f = _np_gelu_erf(_np_linear(blk.ffn_in, _np_layernorm(blk.norm2, x1)))
+    return x1 + _np_linear(blk.ffn_out, f)
+
+
+def test_model_single_token_closed_form():
+    """S = 1: the stack is LN -> v -> out -> +x -> LN -> W1 -> exact GELU -> W2 -> +x per
+    block, then final_norm; restated in numpy fp64 with math.erf."""
+    model = _model64(3, 1, 16, 4, 24, 3, causal=True)
+    x = torch.randn(3, 1, 16, dtype=torch.float64)
+    with torch.no_grad():
+        got = model(x).numpy()
+    want = x.numpy()
+    for blk in model.layers:
+        want = _np_block_s1(blk, want)
+    want = _np_layernorm(model.final_norm, want)
+    assert np.abs(got - want).max() < 1e-10
+
+
+def test_gelu_is_the_exact_erf_form():
+    """The oracle's FFN activation (oracle.model.F.gelu, as the stack calls it) is
+    the exact erf GELU; the tanh form differs by more than any rounding would hide."""
+    from oracle import model as M
+
+    t = torch.linspace(-6, 6, 241, dtype=torch.float64)
+    got = M.F.gelu(t, approximate="none").numpy()
+    assert np.abs(got - _np_gelu_erf(t.numpy())).max() < 1e-14
+
+
+def test_model_attention_half_is_the_sublayer():
+    """Each block's first half is the (separately pinned) attention sublayer's residual."""
+    model = _model64(2, 7, 16, 4, 32, 1, causal=False)
+    sub = OracleAttentionSublayer(16, 4).double()
+    blk = model.layers[0]
+    sub.norm1.load_state_dict(blk.norm1.state_dict())
+    sub.attention.load_state_dict(blk.attention.state_dict())
+    sub.norm2.load_state_dict(blk.norm2.state_dict())
+    x = torch.randn(2, 7, 16, dtype=torch.float64)
+    with torch.no_grad():
+        r, _ = sub(x, return_residual=True)
+        x1 = x + blk.attention(blk.norm1(x), None, False)
+    assert (r - x1).abs().max().item() == 0.0
+
+
+def _model_mask_checks(model, x, mask):
+    """(padded-row max |y|, causal: valid rows vs the unmasked run;
+    non-causal: valid rows vs each sequence's valid tokens alone)."""
+    with torch.no_grad():
+        y = model(x, mask)
+        padded = y[~mask].abs().max().item() if (~mask).any() else 0.0
+        worst = 0.0
+        if model.config.causal:
+            plain = model(x)
+            worst = (y - plain)[mask].abs().max().item()
+        else:
+            for bi in range(x.shape[0]):
+                keep = mask[bi]
+                alone = model(x[bi : bi + 1, keep])
+                worst = max(worst, (y[bi, keep] - alone[0]).abs().max().item())
+    return padded, worst
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_model_masks(causal):
+    """Padded rows are exactly 0 (TTB:144-145, 171-172); under causality with
+    left-aligned padding the valid rows equal the unmasked run (TTB:1110-1115);
+    without causality they equal the model run on the valid tokens alone."""
+    model = _model64(4, 9, 16, 4, 24, 2, causal=causal)
+    x = torch.randn(4, 9, 16, dtype=torch.float64)
+    mask = _ragged_mask(4, 9, seed=7, left_aligned=True)
+    x = x.masked_fill(~mask[..., None], 0)
+    padded, worst = _model_mask_checks(model, x, mask)
+    assert padded == 0.0
+    assert worst < SOFTMAX_TOL
+
+
+# The per-block row mask (TTB:144-145) is not among the plants: with padded keys
+# masked and the output rows masked at the end, no output element depends on
+# it (the reference's fused path likewise skips the attention output's row
+# mask, TTB:1255-1268).
+@pytest.mark.parametrize("mistake", ["gelu_tanh", "norm2_after_add", "no_final_norm", "no_output_mask"])
+def test_model_planted_mistakes_are_caught(mistake, monkeypatch):
+    from oracle import model as M
+
+    if mistake == "gelu_tanh":
+        orig_gelu = F.gelu
+        monkeypatch.setattr(M.F, "gelu", lambda t, approximate="none": orig_gelu(t, approximate="tanh"))
+    elif mistake == "norm2_after_add":
+        def bad_block(self, x, m, causal, block_q=None):
+            x = x + self.attention(self.norm1(x), m, causal, block_q)
+            return self.norm2(x + self.ffn_out(F.gelu(self.ffn_in(x))))
+        monkeypatch.setattr(M.OracleTransformerBlock, "forward", bad_block)
+    elif mistake == "no_final_norm":
+        monkeypatch.setattr(M.OracleTransformer, "forward",
+                            lambda self, x, m=None, block_q=None: self.layers[0](x, m, self.config.causal, block_q)
+                            if len(self.layers) == 1 else x)
+    elif mistake == "no_output_mask":
+        def unmasked_output(self, x, m=None, block_q=None):
+            for layer in self.layers:
+                x = layer(x, m, self.config.causal, block_q)
+            return self.final_norm(x)
+        monkeypatch.setattr(M.OracleTransformer, "forward", unmasked_output)
+    caught = False
+    try:
+        test_model_single_token_closed_form()
+        test_gelu_is_the_exact_erf_form()
+        test_model_masks(False)
+        test_model_masks(True)
+    except AssertionError:
+        caught = True
+    assert caught, f"planted mistake '{mistake}' went unnoticed"
