@@ -17,6 +17,8 @@ Also on the same line:
     reference PyTorch layer) on the host cores, on a bounded sample;
   * ``long``: BASELINE config 5, B=32 d=1024 H=16 S=100000 (``--no-long`` skips);
   * ``sweep``: every other BASELINE configuration, ms and TFLOP/s per forward;
+  * ``model``: the whole ``CobraTransformer`` stack on three of the reference's
+    model cases (tools/sweep.py:31-47), causal, fp16;
   * ``measured_peaks``: fp16 GEMM TFLOP/s and device-copy GB/s on this box;
   * ``graph``: the same forward replayed as a hipGraph, and an empty-graph floor.
 
@@ -249,6 +251,35 @@ def bench_long(dev, steps=2, warmup=1):
             "roofline": roofline("attn_fwd_kernel (per sequence)", a_fl, 4 * S * D * 2, a_ms)}
 
 
+MODEL_CASES = [  # the reference's whole-model cases (tools/sweep.py:31-47): #, B, S, D, H, F, layers (causal)
+    ("case1", 64, 128, 128, 4, 128, 4), ("case8", 64, 128, 1024, 4, 1024, 4), ("case13", 64, 1024, 128, 4, 128, 4),
+]
+
+
+def bench_model(dev, iters=20):
+    """The whole ``CobraTransformer`` stack (hipGraph replay for these sizes), causal, fp16."""
+    from cobra_amd import CobraTransformer, TransformerConfig
+
+    out = {}
+    for name, B, S, D, H, F, L in MODEL_CASES:
+        torch.manual_seed(0)
+        model = CobraTransformer(TransformerConfig(B, S, D, H, F, L, True)).to(device=dev,
+                                                                                dtype=torch.float16).eval()
+        x = torch.randn(B, S, D, device=dev, dtype=torch.float16)
+        with torch.inference_mode():
+            for _ in range(3):
+                model(x)
+            ms = statistics.median([event_ms(lambda: model(x), iters) for _ in range(3)])
+        T = B * S
+        fl = L * (8 * T * D * D + 2 * B * S * S * D + 4 * T * D * F)  # causal attention: half the S^2 work
+        out[name] = {"B": B, "S": S, "D": D, "H": H, "ffn_dim": F, "layers": L, "causal": True,
+                     "ms_per_forward": ms, "tflops": fl / (ms / 1e3) / 1e12}
+        log(f"[model] {name}: {ms:.3f} ms/forward ({out[name]['tflops']:.1f} TFLOP/s)")
+        del model, x
+    torch.cuda.empty_cache()
+    return out
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_layer_split_kernel_B64_d128_H4_S128.txt")
 
 
@@ -363,6 +394,9 @@ def main() -> int:
         for v in line["sweep"].values():
             v["measured_mfma_frac"] = v["tflops_in_graph"] / peaks["fp16_gemm_8192_tflops"]
             v["measured_hbm_frac"] = v["hbm_gbs_in_graph"] / peaks["device_copy_gbs"]
+        line["model"] = bench_model(dev)
+        for v in line["model"].values():
+            v["measured_mfma_frac"] = v["tflops"] / peaks["fp16_gemm_8192_tflops"]
     if not args.no_long:
         try:
             line["long"] = bench_long(dev)
