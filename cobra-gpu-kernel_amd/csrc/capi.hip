@@ -126,7 +126,8 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
 
 int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked) {
   if (!layer_shape_ok(batch, seq_len, d_model, heads)) return -1;
-  return !masked && cobra::layer_small_ok(seq_len, d_model, heads) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
+  (void)masked;  // both plans take a token mask
+  return cobra::layer_small_ok(seq_len, d_model, heads) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
 }
 
 int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked) {
@@ -154,6 +155,7 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     if (T == 0) return 0;
     cobra::SmallLayerArgs a{x,     x_dtype, w_qkv, b_qkv, w_o,     b_o,     ln1_w,     ln1_b,   ln2_w, ln2_b,
                             y,     resid_out, batch, seq_len, d_model, heads, causal ? 1 : 0, eps, s};
+    a.valid_mask = valid_mask;
     return code(cobra::run_layer_small(a));
   }
   const LayerBuffers lb = layer_buffers(batch, seq_len, D, masked);

@@ -119,6 +119,7 @@ struct SmallLayerArgs {
   int causal;
   float eps;
   hipStream_t stream;
+  const uint8_t* valid_mask = nullptr;  // optional [B, S] token mask, 0 = padded
 };
 bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads);
 hipError_t run_layer_small(const SmallLayerArgs& a);

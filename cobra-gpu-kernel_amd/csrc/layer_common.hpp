@@ -47,6 +47,54 @@ __device__ __forceinline__ f16x8 half_to_f16(const f32x16& acc, int half, const 
   return o;
 }
 
+// ---- token masks in the fused kernels (S <= 128) ----------------------------
+// The validity of the (at most 128) keys of a sequence lives in two wave-uniform
+// 64-bit words: lane j reads the mask bytes of keys j and 64 + j, and the two
+// ballots are the words.  Keys past S count as padded.
+struct KeyBytes {
+  uint8_t lo, hi;
+};
+__device__ __forceinline__ KeyBytes load_key_bytes(const uint8_t* __restrict__ mrow, int S, int lane) {
+  return {mrow[min(lane, S - 1)], mrow[min(64 + lane, S - 1)]};
+}
+// (Selects, not array indexing: a per-lane index into a private array makes the
+// compiler move the array to LDS, and an LDS store behind in-flight LDS-DMA
+// costs a wait for every transfer.)
+struct KeyBits {
+  uint64_t lo, hi;  // keys 0..63, 64..127
+  // bits of keys 32t .. 32t+31 (t < 4)
+  __device__ __forceinline__ uint32_t tile(int t) const { return (uint32_t)((t < 2 ? lo : hi) >> (32 * (t & 1))); }
+  __device__ __forceinline__ bool valid(int key) const { return ((key < 64 ? lo : hi) >> (key & 63)) & 1; }
+};
+__device__ __forceinline__ KeyBits key_bits_of(KeyBytes kb, int S, int lane) {
+  return {__builtin_amdgcn_ballot_w64(lane < S && kb.lo != 0), __builtin_amdgcn_ballot_w64(64 + lane < S && kb.hi != 0)};
+}
+
+// Padded keys of a 32-key score tile in the S^T = K Q^T layout (register r of
+// lane (li, g) holds key 8(r/4) + 4g + r%4 of the tile) get -inf.
+__device__ __forceinline__ void mask_key_tile(f32x16& s, uint32_t tile_bits, int g) {
+  const uint32_t lw = tile_bits >> (4 * g);
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (!((lw >> (8 * (r >> 2) + (r & 3))) & 1)) s[r] = kNegInf;
+}
+
+// One step of the exact two-block softmax when keys may be masked: a query's
+// running max starts at -inf and is set by the first block with a valid key
+// for it; until then every probability is exp2(-inf) = 0.  Returns the offset
+// the block's probabilities are taken against and the rescale of the
+// running sum / output (0 while nothing was accumulated).
+struct SoftmaxStep {
+  float m_use, alpha;
+};
+__device__ __forceinline__ SoftmaxStep masked_softmax_step(float& m_run, float block_max_scaled) {
+  const float m_new = fmaxf(m_run, block_max_scaled);
+  const float m_use = m_new == kNegInf ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+  m_run = m_new;
+  return {m_use, alpha};
+}
+
 constexpr int kSmallMaxS = 128;
 constexpr int kSmallWaves = kSmallMaxS / 32;  // one wave per 32-token tile; always launched in full
 constexpr int kLdsBytes = 163840;  // gfx950: LDS per workgroup

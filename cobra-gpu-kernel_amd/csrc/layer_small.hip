@@ -62,14 +62,14 @@ struct SmallLds {
   static_assert(CORE * 16 <= kLdsBytes, "weights + K/V must fit the workgroup's LDS");
 };
 
-template <int D, int HD, bool CAUSAL, typename TX>
+template <int D, int HD, bool CAUSAL, bool MASKED, typename TX>
 __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
                                                           const float* __restrict__ bqkv, const f16* __restrict__ wo,
                                                           const float* __restrict__ bo, const float* __restrict__ g1,
                                                           const float* __restrict__ be1, const float* __restrict__ g2,
                                                           const float* __restrict__ be2, TX* __restrict__ y,
                                                           float* __restrict__ resid_out, int B, int S, float c2,
-                                                          float eps) {
+                                                          float eps, const uint8_t* __restrict__ vmask) {
   using L = SmallLds<D, HD>;
   constexpr int KD = L::KD;     // k-steps over d_model
   constexpr int NH = D / HD;    // heads
@@ -140,9 +140,13 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
 
   using Raw8 = typename XChunks<TX>::c8;
   using Raw4 = typename XChunks<TX>::c4;
-  // LN1 input of the next sequence, loaded one sequence ahead.
+  // LN1 input (and token mask bytes) of the next sequence, loaded one sequence ahead.
   Raw8 xpre[KD];
+  KeyBytes kpre{1, 1};
   auto load_ln1_input = [&](int sq) {
+    if constexpr (MASKED) {
+      if (sq < B) kpre = load_key_bytes(vmask + (int64_t)sq * S, S, lane);
+    }
     const TX* xr = x + ((int64_t)sq * S + tok) * D + 8 * g;
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) {
@@ -158,6 +162,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
 
   for (int seq = blockIdx.x; seq < B; seq += gridDim.x) {
     const int64_t row = (int64_t)seq * S + tok;
+    KeyBits kbits{~0ull, ~0ull};
+    if constexpr (MASKED) kbits = key_bits_of(kpre, S, lane);
     const TX* xrow = x + row * D;
     const float *gamma1, *beta1, *gamma2, *beta2, *bias_o, *bias_qkv;
     if constexpr (L::PARAMS) {
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
       f32x16 ot[NDT];
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) ot[dt] = zero16();
-      float m_run = 0.f, l = 0.f;
+      float m_run = MASKED ? kNegInf : 0.f, l = 0.f;
       // Every key tile is computed, branch-free: all four waves always write their
       // K/V slots (finite values, also past S), and masked keys get p = 0.  The
       // wasted tiles cost no latency -- the slowest wave bounds every barrier.
@@ -288,13 +294,23 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
             for (int r = 0; r < 16; ++r)
               if (8 * (r >> 2) + (r & 3) >= lim) sacc[u][r] = kNegInf;
           }
+          if constexpr (MASKED) {
+            if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc[u], kbits.tile(t), g);
+          }
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
         }
         mx = max_xor32(mx);
-        const float m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);  // block 0 always holds key 0
-        const float alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
+        float m_new, alpha;
+        if constexpr (MASKED) {
+          const SoftmaxStep st = masked_softmax_step(m_run, mx * c2);
+          m_new = st.m_use;
+          alpha = st.alpha;
+        } else {
+          m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);  // block 0 always holds key 0
+          alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
+        }
         f16x8 pB[2][2];
         float ps = 0.f;
 #pragma unroll
@@ -323,7 +339,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
               ot[dt] = mfma32x32x16(Vl[(((2 * blk + u) * NDT + dt) * 2 + half) * 64 + lane], pB[u][half], ot[dt]);
       }
       l = sum_xor32(l);
-      const float inv = __builtin_amdgcn_rcpf(l);
+      // A query with no valid key (only a padded one) gets a zero row.
+      const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -359,6 +376,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
     // ---- r = out + b_o + x;  y = LN2(r) ------------------------------------------
     float v[NNT][4][4];
     float s = 0.f;
+    // A padded token's attention output is zero (masked_fill before the residual add).
+    const bool tv = !MASKED || kbits.valid(tok);
 #pragma unroll
     for (int nt = 0; nt < NNT; ++nt)
 #pragma unroll
@@ -367,7 +386,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
         const f32x4 bb = *reinterpret_cast<const f32x4*>(bias_o + n0);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[nt][qd][e] = oacc[nt][4 * qd + e] + bb[e] + (float)xres[nt][qd][e];
+          v[nt][qd][e] = (tv ? oacc[nt][4 * qd + e] + bb[e] : 0.f) + (float)xres[nt][qd][e];
           s += v[nt][qd][e];
         }
       }
@@ -418,10 +437,16 @@ bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads) {
 template <int D, int HD, bool CAUSAL, typename TX>
 static hipError_t launch_small(const SmallLayerArgs& a, float c2) {
   const int64_t grid = a.batch < compute_units() ? a.batch : compute_units();
-  hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, TX>), dim3((unsigned)grid), dim3(64 * kSmallWaves), 0, a.stream,
-                     static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
-                     static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
-                     static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps);
+  if (a.valid_mask)
+    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, true, TX>), dim3((unsigned)grid), dim3(64 * kSmallWaves), 0,
+                       a.stream, static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
+                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
+                       static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps, a.valid_mask);
+  else
+    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, false, TX>), dim3((unsigned)grid), dim3(64 * kSmallWaves), 0,
+                       a.stream, static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
+                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
+                       static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps, nullptr);
   return hipGetLastError();
 }
 

@@ -108,12 +108,12 @@ __device__ __forceinline__ f16x8 tile_chunk(const char* tile, int r, int c) {
 
 }  // namespace
 
-template <int D, int HD, bool CAUSAL>
+template <int D, int HD, bool CAUSAL, bool MASKED>
 __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     const f16* __restrict__ x, const f16* __restrict__ wqkv, const float* __restrict__ bqkv,
     const f16* __restrict__ wo, const float* __restrict__ bo, const float* __restrict__ g1,
     const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, f16* __restrict__ y,
-    float* __restrict__ resid_out, int S, int NS, float c2, float eps) {
+    float* __restrict__ resid_out, int S, int NS, float c2, float eps, const uint8_t* __restrict__ vmask) {
   using P = SplitPlan<D, HD>;
   constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH;
 
@@ -147,6 +147,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   char* const rWq = rQ + hq * NDT * P::TILEB;
   char* const rWo = rQ + dq * P::TILEB;
   char* const rTok = rX + w * P::TILEB;
+
+  // Token mask bytes first: the oldest transfers, so every later vmcnt wait covers them.
+  KeyBytes kbytes{1, 1};
+  if constexpr (MASKED) {
+    kbytes = load_key_bytes(vmask + (int64_t)b * S, S, lane);
+    asm volatile("" ::: "memory");
+  }
 
   // ---- DMA, in the order the data is needed -------------------------------------------
   {  // [gamma1 | beta1]
@@ -185,6 +192,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 
   // ---- LN1 of token 32w + li (columns 16kk + 8g + e): its tile and parameters are in.
   wait_vmcnt<1 + P::N_A + P::N_Q + P::N_R>();
+  KeyBits kbits{~0ull, ~0ull};
+  if constexpr (MASKED) kbits = key_bits_of(kbytes, S, lane);
   {
     float xv[KD][8];
     float sum = 0.f;
@@ -310,7 +319,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     f32x16 ot[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) ot[dt] = zero16();
-    float m_run = 0.f, l = 0.f;
+    float m_run = MASKED ? kNegInf : 0.f, l = 0.f;
 #pragma unroll
     for (int blk = 0; blk < kSplitTiles / 2; ++blk) {
       f32x16 sacc[2];
@@ -330,15 +339,25 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
           for (int r = 0; r < 16; ++r)
             if (8 * (r >> 2) + (r & 3) >= lim) sacc[u][r] = kNegInf;
         }
+        if constexpr (MASKED) {
+          if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc[u], kbits.tile(t), g);
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
       }
       mx = max_xor32(mx);
-      // Block 0 holds key 0, valid for every query, so its max is finite; a fully
-      // masked later block leaves the running max as it is.
-      const float m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);
-      const float alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
+      // Unmasked: block 0 holds key 0, valid for every query, so its max is finite;
+      // a fully masked later block leaves the running max as it is.
+      float m_new, alpha;
+      if constexpr (MASKED) {
+        const SoftmaxStep st = masked_softmax_step(m_run, mx * c2);
+        m_new = st.m_use;
+        alpha = st.alpha;
+      } else {
+        m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);
+        alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+      }
       f16x8 pB[2][2];
       float ps = 0.f;
 #pragma unroll
@@ -368,7 +387,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
                                   pB[u][half], ot[dt]);
     }
     l = sum_xor32(l);
-    const float inv = __builtin_amdgcn_rcpf(l);
+    // A query with no valid key (only a padded one) gets a zero row.
+    const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -392,13 +412,15 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       oacc = mfma32x32x16(a, Cx[ks * 64 + lane], oacc);
     }
+    // A padded query's attention output is zero (masked_fill before the residual add).
+    const bool qv = !MASKED || kbits.valid(qtok);
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
       const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 128 + 8 * qd + 4 * g);
       const f16x4 xr = *reinterpret_cast<const f16x4*>(rR + li * 64 + 16 * (qd ^ ((li >> 2) & 3)) + 8 * g);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[qd][e] = oacc[4 * qd + e] + bb[e] + (float)xr[e];
+        v[qd][e] = (qv ? oacc[4 * qd + e] + bb[e] : 0.f) + (float)xr[e];
         sum += v[qd][e];
       }
     }
@@ -459,10 +481,16 @@ static hipError_t launch_split(const SmallLayerArgs& a, float c2) {
   const int ns = (int)((a.seq_len + 31) / 32);
   const int64_t grid = a.batch * ns;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((layer_split_kernel<D, HD, CAUSAL>), dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream,
-                     static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
-                     static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
-                     static_cast<f16*>(a.y), a.resid_out, (int)a.seq_len, ns, c2, a.eps);
+  if (a.valid_mask)
+    hipLaunchKernelGGL((layer_split_kernel<D, HD, CAUSAL, true>), dim3((unsigned)grid), dim3(64 * kSplitWaves), 0,
+                       a.stream, static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
+                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
+                       static_cast<f16*>(a.y), a.resid_out, (int)a.seq_len, ns, c2, a.eps, a.valid_mask);
+  else
+    hipLaunchKernelGGL((layer_split_kernel<D, HD, CAUSAL, false>), dim3((unsigned)grid), dim3(64 * kSplitWaves), 0,
+                       a.stream, static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
+                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
+                       static_cast<f16*>(a.y), a.resid_out, (int)a.seq_len, ns, c2, a.eps, nullptr);
   return hipGetLastError();
 }
 

@@ -128,9 +128,10 @@ enum {
 
 /*
  * Which plan cobra_layer_fwd runs for this shape, or -1 if the shape is not
- * supported.  FUSED covers unmasked calls with seq_len <= 128 and d_model 128
- * (head_dim 32 or 64), 64 (32, 64) or 96 (32); masked != 0 (a token mask will
- * be passed) selects STAGED.  Host-only: no device work.  The reference's
+ * supported.  FUSED covers seq_len <= 128 with d_model 128 (head_dim 32 or 64),
+ * 64 (32, 64) or 96 (32), with or without a token mask; `masked` (a token mask
+ * will be passed) only changes the STAGED plan's workspace.  Host-only: no
+ * device work.  The reference's
  * counterpart is the gate set of UserOptimizedTransformer._prepare
  * (TTB:1030-1071).
  */

@@ -41,8 +41,11 @@ def token_mask(B, S, seed, left_aligned):
 @pytest.mark.parametrize(
     "B,S,D,H",
     [
-        (16, 128, 128, 4),   # the headline geometry (fused when unmasked)
-        (3, 17, 96, 3),
+        (16, 128, 128, 4),   # the headline geometry: query-split fused kernel
+        (5, 80, 128, 2),     # query-split, head_dim 64, ragged S
+        (4, 128, 64, 2),     # query-split, d_model 64
+        (300, 128, 128, 4),  # persistent fused kernel (more than two rounds of slices)
+        (3, 17, 96, 3),      # persistent fused kernel, d_model 96
         (3, 333, 128, 2),    # hd 64, several key blocks, 8-wave attention
         (3, 100, 256, 2),    # hd 128, D > 128 (separate LN2 pass)
         (3, 40, 512, 2),     # hd 256 (32-key blocks)
@@ -87,15 +90,37 @@ def test_masked_graph_replays_with_new_masks():
     assert mod._graph is not None
 
 
-def test_all_valid_mask_equals_no_mask():
-    ref, mod = build_pair(128, 4)
-    x = make_input(8, 128, 128, seed=5).half().to(DEV)
+@pytest.mark.parametrize("B,S,D,H", [(8, 128, 128, 4), (300, 128, 128, 4), (4, 200, 128, 4)])
+def test_all_valid_mask_equals_no_mask(B, S, D, H):
+    """An all-true mask gives the unmasked result bit for bit (fused kernels, both
+    variants, and the staged plan)."""
+    ref, mod = build_pair(D, H)
+    x = make_input(B, S, D, seed=5).half().to(DEV)
     with torch.inference_mode():
-        a = mod(x).float()
-        b = mod(x, torch.ones(8, 128, dtype=torch.bool, device=DEV)).float()
+        a = mod(x).clone()
+        b = mod(x, torch.ones(B, S, dtype=torch.bool, device=DEV))
         torch.cuda.synchronize()
-    assert mod.plan == 1  # a mask selects the staged plan
-    res = compare_outputs(a.cpu(), b.cpu())
+    assert torch.equal(a, b)
+
+
+def test_fused_masked_fp32_io():
+    """fp32 activations run the persistent fused kernel; masked against the masked oracle."""
+    from cobra_amd import CobraAttentionSublayer
+    from oracle import make_sublayer
+    from oracle.cases import oracle_forward
+
+    ref = make_sublayer(128, 4, seed=0)
+    mod = CobraAttentionSublayer(128, 4)
+    mod.load_state_dict(ref.state_dict())
+    mod = mod.to(DEV).eval()
+    x = make_input(6, 128, 128, seed=8)
+    m = token_mask(6, 128, seed=3, left_aligned=False)
+    with torch.inference_mode():
+        y = mod(x.to(DEV), m.to(DEV), causal=True)
+        torch.cuda.synchronize()
+    assert mod.plan == 0
+    res = compare_outputs(oracle_forward(ref, x, causal=True, valid_token_mask=m), y.cpu())
+    log(f"[mask fp32] max_abs={res.max_abs_error:.3e} failed={res.failed_elements}")
     assert res.passed, res
 
 

@@ -51,7 +51,7 @@ def test_argument_validation_rejects_before_any_launch():
     assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10, 0) == -1      # head_dim 12
     assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0) > 0     # staged plan (head_dim 8)
     assert lib.cobra_layer_plan(2, 16, 128, 4, 0) == _lib.PLAN_FUSED
-    assert lib.cobra_layer_plan(2, 16, 128, 4, 1) == _lib.PLAN_STAGED  # token masks run staged
+    assert lib.cobra_layer_plan(2, 16, 128, 4, 1) == _lib.PLAN_FUSED  # the fused kernels take token masks
 
 
 def test_workspace_size_formula():
@@ -66,7 +66,8 @@ def test_workspace_size_formula():
     # a token mask adds the packed key bits, [B][ceil(S/64)] u64, 256-B aligned
     bits = -(-(32 * 1563 * 8) // 256) * 256
     assert ops.layer_workspace_bytes(32, 100000, 1024, 16, masked=True) == t * d * 2 + t * 3 * d * 2 + t * d * 4 + bits
-    assert ops.layer_workspace_bytes(64, 128, 128, 4, masked=True) == 8192 * 128 * 2 + 8192 * 384 * 2 + 1024
+    assert ops.layer_workspace_bytes(64, 128, 128, 4, masked=True) == 0  # fused: the kernel reads the mask bytes
+    assert ops.layer_workspace_bytes(64, 128, 128, 16, masked=True) == 8192 * 128 * 2 + 8192 * 384 * 2 + 1024
 
 
 def test_plan_selection_per_config():
