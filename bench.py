@@ -233,6 +233,15 @@ def bench_long(dev, steps=2, warmup=1):
             layer(x)
         torch.cuda.synchronize()
         ms = event_ms(lambda: layer(x), steps)
+        # host-resident input (8 sequences, pageable): streamed in chunks with the copies
+        # overlapping compute; the PCIe-inclusive rate, never `value`
+        xh = x[:8].cpu()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        yh = layer(xh)
+        torch.cuda.synchronize()
+        host_ms = (time.perf_counter() - t0) * 1e3
+        del xh, yh
         # the attention kernel alone, on two sequences of the same shape
         p = layer._packed()
         x2 = x[:2].reshape(2 * S, D)
@@ -248,6 +257,10 @@ def bench_long(dev, steps=2, warmup=1):
                        "d_model": D, "heads": H},
             "ms_per_step": ms, "tflops": fl / (ms / 1e3) / 1e12,
             "mfma_frac": fl / (ms / 1e3) / 1e12 / PEAK_FP16_TFLOPS, "steps": steps, "warmup": warmup,
+            "host_resident_8seq": {"ms": host_ms, "tflops": fl / 4 / (host_ms / 1e3) / 1e12,
+                                   "device_resident_ms_same_work": ms / 4,
+                                   "note": "pageable host input and output, 4 chunks of 2 sequences, H2D/D2H and "
+                                           "host staging copies overlapped with compute (PCIe-inclusive)"},
             "roofline": roofline("attn_fwd_kernel (per sequence)", a_fl, 4 * S * D * 2, a_ms)}
 
 

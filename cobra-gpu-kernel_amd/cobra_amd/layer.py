@@ -99,6 +99,8 @@ class CobraAttentionSublayer(nn.Module):
         # a single-kernel plan launches directly, which measures ~4x cheaper than
         # replaying a one-node graph); True / False force it.
         self.graph = graph
+        # Upper bound on sequences per device pass when a batch is streamed (None: from free memory).
+        self.stream_chunk: Optional[int] = None
         self.plan: Optional[int] = None
         self._params = list(self.parameters())
         self._versioned = [not p.is_inference() for p in self._params]
@@ -271,20 +273,43 @@ class CobraAttentionSublayer(nn.Module):
                 raise TypeError(f"valid_token_mask must be bool or uint8, got {valid_token_mask.dtype}")
         free, _ = torch.cuda.mem_get_info(dev)
         step = streaming.plan_chunk(B, self._per_seq_bytes(x, return_residual), free)
+        if self.stream_chunk:
+            step = max(1, min(step, int(self.stream_chunk)))
         y_all = torch.empty_like(x)
         r_all = torch.empty(x.shape, dtype=torch.float32, device=x.device) if return_residual else None
         ws_cache = {}
 
-        def run_chunk(b0: int, b1: int) -> None:
-            xc = x[b0:b1]
-            xc = xc.to(dev, non_blocking=True) if host else xc.contiguous()
-            n = b1 - b0
-            mc = self._mask_bytes(valid_token_mask[b0:b1], xc) if masked else None
+        def workspace(n: int) -> torch.Tensor:
             if n not in ws_cache:
                 ws_cache.clear()
                 ws_cache[n] = torch.empty(ops.layer_workspace_bytes(n, S, D, self.attention.num_heads, masked),
                                           dtype=torch.uint8, device=dev)
-            out = self._run_eager(xc, mc, pack, causal, return_residual, ws=ws_cache[n])
+            return ws_cache[n]
+
+        def on_oom() -> None:
+            ws_cache.clear()
+            gc.collect()
+            torch.cuda.empty_cache()
+
+        def is_oom(e: BaseException) -> bool:
+            return isinstance(e, torch.cuda.OutOfMemoryError)
+
+        if host:
+            # Copies in and out overlap the compute of neighbouring chunks.
+            def run(xd, md):
+                mc = self._mask_bytes(md, xd) if masked else None
+                out = self._run_eager(xd, mc, pack, causal, return_residual, ws=workspace(xd.shape[0]))
+                return out if return_residual else (out,)
+
+            outs = [r_all, y_all] if return_residual else [y_all]
+            streaming.stream_host(x, valid_token_mask, outs, streaming.host_chunk(B, step), run, dev, is_oom,
+                                  on_oom)
+            return (r_all, y_all) if return_residual else y_all
+
+        def run_chunk(b0: int, b1: int) -> None:
+            xc = x[b0:b1].contiguous()
+            mc = self._mask_bytes(valid_token_mask[b0:b1], xc) if masked else None
+            out = self._run_eager(xc, mc, pack, causal, return_residual, ws=workspace(b1 - b0))
             if return_residual:
                 r_all[b0:b1].copy_(out[0])
                 y_all[b0:b1].copy_(out[1])
@@ -296,6 +321,5 @@ class CobraAttentionSublayer(nn.Module):
             gc.collect()
             torch.cuda.empty_cache()
 
-        streaming.run_chunked(B, step, run_chunk, on_oom,
-                              lambda e: isinstance(e, torch.cuda.OutOfMemoryError))
+        streaming.run_chunked(B, step, run_chunk, on_oom, is_oom)
         return (r_all, y_all) if return_residual else y_all

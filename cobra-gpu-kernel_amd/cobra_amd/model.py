@@ -114,6 +114,8 @@ class CobraTransformer(nn.Module):
         self.final_norm = nn.LayerNorm(config.d_model)
         # hipGraph replay: None = automatic (inputs <= 64 MiB), True / False force it.
         self.graph = graph
+        # Upper bound on sequences per device pass when a batch is streamed (None: from free memory).
+        self.stream_chunk: Optional[int] = None
         self._params = list(self.parameters())
         self._versioned = [not p.is_inference() for p in self._params]
         self._packs: Optional[List[_BlockPack]] = None
@@ -267,22 +269,32 @@ class CobraTransformer(nn.Module):
         dev = self.final_norm.weight.device
         packs = self._packed()
         B = x.shape[0]
-        host = not x.is_cuda
         free, _ = torch.cuda.mem_get_info(dev)
         step = streaming.plan_chunk(B, self._per_seq_bytes(x), free)
+        if self.stream_chunk:
+            step = max(1, min(step, int(self.stream_chunk)))
         out = torch.empty_like(x)
-
-        def run_chunk(b0: int, b1: int) -> None:
-            xc = x[b0:b1]
-            xc = xc.to(dev, non_blocking=True) if host else xc.contiguous()
-            mc = None
-            if valid_token_mask is not None:
-                mc = self._mask_bytes(valid_token_mask[b0:b1], xc)
-            out[b0:b1].copy_(self._run(xc, mc, packs))
 
         def on_oom() -> None:
             gc.collect()
             torch.cuda.empty_cache()
 
-        streaming.run_chunked(B, step, run_chunk, on_oom, lambda e: isinstance(e, torch.cuda.OutOfMemoryError))
+        def is_oom(e: BaseException) -> bool:
+            return isinstance(e, torch.cuda.OutOfMemoryError)
+
+        if not x.is_cuda:
+            # Copies in and out overlap the compute of neighbouring chunks.
+            def run(xd, md):
+                return (self._run(xd, None if md is None else self._mask_bytes(md, xd), packs),)
+
+            streaming.stream_host(x, valid_token_mask, [out], streaming.host_chunk(B, step), run, dev, is_oom,
+                                  on_oom)
+            return out
+
+        def run_chunk(b0: int, b1: int) -> None:
+            xc = x[b0:b1].contiguous()
+            mc = None if valid_token_mask is None else self._mask_bytes(valid_token_mask[b0:b1], xc)
+            out[b0:b1].copy_(self._run(xc, mc, packs))
+
+        streaming.run_chunked(B, step, run_chunk, on_oom, is_oom)
         return out

@@ -81,3 +81,109 @@ def run_chunked(
         done.append((b0, b1))
         b0 = b1
     return done
+
+
+# ---- host-resident batches: copies overlapped with compute ---------------------------
+
+HOST_MIN_CHUNKS = 4  # a host-resident batch is cut into at least this many chunks when it can be
+
+
+def host_chunk(batch: int, device_step: int, min_chunks: int = HOST_MIN_CHUNKS) -> int:
+    """Chunk size for a host-resident batch: what the device holds, but small enough
+    that the copies of one chunk can overlap the compute of its neighbours."""
+    return max(1, min(device_step, -(-batch // min_chunks)))
+
+
+def stream_host(x, mask, outs, step: int, run, dev, is_oom, on_oom) -> None:
+    """Run a host-resident batch through the GPU in chunks, filling the host tensors ``outs``.
+
+    ``x``: host [B, ...]; ``mask``: [B, S] (host or device) or None; ``run(xd, md)``
+    returns one device tensor per entry of ``outs``.  Two slots of pinned staging and
+    device buffers: while chunk i computes on the current stream, a copy stream (default
+    priority) brings chunk i+1 in and takes chunk i-1 out, and the host copies between
+    pageable and pinned memory run on the CPU in the meantime.  Out of memory: drain,
+    halve the chunk, resume at the first chunk whose result was not written.
+    """
+    import torch
+
+    B = x.shape[0]
+    compute = torch.cuda.current_stream(dev)
+    copy = torch.cuda.Stream(dev)
+    pinned_x = x.is_pinned()
+    slots = []
+
+    def new_slot(n):
+        s = {"n": n, "pending": None}
+        s["pin_in"] = None if pinned_x else torch.empty((n,) + tuple(x.shape[1:]), dtype=x.dtype, pin_memory=True)
+        s["dev_in"] = torch.empty((n,) + tuple(x.shape[1:]), dtype=x.dtype, device=dev)
+        if mask is not None:
+            s["dev_m"] = torch.empty((n,) + tuple(mask.shape[1:]), dtype=mask.dtype, device=dev)
+            s["pin_m"] = None if mask.is_cuda else torch.empty((n,) + tuple(mask.shape[1:]), dtype=mask.dtype,
+                                                                pin_memory=True)
+        s["pin_out"] = [torch.empty((n,) + tuple(o.shape[1:]), dtype=o.dtype, pin_memory=True) for o in outs]
+        s["ev_in"] = torch.cuda.Event()
+        s["ev_out"] = torch.cuda.Event()
+        return s
+
+    def drain(s):
+        if s["pending"] is None:
+            return
+        c0, c1 = s["pending"]
+        s["ev_out"].synchronize()
+        for o, p in zip(outs, s["pin_out"]):
+            o[c0:c1].copy_(p[: c1 - c0])
+        s["pending"] = None
+
+    c0 = 0
+    while c0 < B:
+        if not slots or slots[0]["n"] < step:
+            slots = [new_slot(step), new_slot(step)]
+        i = 0
+        try:
+            while c0 < B:
+                c1 = min(c0 + step, B)
+                n = c1 - c0
+                s = slots[i % 2]
+                drain(s)  # chunk i-2: its copy-in, compute and copy-out are all done after this
+                src = x[c0:c1]
+                if not pinned_x:
+                    s["pin_in"][:n].copy_(src)
+                    src = s["pin_in"][:n]
+                with torch.cuda.stream(copy):
+                    s["dev_in"][:n].copy_(src, non_blocking=True)
+                    if mask is not None:
+                        msrc = mask[c0:c1]
+                        if s["pin_m"] is not None:
+                            s["pin_m"][:n].copy_(msrc)
+                            msrc = s["pin_m"][:n]
+                        s["dev_m"][:n].copy_(msrc, non_blocking=True)
+                    s["ev_in"].record(copy)
+                compute.wait_event(s["ev_in"])
+                ys = run(s["dev_in"][:n], s["dev_m"][:n] if mask is not None else None)
+                done = torch.cuda.Event()
+                done.record(compute)
+                with torch.cuda.stream(copy):
+                    copy.wait_event(done)
+                    for y, p in zip(ys, s["pin_out"]):
+                        y.record_stream(copy)  # the allocator must not hand y out again before this copy
+                        p[:n].copy_(y, non_blocking=True)
+                    s["ev_out"].record(copy)
+                s["pending"] = (c0, c1)
+                i += 1
+                c0 = c1
+            for k in (i % 2, (i + 1) % 2):  # the older pending chunk first
+                drain(slots[k])
+        except BaseException as exc:  # noqa: BLE001 - re-raised unless it is an OOM we can absorb
+            if not is_oom(exc):
+                raise
+            # Older chunks still pending are complete once the device is idle: write
+            # them out, then retry from the failed chunk (c0), which was not.
+            torch.cuda.synchronize(dev)
+            for s in slots:
+                drain(s)
+            slots = []
+            on_oom()
+            if step == 1:
+                raise
+            step = max(1, step // 2)
+    torch.cuda.current_stream(dev).wait_stream(copy)
