@@ -267,22 +267,32 @@ def bench_long(dev, steps=2, warmup=1):
 MODEL_CASES = [  # the reference's whole-model cases (tools/sweep.py:31-47): #, B, S, D, H, F, layers (causal)
     ("case1", 64, 128, 128, 4, 128, 4), ("case8", 64, 128, 1024, 4, 1024, 4), ("case13", 64, 1024, 128, 4, 128, 4),
 ]
+# The full matrix of tools/sweep.py:31-47 (``--matrix``); case 14 runs with 8 of its 32
+# sequences (one forward is ~2.8 s at full batch).
+MATRIX_CASES = [
+    ("case1", 64, 128, 128, 4, 128, 4), ("case2", 1, 128, 128, 4, 128, 4), ("case3", 4, 128, 128, 4, 128, 4),
+    ("case4", 16, 128, 128, 4, 128, 4), ("case5", 128, 128, 128, 4, 128, 4), ("case6", 10000, 128, 128, 4, 128, 4),
+    ("case7", 64, 128, 32, 4, 32, 4), ("case8", 64, 128, 1024, 4, 1024, 4), ("case9", 64, 128, 128, 1, 128, 4),
+    ("case10", 64, 128, 128, 2, 128, 4), ("case11", 64, 128, 128, 16, 128, 4), ("case12", 64, 32, 128, 4, 128, 4),
+    ("case13", 64, 1024, 128, 4, 128, 4), ("case14_8seq", 8, 100000, 1024, 16, 1024, 2),
+]
 
 
-def bench_model(dev, iters=20):
-    """The whole ``CobraTransformer`` stack (hipGraph replay for these sizes), causal, fp16."""
+def bench_model(dev, iters=20, cases=MODEL_CASES):
+    """The whole ``CobraTransformer`` stack (hipGraph replay for inputs <= 64 MiB), causal, fp16."""
     from cobra_amd import CobraTransformer, TransformerConfig
 
     out = {}
-    for name, B, S, D, H, F, L in MODEL_CASES:
+    for name, B, S, D, H, F, L in cases:
+        n = 1 if B * S * D >= 100_000_000 else iters
         torch.manual_seed(0)
         model = CobraTransformer(TransformerConfig(B, S, D, H, F, L, True)).to(device=dev,
                                                                                 dtype=torch.float16).eval()
         x = torch.randn(B, S, D, device=dev, dtype=torch.float16)
         with torch.inference_mode():
-            for _ in range(3):
+            for _ in range(3 if n > 1 else 1):
                 model(x)
-            ms = statistics.median([event_ms(lambda: model(x), iters) for _ in range(3)])
+            ms = statistics.median([event_ms(lambda: model(x), n) for _ in range(3)])
         T = B * S
         fl = L * (8 * T * D * D + 2 * B * S * S * D + 4 * T * D * F)  # causal attention: half the S^2 work
         out[name] = {"B": B, "S": S, "D": D, "H": H, "ffn_dim": F, "layers": L, "causal": True,
@@ -334,6 +344,8 @@ def main() -> int:
     ap.add_argument("--no-long", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--matrix", action="store_true",
+                    help="time CobraTransformer on the reference's whole-model case matrix and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -344,6 +356,9 @@ def main() -> int:
         return 2
 
     dev = torch.device("cuda:0")
+    if args.matrix:
+        print(json.dumps({"matrix": bench_model(torch.device("cuda:0"), cases=MATRIX_CASES)}), flush=True)
+        return 0
     if args.pmc_driver:
         pmc_driver(dev)
         return 0
