@@ -47,6 +47,9 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_f32,
          _vp],
     ),
+    "cobra_ln_linear_fwd": (
+        _c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_f32, _vp],
+    ),
     "cobra_mask_bits": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "cobra_attn_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp]),
     "cobra_layer_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),

@@ -224,6 +224,38 @@ def linear_ln(
     return out, normed
 
 
+def ln_linear_ok(d: int, x_dtype: torch.dtype) -> bool:
+    """Whether ``ln_linear`` covers rows of width d (one k-tile per row)."""
+    return d in (64, 128) and x_dtype in (torch.float16, torch.float32)
+
+
+def ln_linear(x: torch.Tensor, w_ln: torch.Tensor, b_ln: torch.Tensor, w: torch.Tensor,
+              bias: Optional[torch.Tensor], eps: float = 1e-5) -> torch.Tensor:
+    """``LayerNorm(x) @ w.T + bias`` in one kernel, fp16 out; the normalised rows
+    never reach memory.  Stands for ``_tl_add_ln`` followed by ``F.linear``
+    (TTB:1216-1234).  x: [M, d] fp16/fp32 with d 64 or 128; w: [N, d] fp16 with
+    N <= 3d (a QKV projection) and N % 8 == 0.
+    """
+    _dev(x, "x")
+    _dev(w, "w")
+    if x.dim() != 2:
+        raise ValueError("x must be [M, d]")
+    M, d = x.shape
+    if not ln_linear_ok(d, x.dtype):
+        raise ValueError(f"ln_linear needs d 64 or 128 and fp16/fp32 x, got d={d} {x.dtype}")
+    if w.dtype != torch.float16 or w.dim() != 2 or w.shape[1] != d:
+        raise ValueError(f"w must be fp16 [N, {d}]")
+    N = w.shape[0]
+    if N > 3 * d or N % 8:
+        raise ValueError(f"ln_linear needs N <= {3 * d} and N % 8 == 0, got N={N}")
+    gw, gb = _f32_param(w_ln, d, "w_ln"), _f32_param(b_ln, d, "b_ln")
+    b32 = _f32_param(bias, N, "bias") if bias is not None else None
+    out = torch.empty((M, N), device=x.device, dtype=torch.float16)
+    call("cobra_ln_linear_fwd", x.data_ptr(), _dtype_code(x, "x"), gw.data_ptr(), gb.data_ptr(), w.data_ptr(),
+         _ptr(b32), out.data_ptr(), M, N, d, float(eps), _stream(x))
+    return out
+
+
 def mask_bits(mask: torch.Tensor) -> torch.Tensor:
     """[B, S] bool/uint8 token mask -> packed key bits ``[B, ceil(S/64)]`` (int64 storage of u64 words)."""
     if mask.dim() != 2:

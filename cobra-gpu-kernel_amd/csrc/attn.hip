@@ -437,7 +437,9 @@ static hipError_t dispatch_waves(const AttnArgs& a, float c2) {
   // keep 4: the O accumulator already fills the register file.  Key blocks of
   // BN keys (one 1 KB DMA span per wave at least), ST stages deep.
   constexpr int BN = HD >= 256 ? 32 : 64;
-  constexpr int BN8 = HD <= 16 ? 128 : BN;  // 8 waves x one 1 KB span per stage
+  // 8-wave launches: at least one 1 KB span per wave per stage, and for narrow heads
+  // 128-key blocks (half the barriers per key; +7-10 % at head_dim 32, measured)
+  constexpr int BN8 = HD <= 32 ? 128 : BN;
   constexpr int ST = HD >= 128 ? 3 : 4;
   if constexpr (HD <= 64) {
     if (a.seq_len <= 32) return launch_attn<HD, 1, BN, ST, CAUSAL>(a, c2);

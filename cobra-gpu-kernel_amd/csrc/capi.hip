@@ -105,6 +105,17 @@ int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const v
   return code(cobra::run_gemm(g));
 }
 
+int cobra_ln_linear_fwd(const void* x, int x_dtype, const float* gamma, const float* beta, const void* w,
+                        const float* bias, void* c, int64_t M, int64_t N, int64_t d, float eps, void* stream) {
+  if (!x || !gamma || !beta || !w || !c || !is_dtype(x_dtype)) return kBad;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(beta) || !aligned16(w) || !aligned16(c) ||
+      !opt_aligned16(bias))
+    return kBad;
+  if (!cobra::ln_gemm_ok(d, x_dtype) || M < 0 || N <= 0 || N > 0x7fffffff || N % 8 != 0) return kBad;
+  cobra::LnGemmArgs a{x, x_dtype, gamma, beta, w, bias, c, M, (int)N, d, eps, static_cast<hipStream_t>(stream)};
+  return code(cobra::run_ln_gemm(a));
+}
+
 int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int64_t seq_len, void* stream) {
   if (!mask || !key_bits || (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
   if (batch < 0 || seq_len < 0 || seq_len > 0x7fffffff) return kBad;
@@ -167,14 +178,19 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
   void* ctx = h;  // h is dead once the QKV projection has read it
   uint64_t* bits = masked ? reinterpret_cast<uint64_t*>(ws + lb.bits_off) : nullptr;
 
-  cobra::LnArgs ln1{x, x_dtype, nullptr, 0, ln1_w, ln1_b, nullptr, h, kF16, T, (int)D, eps, s};
-  hipError_t e = cobra::run_ln(ln1);
-  if (e != hipSuccess) return code(e);
+  hipError_t e = hipSuccess;
   if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
-
-  cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kF16, qkv, kF16, T, (int)(3 * D), (int)D,
-                       nullptr, nullptr, nullptr, kF16, eps, s};
-  if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
+  if (cobra::ln_gemm_ok(D, x_dtype)) {
+    // LN1 in the QKV projection's prologue: h never goes to memory.
+    cobra::LnGemmArgs proj{x, x_dtype, ln1_w, ln1_b, w_qkv, b_qkv, qkv, T, (int)(3 * D), D, eps, s};
+    if ((e = cobra::run_ln_gemm(proj)) != hipSuccess) return code(e);
+  } else {
+    cobra::LnArgs ln1{x, x_dtype, nullptr, 0, ln1_w, ln1_b, nullptr, h, kF16, T, (int)D, eps, s};
+    if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
+    cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kF16, qkv, kF16, T, (int)(3 * D), (int)D,
+                         nullptr, nullptr, nullptr, kF16, eps, s};
+    if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
+  }
 
   cobra::AttnArgs at{qkv, ctx, batch, (int)seq_len, (int)heads, (int)(D / heads),
                      (float)(1.0 / sqrt((double)(D / heads))), causal ? 1 : 0, s};

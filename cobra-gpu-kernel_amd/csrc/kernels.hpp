@@ -80,6 +80,25 @@ hipError_t run_gemm(const GemmArgs& a);
 bool gemm_dma_ok(const GemmArgs& a);
 hipError_t run_gemm_dma(const GemmArgs& a);
 
+// LayerNorm in the prologue of the projection that consumes it (ln_gemm.hip):
+// c = (LayerNorm(x) * gamma + beta) w^T + bias, rows of d = 64 or 128, fp16 out.
+struct LnGemmArgs {
+  const void* x;           // [M, d], x_dtype
+  int x_dtype;
+  const float* gamma;      // [d]
+  const float* beta;       // [d]
+  const void* w;           // [N, d] fp16
+  const float* bias;       // optional [N]
+  void* c;                 // [M, N] fp16
+  int64_t M;
+  int N;
+  int64_t d;
+  float eps;
+  hipStream_t stream;
+};
+bool ln_gemm_ok(int64_t d, int x_dtype);
+hipError_t run_ln_gemm(const LnGemmArgs& a);
+
 struct AttnArgs {
   const void* qkv;         // [B*S, 3*H*hd] fp16: q | k | v column blocks, head-major inside each
   void* ctx;               // [B*S, H*hd] fp16

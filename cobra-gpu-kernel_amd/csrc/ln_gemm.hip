@@ -1,0 +1,182 @@
+// LayerNorm fused into the prologue of the projection that consumes it, for
+// rows that fit one k-tile (d_model 64 or 128):
+//
+//   h = LayerNorm(x) * gamma + beta   (per row, fp32 statistics, biased variance)
+//   c = h W^T + bias                  (fp16 operands, fp32 accumulate, fp16 out)
+//
+// The reference runs _add_ln_kernel and then the QKV GEMM (TTB:1216-1234), so
+// h makes a round trip through HBM.  Here a workgroup normalises its 128 rows
+// of x straight into the LDS tile the matrix cores read: h never exists in
+// memory.  Row statistics use 8 or 16 lanes per row (DPP reductions); the
+// normalised rows and the W tile sit row-major in LDS with 16-byte chunks
+// XOR-swizzled by row, so every MFMA operand read is conflict-free.  The
+// 128 x 128 fp16 result is staged back through the same LDS and written as
+// whole 256-byte row segments (16 lanes per row), not as the 8-byte quads the
+// accumulator layout would give.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cobra {
+
+namespace {
+
+constexpr int kLgBM = 128, kLgBN = 128, kLgThreads = 256;
+
+template <int D>
+__device__ __forceinline__ int lg_swz(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);  // 16 / 8 chunks per row
+}
+
+}  // namespace
+
+template <int D, typename TX>
+__global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restrict__ x, const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta, const f16* __restrict__ W,
+                                                           const float* __restrict__ bias, f16* __restrict__ C,
+                                                           int64_t M, int N, float eps) {
+  static_assert(D == 64 || D == 128, "one k-tile per row");
+  constexpr int ROWB = D * 2;               // bytes of one fp16 row
+  constexpr int CPR = D / 8;                // 16-byte chunks per row (= lanes per row in the LN)
+  constexpr int RPW = 64 / CPR;             // rows per wave per pass
+  constexpr int PASSES = kLgBM / (4 * RPW);
+  constexpr int WCH = kLgBN * CPR / kLgThreads;  // W chunks per thread
+  constexpr int KS = D / 16;
+  constexpr int OUTB = kLgBN * 2;           // bytes of one staged output row (128 fp16)
+  constexpr int LDSB = (kLgBM + kLgBN) * ROWB > kLgBM * OUTB ? (kLgBM + kLgBN) * ROWB : kLgBM * OUTB;
+  __shared__ __attribute__((aligned(16))) char smem[LDSB];
+  char* const Hs = smem;
+  char* const Ws = smem + kLgBM * ROWB;
+
+  // Row blocks outermost, so the column tiles of a row block (which re-read the
+  // same x rows) run next to each other on one XCD.
+  const int nbn = (N + kLgBN - 1) / kLgBN;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t m0 = (int64_t)(tile / nbn) * kLgBM;
+  const int n0 = (tile % nbn) * kLgBN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, g = lane >> 5;
+
+  // ---- loads: the W tile (rows past N repeat row N-1; never stored) and x rows ------
+  f16x8 wr[WCH];
+#pragma unroll
+  for (int i = 0; i < WCH; ++i) {
+    const int c = tid + i * kLgThreads;
+    const int r = c / CPR, ch = c % CPR;
+    wr[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)min(n0 + r, N - 1) * D + 8 * ch);
+  }
+  const int cl = lane % CPR;  // this lane's 8 columns: 8cl .. 8cl+7
+  float xv[PASSES][8];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int r = (p * 4 + w) * RPW + lane / CPR;
+    load8(x + min(m0 + r, M - 1) * D + 8 * cl, xv[p]);
+  }
+  float gv[8], bv[8];
+  load8(gamma + 8 * cl, gv);
+  load8(beta + 8 * cl, bv);
+#pragma unroll
+  for (int i = 0; i < WCH; ++i) {
+    const int c = tid + i * kLgThreads;
+    const int r = c / CPR, ch = c % CPR;
+    *reinterpret_cast<f16x8*>(Ws + r * ROWB + 16 * (ch ^ lg_swz<D>(r))) = wr[i];
+  }
+  // ---- LayerNorm of every row into the h tile ---------------------------------------
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int r = (p * 4 + w) * RPW + lane / CPR;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += xv[p][e];
+    const float mean = group_sum<CPR>(s) * (1.0f / D);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float t = xv[p][e] - mean;
+      q += t * t;
+    }
+    const float rstd = rsqrtf(group_sum<CPR>(q) * (1.0f / D) + eps);
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[p][e] - mean) * rstd * gv[e] + bv[e]);
+    *reinterpret_cast<f16x8*>(Hs + r * ROWB + 16 * (cl ^ lg_swz<D>(r))) = h;
+  }
+  __syncthreads();
+
+  // ---- c^T tiles: wave (wm, wn) owns rows 64wm.., columns 64wn.. -------------------
+  const int wm = w >> 1, wn = w & 1;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) acc[j][i] = zero16();
+  const int sw = lg_swz<D>(li);  // rows 32k + li share the swizzle of li
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const int co = 16 * ((2 * kk + g) ^ sw);
+    f16x8 af[2], wf[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const f16x8*>(Hs + (64 * wm + 32 * i + li) * ROWB + co);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) wf[j] = *reinterpret_cast<const f16x8*>(Ws + (64 * wn + 32 * j + li) * ROWB + co);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) acc[j][i] = mfma32x32x16(wf[j], af[i], acc[j][i]);
+  }
+  __syncthreads();  // every operand read is done: the LDS becomes the output staging tile
+
+  // ---- + bias into a [128][128] fp16 staging tile (16-byte chunk c of row r at
+  // c ^ (r & 15)), then whole row segments to C --------------------------------------------
+  // lane li of (i, j) holds row 64wm + 32i + li, columns 64wn + 32j + 8q + 4g + {0..3}
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = 64 * wn + 32 * j + 8 * q + 4 * g;
+      const int n = n0 + col;
+      const f32x4 bq = (bias && n < N) ? *reinterpret_cast<const f32x4*>(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = 64 * wm + 32 * i + li;
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (f16)(acc[j][i][4 * q + e] + bq[e]);
+        *reinterpret_cast<f16x4*>(smem + row * OUTB + 16 * ((col >> 3) ^ (row & 15)) + 8 * g) = o;
+      }
+    }
+  __syncthreads();
+  constexpr int CH = OUTB / 16;  // 16 chunks per staged row
+#pragma unroll
+  for (int it = 0; it < kLgBM * CH / kLgThreads; ++it) {
+    const int idx = tid + it * kLgThreads;
+    const int row = idx / CH, c = idx % CH;
+    const int64_t m = m0 + row;
+    const int n = n0 + 8 * c;
+    if (m < M && n < N)  // N % 8 == 0: a chunk is all in or all out
+      *reinterpret_cast<f16x8*>(C + m * N + n) =
+          *reinterpret_cast<const f16x8*>(smem + row * OUTB + 16 * (c ^ (row & 15)));
+  }
+}
+
+template <int D, typename TX>
+static hipError_t launch_ln_gemm(const LnGemmArgs& a) {
+  const int64_t tiles = ((a.M + kLgBM - 1) / kLgBM) * (int64_t)((a.N + kLgBN - 1) / kLgBN);
+  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((ln_gemm_kernel<D, TX>), dim3((unsigned)tiles), dim3(kLgThreads), 0, a.stream,
+                     static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
+                     static_cast<f16*>(a.c), a.M, a.N, a.eps);
+  return hipGetLastError();
+}
+
+bool ln_gemm_ok(int64_t d, int x_dtype) { return (d == 64 || d == 128) && (x_dtype == kF16 || x_dtype == kF32); }
+
+hipError_t run_ln_gemm(const LnGemmArgs& a) {
+  if (!ln_gemm_ok(a.d, a.x_dtype) || a.M < 0 || a.N <= 0 || a.N % 8 != 0 || a.N > 3 * a.d) return hipErrorInvalidValue;
+  if (!a.x || !a.w || !a.c || !a.gamma || !a.beta) return hipErrorInvalidValue;
+  if (a.M == 0) return hipSuccess;
+  if (a.d == 128) return a.x_dtype == kF16 ? launch_ln_gemm<128, f16>(a) : launch_ln_gemm<128, float>(a);
+  return a.x_dtype == kF16 ? launch_ln_gemm<64, f16>(a) : launch_ln_gemm<64, float>(a);
+}
+
+}  // namespace cobra

@@ -96,6 +96,18 @@ int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const v
                         void* y, int y_dtype, int64_t M, int64_t N, int64_t K, float eps, void* stream);
 
 /*
+ * LayerNorm fused into the prologue of the projection that consumes it:
+ *     h = (x - mean) * rsqrt(var + eps) * gamma + beta   per row (biased var);
+ *     c = h . w^T + bias                                  (h never stored)
+ * x: [M, d] in x_dtype with d = 64 or 128 (one k-tile per row); gamma, beta:
+ * [d] fp32; w: [N, d] fp16 with N <= 3 d (a QKV projection); bias: [N] fp32
+ * (optional); c: [M, N] fp16.  N % 8 == 0.  Replaces the pair _tl_add_ln -> F.linear of the reference's
+ * layer-0 / pre-attention path (TTB:1216-1234) with one kernel.
+ */
+int cobra_ln_linear_fwd(const void* x, int x_dtype, const float* gamma, const float* beta, const void* w,
+                        const float* bias, void* c, int64_t M, int64_t N, int64_t d, float eps, void* stream);
+
+/*
  * Token mask -> packed key bits for cobra_attn_fwd:
  *     mask: [batch, seq_len] bytes (0 = padded token);
  *     key_bits: [batch][ceil(seq_len / 64)] uint64, 8-byte aligned; bit j of

@@ -346,3 +346,23 @@ def test_invalid_shapes_raise():
         mod(x, torch.ones(2, 7, dtype=torch.bool, device=DEV))  # mask shape
     with pytest.raises(TypeError):
         mod(x, torch.ones(2, 8, dtype=torch.float32, device=DEV))  # mask dtype
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_ln_linear_op(d, xdt):
+    """LayerNorm in the GEMM prologue against fp32 torch (LayerNorm, fp16 rounding of h, GEMM)."""
+    from cobra_amd import ops
+
+    torch.manual_seed(d)
+    for M, N in [(8192, 3 * d), (65536, 3 * d), (1000, 3 * d), (77, 2 * d + 8), (3, 8)]:
+        x = (torch.randn(M, d, device=DEV) * 1.5 + 0.3).to(xdt)
+        g = torch.rand(d, device=DEV) + 0.5
+        be = torch.randn(d, device=DEV) * 0.2
+        w = (torch.randn(N, d, device=DEV) / d ** 0.5).half()
+        b = torch.randn(N, device=DEV)
+        got = ops.ln_linear(x, g, be, w, b)
+        h = torch.nn.functional.layer_norm(x.float(), (d,), g, be, 1e-5).half().float()
+        want = h @ w.float().t() + b
+        err = (got.float() - want).abs().max().item()
+        assert torch.allclose(got.float(), want, atol=4e-3, rtol=4e-3), (d, xdt, M, N, err)
