@@ -273,6 +273,7 @@ hipError_t run_gemm(const GemmArgs& a) {
   if (a.M == 0) return hipSuccess;
   const bool has_resid = a.resid != nullptr;
   if (has_resid && a.resid_dtype != kF16 && a.resid_dtype != kF32) return hipErrorInvalidValue;
+  if (a.ln_gamma && gemm_ln_rows_ok(a)) return run_gemm_ln_rows(a);
   if (a.ln_gamma) {
     if (!a.ln_beta || !a.ln_y || a.N > 128 || a.N % 8 != 0) return hipErrorInvalidValue;
     if (a.c && a.c_dtype != kF32) return hipErrorInvalidValue;

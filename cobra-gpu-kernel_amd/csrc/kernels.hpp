@@ -98,6 +98,10 @@ struct LnGemmArgs {
 };
 bool ln_gemm_ok(int64_t d, int x_dtype);
 hipError_t run_ln_gemm(const LnGemmArgs& a);
+// LayerNorm epilogue for K = 64 / 128 and N = 64 / 128 (ln_gemm.hip); run_gemm
+// routes eligible calls there.
+bool gemm_ln_rows_ok(const GemmArgs& a);
+hipError_t run_gemm_ln_rows(const GemmArgs& a);
 
 struct AttnArgs {
   const void* qkv;         // [B*S, 3*H*hd] fp16: q | k | v column blocks, head-major inside each

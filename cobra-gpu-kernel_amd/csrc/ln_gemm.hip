@@ -159,6 +159,197 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// The epilogue-side counterpart for short K (out-projection at d_model 64 / 128):
+//   r = a W^T + bias (kEpiMaskBranch) + resid (kEpiMaskResid);  resid_out = r;
+//   y = LayerNorm(r) * gamma + beta (kEpiMaskOut)
+// with N = 64 or 128 columns (whole rows per workgroup) and K = 64 or 128 (one
+// k-tile): the a and W tiles are loaded once, the fp32 product (+ bias) is staged
+// in LDS, and a row pass of 16 lanes per row adds the residual, normalises and
+// writes r and y as whole row segments.  Replaces _gemm_ln_kernel / _tl_linear_ln
+// (TTB:394-488) for these shapes; its k loop and per-element residual loads are
+// what the register-staged GEMM's LayerNorm epilogue spends its time on.
+template <int K, int N, int BM, typename TR, typename TY>
+__global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
+    const f16* __restrict__ A, const f16* __restrict__ W, const float* __restrict__ bias, const TR* __restrict__ resid,
+    float* __restrict__ resid_out, const float* __restrict__ gamma, const float* __restrict__ beta, TY* __restrict__ Y,
+    int64_t M, float eps, const uint8_t* __restrict__ row_mask, int epi) {
+  static_assert((K == 64 || K == 128) && (N == 64 || N == 128), "one k-tile, whole rows");
+  constexpr int ROWB = K * 2;
+  constexpr int CPR = K / 8;
+  constexpr int WM = BM >= 64 ? 2 : 1, WN = 4 / WM;  // waves over rows x columns
+  constexpr int WTM = BM / WM, WTN = N / WN;         // wave tile
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+  constexpr int ACH = BM * CPR / kLgThreads, WCH = N * CPR / kLgThreads;
+  static_assert(ACH >= 1 && WCH >= 1 && ACH * kLgThreads == BM * CPR && WCH * kLgThreads == N * CPR, "loads");
+  constexpr int LDC = N + 4;  // fp32 staging row stride
+  constexpr int OPB = (BM + N) * ROWB, EPB = BM * LDC * 4;
+  __shared__ __attribute__((aligned(16))) char smem[OPB > EPB ? OPB : EPB];
+  char* const As = smem;
+  char* const Ws = smem + BM * ROWB;
+  float* const Cs = reinterpret_cast<float*>(smem);
+
+  const int64_t m0 = (int64_t)xcd_remap(blockIdx.x, gridDim.x) * BM;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int li = lane & 31, g = lane >> 5;
+
+  f16x8 ar[ACH], wr[WCH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int c = tid + i * kLgThreads;
+    ar[i] = *reinterpret_cast<const f16x8*>(A + min(m0 + c / CPR, M - 1) * K + 8 * (c % CPR));
+  }
+#pragma unroll
+  for (int i = 0; i < WCH; ++i) {
+    const int c = tid + i * kLgThreads;
+    wr[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)(c / CPR) * K + 8 * (c % CPR));
+  }
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int c = tid + i * kLgThreads, r = c / CPR;
+    *reinterpret_cast<f16x8*>(As + r * ROWB + 16 * ((c % CPR) ^ lg_swz<K>(r))) = ar[i];
+  }
+#pragma unroll
+  for (int i = 0; i < WCH; ++i) {
+    const int c = tid + i * kLgThreads, r = c / CPR;
+    *reinterpret_cast<f16x8*>(Ws + r * ROWB + 16 * ((c % CPR) ^ lg_swz<K>(r))) = wr[i];
+  }
+  __syncthreads();
+
+  const int wm = w / WN, wn = w % WN;
+  f32x16 acc[TN][TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) acc[j][i] = zero16();
+  const int sw = lg_swz<K>(li);
+#pragma unroll
+  for (int kk = 0; kk < K / 16; ++kk) {
+    const int co = 16 * ((2 * kk + g) ^ sw);
+    f16x8 af[TM], wf[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f16x8*>(As + (wm * WTM + 32 * i + li) * ROWB + co);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) wf[j] = *reinterpret_cast<const f16x8*>(Ws + (wn * WTN + 32 * j + li) * ROWB + co);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[j][i] = mfma32x32x16(wf[j], af[i], acc[j][i]);
+  }
+  __syncthreads();  // operands are dead: the LDS becomes the fp32 staging tile
+
+  // product + bias (padded rows' branch zeroed) into Cs[row][col]; lane li of (i, j) holds
+  // row wm*WTM + 32i + li, columns wn*WTN + 32j + 8q + 4g + {0..3}
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = wm * WTM + 32 * i + li;
+    const int64_t m = m0 + row;
+    const bool zero = (epi & kEpiMaskBranch) && m < M && row_mask[m] == 0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = wn * WTN + 32 * j + 8 * q + 4 * g;
+        const f32x4 bq = bias ? *reinterpret_cast<const f32x4*>(bias + col) : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = zero ? 0.f : acc[j][i][4 * q + e] + bq[e];
+        *reinterpret_cast<f32x4*>(Cs + row * LDC + col) = v;
+      }
+  }
+  __syncthreads();
+
+  // row pass: LPR lanes per row, 8 consecutive columns per lane
+  constexpr int LPR = N / 8, RPP = kLgThreads / LPR;
+  static_assert(BM % RPP == 0, "row pass covers the block");
+  const int cl = tid % LPR;
+  float gv[8], bv[8];
+  load8(gamma + 8 * cl, gv);
+  load8(beta + 8 * cl, bv);
+#pragma unroll
+  for (int rr0 = 0; rr0 < BM; rr0 += RPP) {
+    const int row = rr0 + tid / LPR;
+    const int64_t m = m0 + row;
+    const bool ok = m < M;
+    const int64_t mm = ok ? m : M - 1;
+    float v[8], rv[8];
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(Cs + row * LDC + 8 * cl);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(Cs + row * LDC + 8 * cl + 4);
+    if (resid) {
+      load8(resid + mm * N + 8 * cl, rv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rv[e] = 0.f;
+    }
+    const float keep = (row_mask && ok && row_mask[m] == 0) ? 0.f : 1.f;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] = (e < 4 ? c0[e] : c1[e - 4]) + rv[e];
+      if (epi & kEpiMaskResid) v[e] *= keep;
+      s += v[e];
+    }
+    const float mean = group_sum<LPR>(s) * (1.0f / N);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float t = v[e] - mean;
+      q += t * t;
+    }
+    const float rstd = rsqrtf(group_sum<LPR>(q) * (1.0f / N) + eps);
+    if (!ok) continue;
+    if (resid_out) store8(resid_out + m * N + 8 * cl, v);
+    const float ok_out = (epi & kEpiMaskOut) ? keep : 1.f;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = ((v[e] - mean) * rstd * gv[e] + bv[e]) * ok_out;
+    store8(Y + m * N + 8 * cl, o);
+  }
+}
+
+template <int K, int N, typename TR, typename TY>
+static hipError_t launch_gemm_ln_rows(const GemmArgs& a) {
+  // 128-row blocks while they still give every CU a workgroup, else the smallest
+  // block whose wave tiles are still 32 columns wide (32 rows at N = 128, 64 at 64).
+  constexpr int SBM = N == 128 ? 32 : 64;
+  if (a.M >= (int64_t)128 * compute_units()) {
+    const int64_t blocks = (a.M + 127) / 128;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_ln_rows_kernel<K, N, 128, TR, TY>), dim3((unsigned)blocks), dim3(kLgThreads), 0,
+                       a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+                       static_cast<const TR*>(a.resid), static_cast<float*>(a.c), a.ln_gamma, a.ln_beta,
+                       static_cast<TY*>(a.ln_y), a.M, a.eps, a.row_mask, a.epi);
+  } else {
+    const int64_t blocks = (a.M + SBM - 1) / SBM;
+    hipLaunchKernelGGL((gemm_ln_rows_kernel<K, N, SBM, TR, TY>), dim3((unsigned)blocks), dim3(kLgThreads), 0,
+                       a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+                       static_cast<const TR*>(a.resid), static_cast<float*>(a.c), a.ln_gamma, a.ln_beta,
+                       static_cast<TY*>(a.ln_y), a.M, a.eps, a.row_mask, a.epi);
+  }
+  return hipGetLastError();
+}
+
+template <typename TR, typename TY>
+static hipError_t gemm_ln_rows_shape(const GemmArgs& a) {
+  if (a.K == 128) return a.N == 128 ? launch_gemm_ln_rows<128, 128, TR, TY>(a) : launch_gemm_ln_rows<128, 64, TR, TY>(a);
+  return a.N == 128 ? launch_gemm_ln_rows<64, 128, TR, TY>(a) : launch_gemm_ln_rows<64, 64, TR, TY>(a);
+}
+
+bool gemm_ln_rows_ok(const GemmArgs& a) {
+  return a.ln_gamma && a.ln_beta && a.ln_y && (a.K == 64 || a.K == 128) && (a.N == 64 || a.N == 128) &&
+         !(a.epi & kEpiGelu) && (!a.c || a.c_dtype == kF32) && (a.ln_y_dtype == kF16 || a.ln_y_dtype == kF32);
+}
+
+hipError_t run_gemm_ln_rows(const GemmArgs& a) {
+  if (!gemm_ln_rows_ok(a)) return hipErrorInvalidValue;
+  if (a.M == 0) return hipSuccess;
+  const bool y16 = a.ln_y_dtype == kF16;
+  if (!a.resid || a.resid_dtype == kF32) return y16 ? gemm_ln_rows_shape<float, f16>(a) : gemm_ln_rows_shape<float, float>(a);
+  return y16 ? gemm_ln_rows_shape<f16, f16>(a) : gemm_ln_rows_shape<f16, float>(a);
+}
+
 template <int D, typename TX>
 static hipError_t launch_ln_gemm(const LnGemmArgs& a) {
   const int64_t tiles = ((a.M + kLgBM - 1) / kLgBM) * (int64_t)((a.N + kLgBN - 1) / kLgBN);

@@ -194,7 +194,26 @@ def test_linear_ln_and_add_ln_masks():
     from cobra_amd import ops
 
     torch.manual_seed(9)
-    M, N, K = 2048, 128, 128
+    for M, N, K in [(2048, 128, 128), (40000, 64, 64), (999, 96, 128)]:
+        _check_linear_ln_masks(ops, M, N, K)
+
+    M, N = 2048, 128
+    g, be = torch.rand(N, device=DEV) + 0.5, torch.randn(N, device=DEV)
+    m = torch.rand(M, device=DEV) < 0.7
+    mf = m.float()[:, None]
+    ln = lambda t: F.layer_norm(t, (N,), g, be, 1e-5)  # noqa: E731
+    x = torch.randn(M, N, device=DEV)
+    br = torch.randn(M, N, device=DEV).half()
+    r, y = ops.add_ln(x, br, m, g, be, cast_fp16=False, store_resid=True, mask_out=True)
+    want_r = (x + br.float()) * mf
+    assert torch.equal(r, want_r)
+    assert torch.allclose(y, ln(want_r) * mf, atol=2e-5, rtol=1e-4)
+    r, y = ops.add_ln(x, None, m, g, be, cast_fp16=False, store_resid=False, mask_out=False)
+    assert r is None
+    assert torch.allclose(y, ln(x), atol=2e-5, rtol=1e-4)  # no store, no mask_out: the mask is unused
+
+
+def _check_linear_ln_masks(ops, M, N, K):
     a = (torch.randn(M, K, device=DEV) * 0.5).half()
     w = (torch.randn(N, K, device=DEV) / K ** 0.5).half()
     b = torch.randn(N, device=DEV)
@@ -213,13 +232,3 @@ def test_linear_ln_and_add_ln_masks():
     want_r = prod * mf + res
     assert torch.equal(r[~m], res[~m])
     assert torch.allclose(y, ln(want_r), atol=2e-3, rtol=1e-3)
-
-    x = torch.randn(M, N, device=DEV)
-    br = torch.randn(M, N, device=DEV).half()
-    r, y = ops.add_ln(x, br, m, g, be, cast_fp16=False, store_resid=True, mask_out=True)
-    want_r = (x + br.float()) * mf
-    assert torch.equal(r, want_r)
-    assert torch.allclose(y, ln(want_r) * mf, atol=2e-5, rtol=1e-4)
-    r, y = ops.add_ln(x, None, m, g, be, cast_fp16=False, store_resid=False, mask_out=False)
-    assert r is None
-    assert torch.allclose(y, ln(x), atol=2e-5, rtol=1e-4)  # no store, no mask_out: the mask is unused

@@ -283,11 +283,16 @@ def test_linear_ln_op():
     from cobra_amd import ops
 
     torch.manual_seed(1)
-    for M, N, K in [(8192, 128, 128), (333, 96, 96), (64, 32, 32)]:
+    # K, N in {64, 128} take the whole-row short-K kernel (32/64-row and, from
+    # M = 128 x CUs, 128-row blocks); the others the general LayerNorm epilogue.
+    shapes = [(8192, 128, 128), (333, 96, 96), (64, 32, 32), (40000, 128, 128), (333, 64, 64),
+              (33001, 64, 64), (77, 128, 64), (65, 64, 128), (1, 64, 64)]
+    for i, (M, N, K) in enumerate(shapes):
         a = torch.randn(M, K, device=DEV).half()
         w = (torch.randn(N, K, device=DEV) / math.sqrt(K)).half()
         b = torch.randn(N, device=DEV)
-        res = torch.randn(M, N, device=DEV).half()
+        res = torch.randn(M, N, device=DEV)
+        res = res.half() if i % 2 == 0 else res
         g = torch.rand(N, device=DEV) + 0.5
         be = torch.randn(N, device=DEV)
         r, y = ops.linear_ln(a, w, b, res, g, be)
