@@ -39,6 +39,14 @@ __device__ __forceinline__ f16x8 scaled_f16(const f32x16& acc, int half, float s
   return o;
 }
 
+// Registers 8*half .. 8*half+7 of a 32x32 accumulator, as fp16.
+__device__ __forceinline__ f16x8 acc_f16(const f32x16& acc, int half) {
+  f16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (f16)acc[8 * half + e];
+  return o;
+}
+
 // Registers 8*half .. 8*half+7 of a 32x32 accumulator (+ per-register bias), as fp16.
 __device__ __forceinline__ f16x8 half_to_f16(const f32x16& acc, int half, const float (&bias)[16]) {
   f16x8 o;

@@ -100,6 +100,31 @@ __device__ __forceinline__ void dma_rows(char* dst, int lane, F src_row) {
   }
 }
 
+// The same transfer for a tile whose rows are contiguous in memory (row r at
+// base + r * 2D bytes, `base` wave-uniform).  Instruction i moves, per lane, the
+// 16 bytes at base + 1024 i + off[i % NP]: the swizzle repeats every NP spans,
+// so the per-lane part is NP registers computed once, the rest is a scalar base
+// plus an immediate (no 64-bit per-lane address arithmetic per transfer).
+template <int D>
+struct RowSpans {
+  static constexpr int NP = D == 128 ? 4 : 2;
+  uint32_t off[NP];
+  __device__ __forceinline__ explicit RowSpans(int lane) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int o = 1024 * j + 16 * lane;
+      const int r = o / (2 * D), pos = (o % (2 * D)) / 16;
+      off[j] = (uint32_t)(r * 2 * D - 1024 * j + 16 * (pos ^ row_swz<D>(r)));
+    }
+  }
+};
+
+template <int D, int NI>
+__device__ __forceinline__ void dma_span_rows(char* dst, const char* base, const RowSpans<D>& sp) {
+#pragma unroll
+  for (int i = 0; i < NI; ++i) dma16(base + 1024 * i + sp.off[i % RowSpans<D>::NP], dst + 1024 * i);
+}
+
 // Operand fragment of tile row r, logical chunk c.
 template <int D>
 __device__ __forceinline__ f16x8 tile_chunk(const char* tile, int r, int c) {
@@ -136,7 +161,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 31, g = lane >> 5;
   const int qtok = 32 * s + li;  // query of this lane for attention, out-projection, LN2
-  const bool tok_ok = 32 * w + li < S, q_ok = qtok < S;
+  const bool q_ok = qtok < S;
   const f16* xs = x + (int64_t)b * S * D;
   // Waves past the last d-tile / head issue the same transfers for tile / head 0
   // (identical bytes to the same place), so every wave's wait counts are equal.
@@ -156,12 +181,17 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   }
 
   // ---- DMA, in the order the data is needed -------------------------------------------
+  const RowSpans<D> spans(lane);
   {  // [gamma1 | beta1]
     const int c = 4 * lane;
     dma16(c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0), rP);
   }
-  // Token tile w (rows past S fetch row 0, S >= 1, and are zeroed where used).
-  dma_rows<D, P::N_X>(rTok, lane, [&](int r) { return xs + (int64_t)(32 * w + r < S ? 32 * w + r : 0) * D; });
+  // Token tile w.  Rows past S fetch row 0 (S >= 1): finite values whose keys the
+  // softmax masks and whose queries are never stored.
+  if (32 * w + 32 <= S)
+    dma_span_rows<D, P::N_X>(rTok, reinterpret_cast<const char*>(xs + (int64_t)32 * w * D), spans);
+  else
+    dma_rows<D, P::N_X>(rTok, lane, [&](int r) { return xs + (int64_t)(32 * w + r < S ? 32 * w + r : 0) * D; });
   {  // 32-float segments: b_k, b_v of d-tile dq; b_q of head hq (2 x 32); b_o, gamma2, beta2 of tile dq
     const int seg = lane >> 3, off = 4 * (lane & 7);
     const float* src = seg == 0   ? bqkv + D + 32 * dq + off
@@ -175,58 +205,79 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     dma16(src, rP + 1024);
   }
   // W_k rows 32dq .. 32dq+31, then the W_v rows.
-  dma_rows<D, P::N_A>(rWkv, lane, [&](int r) {
-    return wqkv + (int64_t)((r < 32 ? D : 2 * D - 32) + 32 * dq + r) * D;
-  });
-  // W_q rows of head hq.
-  dma_rows<D, P::N_Q>(rWq, lane, [&](int r) { return wqkv + (int64_t)(HD * hq + r) * D; });
-  // Residual block: queries 32s .. 32s+31, columns 32dq .. 32dq+31, as [32 rows][4 chunks]
-  // with chunk c of row r at c ^ ((r >> 2) & 3).
+  const char* const wbytes = reinterpret_cast<const char*>(wqkv);
+  dma_span_rows<D, P::N_A / 2>(rWkv, wbytes + (int64_t)(D + 32 * dq) * 2 * D, spans);
+  dma_span_rows<D, P::N_A / 2>(rWkv + P::TILEB, wbytes + (int64_t)(2 * D + 32 * dq) * 2 * D, spans);
+  // The W_q rows and the residual block are issued from inside LN1 (below), so the
+  // arithmetic of LN1 overlaps the transfers the CU's load path is still working
+  // through instead of waiting behind them.
+  auto issue_late = [&]() {
+    // W_q rows of head hq.
+    dma_span_rows<D, P::N_Q>(rWq, wbytes + (int64_t)HD * hq * 2 * D, spans);
+    // Residual block: queries 32s .. 32s+31, columns 32dq .. 32dq+31, as [32 rows][4
+    // chunks] with chunk c of row r at c ^ ((r >> 2) & 3).  Span i covers rows
+    // 16i + lane / 4, whose swizzle (lane / 16) & 3 does not depend on i.
+    const uint32_t roff = (uint32_t)((lane >> 2) * 2 * D + 16 * ((lane & 3) ^ ((lane >> 4) & 3)));
+    if (32 * s + 32 <= S) {
+      const char* base = reinterpret_cast<const char*>(xs + (int64_t)32 * s * D + 32 * dq);
 #pragma unroll
-  for (int i = 0; i < P::N_R; ++i) {
-    const int o = 1024 * i + 16 * lane;
-    const int r = o / 64, pos = (o % 64) / 16;
-    const int qr = 32 * s + r < S ? 32 * s + r : 0;
-    dma16(xs + (int64_t)qr * D + 32 * dq + 8 * (pos ^ ((r >> 2) & 3)), rR + 1024 * i);
-  }
+      for (int i = 0; i < P::N_R; ++i) dma16(base + 16 * 2 * D * i + roff, rR + 1024 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < P::N_R; ++i) {
+        const int r = 16 * i + (lane >> 2);
+        const int qr = 32 * s + r < S ? 32 * s + r : 0;
+        dma16(reinterpret_cast<const char*>(xs + (int64_t)qr * D + 32 * dq) + (roff - (lane >> 2) * 2 * D),
+              rR + 1024 * i);
+      }
+    }
+  };
 
   // ---- LN1 of token 32w + li (columns 16kk + 8g + e): its tile and parameters are in.
-  wait_vmcnt<1 + P::N_A + P::N_Q + P::N_R>();
+  wait_vmcnt<1 + P::N_A>();
   KeyBits kbits{~0ull, ~0ull};
   if constexpr (MASKED) kbits = key_bits_of(kbytes, S, lane);
   {
-    float xv[KD][8];
-    float sum = 0.f;
+    // Row sum by fp16 pair dot products with (1, 1) (exact products, fp32
+    // accumulation), in four independent chains; then the centred values in fp32.
+    f16x8 xc[KD];
+#pragma unroll
+    for (int kk = 0; kk < KD; ++kk) xc[kk] = tile_chunk<D>(rTok, li, 2 * kk + g);
+    const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KD; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        part[e] = __builtin_amdgcn_fdot2(f16x2{xc[kk][2 * e], xc[kk][2 * e + 1]}, one2, part[e], false);
+    const float mean = sum_xor32((part[0] + part[1]) + (part[2] + part[3])) * (1.0f / D);
+    issue_late();
+    // gamma1 / beta1 of this lane's columns, all requested before the arithmetic
+    // below so one wait covers them.
+    const float* pg = reinterpret_cast<const float*>(rP);
+    float gv[KD][8], bv[KD][8];
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) {
-      const f16x8 c = tile_chunk<D>(rTok, li, 2 * kk + g);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xv[kk][e] = tok_ok ? (float)c[e] : 0.f;
-        sum += xv[kk][e];
-      }
+      load8(pg + 16 * kk + 8 * g, gv[kk]);
+      load8(pg + D + 16 * kk + 8 * g, bv[kk]);
     }
-    const float mean = sum_xor32(sum) * (1.0f / D);
-    float q = 0.f;
+    float xv[KD][8];
+    float qp[2] = {0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float t = xv[kk][e] - mean;
-        q += t * t;
+        xv[kk][e] = (float)xc[kk][e] - mean;
+        qp[e & 1] = fmaf(xv[kk][e], xv[kk][e], qp[e & 1]);
       }
-    const float rstd = rsqrtf(sum_xor32(q) * (1.0f / D) + eps);
-    const float* pg = reinterpret_cast<const float*>(rP);
+    const float rstd = rsqrtf(sum_xor32(qp[0] + qp[1]) * (1.0f / D) + eps);
     // The output fragments overwrite the token tile in place: every read of it above
     // feeds the mean, so all of them precede the first write.
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) {
-      float gv[8], bv[8];
-      load8(pg + 16 * kk + 8 * g, gv);
-      load8(pg + D + 16 * kk + 8 * g, bv);
       f16x8 h;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[kk][e] - mean) * rstd * gv[e] + bv[e]);
+      for (int e = 0; e < 8; ++e) h[e] = (f16)fmaf(xv[kk][e] * rstd, gv[kk][e], bv[kk][e]);
       Hb[(w * KD + kk) * 64 + lane] = h;
     }
   }
@@ -249,11 +300,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
 
   // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.
-  dma_rows<D, P::N_O>(rWo, lane, [&](int r) { return wo + (int64_t)(32 * dq + r) * D; });
+  dma_span_rows<D, P::N_O>(rWo, reinterpret_cast<const char*>(wo + (int64_t)32 * dq * D), spans);
 
   // ---- K^T and V of d-tile w for every token tile; Q^T of the slice for head w ---------
   if (w < NNT) {
-    float bk[16], bv[16];
+    // The biases start the accumulators (the first product of each chain reads them
+    // as its C operand), so no bias add follows the products.
+    f32x16 bk, bv;
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
       const f32x4 t = *reinterpret_cast<const f32x4*>(pp + 8 * qd + 4 * g);
@@ -265,23 +318,33 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int r = 0; r < 16; ++r) bv[r] = bvl;
     const int h = (32 * w) / HD, t2 = w % NDT;  // head and d tile within the head
     // Two accumulator pairs: the products of token tile t run on the matrix
-    // cores while tile t-1 is biased, converted and stored.
+    // cores while tile t-1 is converted and stored.
     f32x16 ka[2], va[2];
+    // The h fragments of tile t + 1 are requested before the products of tile t,
+    // so the LDS latency hides behind 2 KD matrix instructions.
+    f16x8 hf[2][KD];
+    auto fetch = [&](int t) {
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) hf[t & 1][kk] = Hb[(t * KD + kk) * 64 + lane];
+    };
     auto products = [&](int t) {
-      ka[t & 1] = zero16();
-      va[t & 1] = zero16();
+      if (t + 1 < kSplitTiles) fetch(t + 1);
+      // Keep the requests here: left alone, the scheduler sinks each read next to
+      // its use and the wave then waits out the LDS latency every two products.
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
-        const f16x8 hb = Hb[(t * KD + kk) * 64 + lane];
-        ka[t & 1] = mfma32x32x16(wk[kk], hb, ka[t & 1]);
-        va[t & 1] = mfma32x32x16(hb, wv[kk], va[t & 1]);
+        const f16x8 hb = hf[t & 1][kk];
+        ka[t & 1] = mfma32x32x16(wk[kk], hb, kk == 0 ? bk : ka[t & 1]);
+        va[t & 1] = mfma32x32x16(hb, wv[kk], kk == 0 ? bv : va[t & 1]);
       }
     };
+    fetch(0);
     auto store = [&](int t) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = half_to_f16(ka[t & 1], half, bk);
-        Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = half_to_f16(va[t & 1], half, bv);
+        Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = acc_f16(ka[t & 1], half);
+        Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
       }
     };
     products(0);
@@ -296,18 +359,17 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   if (w < H) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      f32x16 qa = zero16();
-#pragma unroll
-      for (int kk = 0; kk < KD; ++kk) qa = mfma32x32x16(wq[dt][kk], Hb[(s * KD + kk) * 64 + lane], qa);
-      float bq[16];
+      f32x16 qa;
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         const f32x4 t = *reinterpret_cast<const f32x4*>(pp + 64 + 32 * dt + 8 * qd + 4 * g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bq[4 * qd + e] = t[e];
+        for (int e = 0; e < 4; ++e) qa[4 * qd + e] = t[e];
       }
 #pragma unroll
-      for (int half = 0; half < 2; ++half) qB[2 * dt + half] = half_to_f16(qa, half, bq);
+      for (int kk = 0; kk < KD; ++kk) qa = mfma32x32x16(wq[dt][kk], Hb[(s * KD + kk) * 64 + lane], qa);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) qB[2 * dt + half] = acc_f16(qa, half);
     }
   }
   lds_barrier();  // K, V of every token tile and head are in LDS
