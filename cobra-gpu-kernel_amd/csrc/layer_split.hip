@@ -299,10 +299,20 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   const float* pp = reinterpret_cast<const float*>(rP + 1024);  // the 32-float segments above
   lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
 
-  // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.
-  dma_span_rows<D, P::N_O>(rWo, reinterpret_cast<const char*>(wo + (int64_t)32 * dq * D), spans);
+  // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.  A
+  // projecting wave issues them between its token tiles, where the matrix cores are
+  // still busy with the previous tile, rather than stalling on the load path first.
+  const char* const wob = reinterpret_cast<const char*>(wo + (int64_t)32 * dq * D);
+  constexpr int kWoPer = (P::N_O + kSplitTiles - 2) / (kSplitTiles - 1);  // spans per tile 1 ..
+  auto issue_wo = [&](int t) {  // t >= 1
+#pragma unroll
+    for (int i = (t - 1) * kWoPer; i < t * kWoPer && i < P::N_O; ++i)
+      dma16(wob + 1024 * i + spans.off[i % RowSpans<D>::NP], rWo + 1024 * i);
+  };
+  if (w >= NNT) dma_span_rows<D, P::N_O>(rWo, wob, spans);
 
   // ---- K^T and V of d-tile w for every token tile; Q^T of the slice for head w ---------
+  f16x8 qB[KSH];
   if (w < NNT) {
     // The biases start the accumulators (the first product of each chain reads them
     // as its C operand), so no bias add follows the products.
@@ -327,8 +337,20 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) hf[t & 1][kk] = Hb[(t * KD + kk) * 64 + lane];
     };
+    // Tile t - 1 is converted and stored a quarter at a time between the products of
+    // tile t, each quarter pinned after two products (scheduling barriers): the wave
+    // issues instructions in order, so conversions placed after a run of products
+    // would leave the matrix cores idle while they execute.
+    auto store_part = [&](int t, int c) {  // c: K half 0, K half 1, V half 0, V half 1
+      const int half = c & 1;
+      if (c < 2)
+        Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = acc_f16(ka[t & 1], half);
+      else
+        Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
+    };
     auto products = [&](int t) {
       if (t + 1 < kSplitTiles) fetch(t + 1);
+      if (t >= 1) issue_wo(t);
       // Keep the requests here: left alone, the scheduler sinks each read next to
       // its use and the wave then waits out the LDS latency every two products.
       __builtin_amdgcn_sched_barrier(0);
@@ -337,119 +359,107 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         const f16x8 hb = hf[t & 1][kk];
         ka[t & 1] = mfma32x32x16(wk[kk], hb, kk == 0 ? bk : ka[t & 1]);
         va[t & 1] = mfma32x32x16(hb, wv[kk], kk == 0 ? bv : va[t & 1]);
+        if (t >= 1)
+#pragma unroll
+          for (int c = kk * 4 / KD; c < (kk + 1) * 4 / KD; ++c) store_part(t - 1, c);
+        __builtin_amdgcn_sched_barrier(0);
       }
     };
     fetch(0);
-    auto store = [&](int t) {
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = acc_f16(ka[t & 1], half);
-        Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
+    for (int t = 0; t < kSplitTiles; ++t) products(t);
+    // Q^T of the slice for head w (waves past the last head have none), with the
+    // last K / V tile stored between its products.
+    if (w < H) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        f32x16 qa;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4 t = *reinterpret_cast<const f32x4*>(pp + 64 + 32 * dt + 8 * qd + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qa[4 * qd + e] = t[e];
+        }
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) {
+          qa = mfma32x32x16(wq[dt][kk], Hb[(s * KD + kk) * 64 + lane], qa);
+          if (dt == 0)
+#pragma unroll
+            for (int c = kk * 4 / KD; c < (kk + 1) * 4 / KD; ++c) store_part(kSplitTiles - 1, c);
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half) qB[2 * dt + half] = acc_f16(qa, half);
       }
-    };
-    products(0);
+    } else {
 #pragma unroll
-    for (int t = 1; t < kSplitTiles; ++t) {
-      products(t);
-      store(t - 1);
-    }
-    store(kSplitTiles - 1);
-  }
-  f16x8 qB[KSH];
-  if (w < H) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      f32x16 qa;
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 t = *reinterpret_cast<const f32x4*>(pp + 64 + 32 * dt + 8 * qd + 4 * g);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) qa[4 * qd + e] = t[e];
-      }
-#pragma unroll
-      for (int kk = 0; kk < KD; ++kk) qa = mfma32x32x16(wq[dt][kk], Hb[(s * KD + kk) * 64 + lane], qa);
-#pragma unroll
-      for (int half = 0; half < 2; ++half) qB[2 * dt + half] = acc_f16(qa, half);
+      for (int c = 0; c < 4; ++c) store_part(kSplitTiles - 1, c);
     }
   }
   lds_barrier();  // K, V of every token tile and head are in LDS
 
-  // ---- attention of head w: S^T = K Q^T over two blocks of two key tiles, exact
-  // softmax with one rescale between the blocks, O^T = V^T P^T.
+  // ---- attention of head w: S^T = K Q^T for all (at most 128) keys at once, one exact
+  // softmax pass (no running max, no rescale), O^T = V^T P^T.
   if (w < H) {
     const int h = w;
+    // Every K and V fragment of the head is requested up front; the scheduling
+    // barrier keeps the requests ahead of the products that wait on them.
+    f16x8 kf[kSplitTiles][KSH], vf[kSplitTiles][2][NDT];
+#pragma unroll
+    for (int t = 0; t < kSplitTiles; ++t)
+#pragma unroll
+      for (int ks = 0; ks < KSH; ++ks) kf[t][ks] = Kl[((h * kSplitTiles + t) * KSH + ks) * 64 + lane];
+#pragma unroll
+    for (int t = 0; t < kSplitTiles; ++t)
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) vf[t][half][dt] = Vl[(((h * kSplitTiles + t) * NDT + dt) * 2 + half) * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 sacc[kSplitTiles];
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < kSplitTiles; ++t) {
+      sacc[t] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KSH; ++ks) sacc[t] = mfma32x32x16(kf[t][ks], qB[ks], sacc[t]);
+      // Keys past S and, causally, keys after the query.
+      if (32 * t + 32 > S || (CAUSAL && t >= s)) {
+        int lim = S - 32 * t - 4 * g;  // valid: row offset < lim
+        if (CAUSAL) lim = min(lim, qtok - 32 * t - 4 * g + 1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (8 * (r >> 2) + (r & 3) >= lim) sacc[t][r] = kNegInf;
+      }
+      if constexpr (MASKED) {
+        if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc[t], kbits.tile(t), g);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
+    }
+    mx = max_xor32(mx);
+    // Unmasked, key 0 is valid for every query, so the max is finite; a query whose
+    // keys are all padded gets max -inf, all-zero probabilities and a zero row.
+    float m = mx * c2;
+    if constexpr (MASKED) m = mx == kNegInf ? 0.f : m;
     f32x16 ot[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) ot[dt] = zero16();
-    float m_run = MASKED ? kNegInf : 0.f, l = 0.f;
+    float lp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int blk = 0; blk < kSplitTiles / 2; ++blk) {
-      f32x16 sacc[2];
-      float mx = kNegInf;
+    for (int t = 0; t < kSplitTiles; ++t) {
+      f16x8 pB[2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int t = 2 * blk + u;
-        sacc[u] = zero16();
-#pragma unroll
-        for (int ks = 0; ks < KSH; ++ks)
-          sacc[u] = mfma32x32x16(Kl[((h * kSplitTiles + t) * KSH + ks) * 64 + lane], qB[ks], sacc[u]);
-        // Keys past S and, causally, keys after the query.
-        if (32 * t + 32 > S || (CAUSAL && t >= s)) {
-          int lim = S - 32 * t - 4 * g;  // valid: row offset < lim
-          if (CAUSAL) lim = min(lim, qtok - 32 * t - 4 * g + 1);
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (8 * (r >> 2) + (r & 3) >= lim) sacc[u][r] = kNegInf;
-        }
-        if constexpr (MASKED) {
-          if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc[u], kbits.tile(t), g);
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
-      }
-      mx = max_xor32(mx);
-      // Unmasked: block 0 holds key 0, valid for every query, so its max is finite;
-      // a fully masked later block leaves the running max as it is.
-      float m_new, alpha;
-      if constexpr (MASKED) {
-        const SoftmaxStep st = masked_softmax_step(m_run, mx * c2);
-        m_new = st.m_use;
-        alpha = st.alpha;
-      } else {
-        m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);
-        alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-      }
-      f16x8 pB[2][2];
-      float ps = 0.f;
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[u][r], c2, -m_new));
-          ps += pv;
-          pB[u][r >> 3][r & 7] = (f16)pv;
-        }
-      if (blk == 0) {
-        l = ps;
-      } else {
-        l = l * alpha + ps;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) ot[dt][r] *= alpha;
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
+        lp[r & 3] += pv;
+        pB[r >> 3][r & 7] = (f16)pv;
       }
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int half = 0; half < 2; ++half)
 #pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
-            ot[dt] = mfma32x32x16(Vl[(((h * kSplitTiles + 2 * blk + u) * NDT + dt) * 2 + half) * 64 + lane],
-                                  pB[u][half], ot[dt]);
+        for (int dt = 0; dt < NDT; ++dt) ot[dt] = mfma32x32x16(vf[t][half][dt], pB[half], ot[dt]);
     }
-    l = sum_xor32(l);
-    // A query with no valid key (only a padded one) gets a zero row.
+    const float l = sum_xor32((lp[0] + lp[1]) + (lp[2] + lp[3]));
     const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
