@@ -86,6 +86,13 @@ class _Pack:
         self.versions = versions
 
 
+class _Fast:
+    """The steady-state launch of one input signature: the argument list of
+    ``cobra_layer_fwd`` with everything but x, y and the stream filled in."""
+
+    __slots__ = ("shape", "dtype", "device", "causal", "eps", "versions", "args", "fn")
+
+
 class CobraAttentionSublayer(nn.Module):
     def __init__(self, d_model: int, num_heads: int, causal: bool = False, eps: float = 1e-5,
                  graph: Optional[bool] = None) -> None:
@@ -113,6 +120,7 @@ class CobraAttentionSublayer(nn.Module):
         self._static_y: Optional[torch.Tensor] = None
         self._static_r: Optional[torch.Tensor] = None
         self._static_m: Optional[torch.Tensor] = None
+        self._fast: Optional[_Fast] = None
 
     # -- parameters ---------------------------------------------------------
 
@@ -123,13 +131,17 @@ class CobraAttentionSublayer(nn.Module):
         self._versioned = [not p.is_inference() for p in self._params]
         self._pack = None
         self._sig = None
+        self._fast = None
         return out
 
-    def _packed(self) -> _Pack:
+    def _versions(self):
         # In-place updates (load_state_dict, optimiser-style edits) bump _version.
         # Inference tensors (made under torch.inference_mode) keep no version
         # counter; for those only a storage change is detected.
-        versions = tuple([p._version if v else p.data_ptr() for p, v in zip(self._params, self._versioned)])
+        return tuple([p._version if v else p.data_ptr() for p, v in zip(self._params, self._versioned)])
+
+    def _packed(self) -> _Pack:
+        versions = self._versions()
         if self._pack is None or self._pack.versions != versions:
             if not self.norm1.weight.is_cuda:
                 raise RuntimeError("CobraAttentionSublayer runs on the GPU only: move it with .to('cuda')")
@@ -146,6 +158,25 @@ class CobraAttentionSublayer(nn.Module):
         causal: Optional[bool] = None,
         return_residual: bool = False,
     ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+        # Steady state of the common call (same input signature, no mask, weights
+        # unchanged): one allocation and the library call.  At the small shapes the
+        # kernel takes less time than the Python around it, so this path is what
+        # back-to-back forwards are bound by.
+        f = self._fast
+        if (f is not None and valid_token_mask is None and causal is None and not return_residual
+                and x.shape == f.shape and x.dtype == f.dtype and x.is_cuda and x.is_contiguous()
+                and x.get_device() == f.device and self.causal == f.causal and self.norm1.eps == f.eps
+                and self._versions() == f.versions):
+            y = torch.empty_like(x)
+            a = f.args.copy()  # a private list: another thread may be in here too
+            a[0] = x.data_ptr()
+            a[11] = y.data_ptr()
+            a[21] = ops.raw_stream(f.device)
+            code = f.fn(*a)
+            if code:
+                ops.check_code("cobra_layer_fwd", code)
+            return y
+        fast_ok = valid_token_mask is None and causal is None and not return_residual
         causal = self.causal if causal is None else bool(causal)
         pack = self._packed()
         # Free memory moves between calls, so big or host-resident inputs are
@@ -164,7 +195,21 @@ class CobraAttentionSublayer(nn.Module):
         m = self._mask_bytes(valid_token_mask, x) if masked else None
         if self._graph_ok:
             return self._run_graphed(x, m, pack, causal, return_residual)
-        return self._run_eager(x, m, pack, causal, return_residual)
+        out = self._run_eager(x, m, pack, causal, return_residual)
+        if fast_ok and x.is_cuda and x.numel() * x.element_size() < streaming.STREAM_MIN_BYTES:
+            self._fast = self._make_fast(x, pack)
+        return out
+
+    def _make_fast(self, x: torch.Tensor, pack: _Pack) -> _Fast:
+        f = _Fast()
+        f.shape, f.dtype, f.device = x.shape, x.dtype, x.get_device()
+        f.causal, f.eps, f.versions = self.causal, self.norm1.eps, pack.versions
+        B, S, D = x.shape
+        f.args = ops.layer_fwd_args(x, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w, pack.ln1_b,
+                                    pack.ln2_w, pack.ln2_b, x, self._ws, self.attention.num_heads, self.causal,
+                                    self.norm1.eps)
+        f.fn = ops.layer_fwd_fn()
+        return f
 
     # -- planning -------------------------------------------------------------
 
@@ -205,6 +250,7 @@ class CobraAttentionSublayer(nn.Module):
             self._graph_ok = bool(self.graph) and small
         self._graph = None
         self._static_x = self._static_y = self._static_r = self._static_m = None
+        self._fast = None
         self._sig = sig
 
     def _launch(self, x, m, y, r, pack: _Pack, ws: torch.Tensor, causal: bool) -> None:

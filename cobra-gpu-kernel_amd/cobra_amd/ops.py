@@ -356,10 +356,31 @@ def layer_fwd(
     valid_mask: optional [B, S] uint8 (0 = padded token) -- the workspace must then be
     sized with ``masked=True``.
     """
+    call("cobra_layer_fwd", *layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, workspace,
+                                            heads, causal, eps, resid_out, valid_mask))
+
+
+def layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, workspace, heads, causal, eps=1e-5,
+                   resid_out=None, valid_mask=None) -> list:
+    """The argument list of ``cobra_layer_fwd`` (x at 0, y at 11, the stream at 21)."""
     B, S, D = x.shape
-    call(
-        "cobra_layer_fwd", x.data_ptr(), _dtype_code(x, "x"), _ptr(valid_mask), w_qkv.data_ptr(), b_qkv.data_ptr(),
-        w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(), ln2_w.data_ptr(),
-        ln2_b.data_ptr(), y.data_ptr(), _ptr(resid_out), workspace.data_ptr(), workspace.numel(),
-        B, S, D, heads, 1 if causal else 0, float(eps), _stream(x),
-    )
+    return [x.data_ptr(), _dtype_code(x, "x"), _ptr(valid_mask), w_qkv.data_ptr(), b_qkv.data_ptr(),
+            w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(), ln2_w.data_ptr(),
+            ln2_b.data_ptr(), y.data_ptr(), _ptr(resid_out), workspace.data_ptr(), workspace.numel(),
+            B, S, D, heads, 1 if causal else 0, float(eps), _stream(x)]
+
+
+def layer_fwd_fn():
+    """The ctypes function behind ``cobra_layer_fwd`` (returns the error code)."""
+    return getattr(_lib.lib(), "cobra_layer_fwd")
+
+
+def check_code(fn: str, code: int) -> None:
+    _lib.check(fn, code)
+
+
+def raw_stream(device_index: int) -> int:
+    """The current stream handle of a device, by index."""
+    if _raw_stream is not None:
+        return _raw_stream(device_index)
+    return torch.cuda.current_stream(device_index).cuda_stream

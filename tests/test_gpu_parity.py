@@ -227,6 +227,42 @@ def test_weight_update_repacks():
     assert compare_outputs(want, y1.float().cpu()).passed
 
 
+def test_steady_state_fast_path():
+    """Repeat calls of one signature take the cached launch; anything that changes
+    the launch (module.causal, weights, eps, a mask, the shape) leaves it."""
+    ref, mod = build_pair(128, 4)
+    x = make_input(8, 128, 128, seed=3).half().to(DEV)
+    x2 = make_input(8, 128, 128, seed=4).half().to(DEV)
+    with torch.inference_mode():
+        mod(x)
+        assert mod._fast is not None
+        y_fast = mod(x2).clone()
+        y_slow = mod(x2, causal=False).clone()  # an explicit argument takes the full path
+        torch.cuda.synchronize()
+    assert torch.equal(y_fast, y_slow)
+    assert compare_outputs(oracle_on(ref, x2.float().cpu(), False, "cpu"), y_fast.float().cpu()).passed
+    mod.causal = True
+    with torch.inference_mode():
+        y_c = mod(x2).clone()
+        torch.cuda.synchronize()
+    assert compare_outputs(oracle_on(ref, x2.float().cpu(), True, "cpu"), y_c.float().cpu()).passed
+    mod.causal = False
+    with torch.no_grad():
+        mod.attention.out_proj.bias.add_(0.25)
+        ref.attention.out_proj.bias.add_(0.25)
+        ref.attention.out_proj.bias.copy_(ref.attention.out_proj.bias.half().float())
+    with torch.inference_mode():
+        mod(x2)
+        y_w = mod(x2).clone()  # the second call runs on the rebuilt cache
+        torch.cuda.synchronize()
+    assert compare_outputs(oracle_on(ref, x2.float().cpu(), False, "cpu"), y_w.float().cpu()).passed
+    x3 = make_input(3, 77, 128, seed=5).half().to(DEV)
+    with torch.inference_mode():
+        y3 = mod(x3).clone()
+        torch.cuda.synchronize()
+    assert compare_outputs(oracle_on(ref, x3.float().cpu(), False, "cpu"), y3.float().cpu()).passed
+
+
 # ---- op-level wrappers against fp32 references of the same op -------------
 
 def test_linear_op():
