@@ -87,10 +87,10 @@ class _Pack:
 
 
 class _Fast:
-    """The steady-state launch of one input signature: the argument list of
-    ``cobra_layer_fwd`` with everything but x, y and the stream filled in."""
+    """The steady-state launch of one input signature: ``cobra_layer_fwd`` bound
+    (``cobra_layer_bind``) with everything but x, y and the stream."""
 
-    __slots__ = ("shape", "dtype", "device", "causal", "eps", "versions", "args", "fn")
+    __slots__ = ("shape", "dtype", "device", "causal", "eps", "versions", "launch", "handle", "run")
 
 
 class CobraAttentionSublayer(nn.Module):
@@ -168,11 +168,7 @@ class CobraAttentionSublayer(nn.Module):
                 and x.get_device() == f.device and self.causal == f.causal and self.norm1.eps == f.eps
                 and self._versions() == f.versions):
             y = torch.empty_like(x)
-            a = f.args.copy()  # a private list: another thread may be in here too
-            a[0] = x.data_ptr()
-            a[11] = y.data_ptr()
-            a[21] = ops.raw_stream(f.device)
-            code = f.fn(*a)
+            code = f.run(f.handle, x.data_ptr(), None, y.data_ptr(), None, ops.raw_stream(f.device))
             if code:
                 ops.check_code("cobra_layer_fwd", code)
             return y
@@ -205,10 +201,10 @@ class CobraAttentionSublayer(nn.Module):
         f.shape, f.dtype, f.device = x.shape, x.dtype, x.get_device()
         f.causal, f.eps, f.versions = self.causal, self.norm1.eps, pack.versions
         B, S, D = x.shape
-        f.args = ops.layer_fwd_args(x, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w, pack.ln1_b,
-                                    pack.ln2_w, pack.ln2_b, x, self._ws, self.attention.num_heads, self.causal,
-                                    self.norm1.eps)
-        f.fn = ops.layer_fwd_fn()
+        f.launch = ops.LayerLaunch(x.dtype, False, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w,
+                                   pack.ln1_b, pack.ln2_w, pack.ln2_b, self._ws, B, S, D,
+                                   self.attention.num_heads, self.causal, self.norm1.eps)
+        f.handle, f.run = f.launch.handle, f.launch.run_fn
         return f
 
     # -- planning -------------------------------------------------------------

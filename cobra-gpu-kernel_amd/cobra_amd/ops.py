@@ -362,7 +362,7 @@ def layer_fwd(
 
 def layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, workspace, heads, causal, eps=1e-5,
                    resid_out=None, valid_mask=None) -> list:
-    """The argument list of ``cobra_layer_fwd`` (x at 0, y at 11, the stream at 21)."""
+    """The argument list of ``cobra_layer_fwd``."""
     B, S, D = x.shape
     return [x.data_ptr(), _dtype_code(x, "x"), _ptr(valid_mask), w_qkv.data_ptr(), b_qkv.data_ptr(),
             w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(), ln2_w.data_ptr(),
@@ -370,9 +370,31 @@ def layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, wor
             B, S, D, heads, 1 if causal else 0, float(eps), _stream(x)]
 
 
-def layer_fwd_fn():
-    """The ctypes function behind ``cobra_layer_fwd`` (returns the error code)."""
-    return getattr(_lib.lib(), "cobra_layer_fwd")
+class LayerLaunch:
+    """A bound ``cobra_layer_fwd`` (``cobra_layer_bind``): ``run(x, y, stream)``
+    launches with every other argument fixed.  Keeps the buffers it names alive."""
+
+    __slots__ = ("handle", "run_fn", "_keep", "_unbind")
+
+    def __init__(self, x_dtype, masked, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, workspace, batch,
+                 seq_len, d_model, heads, causal, eps):
+        lib = _lib.lib()
+        self.handle = None
+        h = lib.cobra_layer_bind(_DT[x_dtype], 1 if masked else 0, w_qkv.data_ptr(), b_qkv.data_ptr(),
+                                 w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(),
+                                 ln2_w.data_ptr(), ln2_b.data_ptr(), workspace.data_ptr(), workspace.numel(),
+                                 batch, seq_len, d_model, heads, 1 if causal else 0, float(eps))
+        if not h:
+            raise ValueError("cobra_layer_bind rejected the arguments")
+        self.handle = h
+        self.run_fn = lib.cobra_layer_run
+        self._unbind = lib.cobra_layer_unbind
+        self._keep = (w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, workspace)
+
+    def __del__(self):
+        if self.handle:
+            self._unbind(self.handle)
+            self.handle = None
 
 
 def check_code(fn: str, code: int) -> None:

@@ -2,6 +2,8 @@
 // orchestration of the whole attention sublayer.
 #include "cobra_amd.h"
 
+#include <new>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -215,5 +217,45 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
   cobra::LnArgs ln2{r, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
   return code(cobra::run_ln(ln2));
 }
+
+
+struct cobra_layer_launch {
+  int x_dtype, masked, causal;
+  const void* w_qkv;
+  const float *b_qkv, *b_o, *ln1_w, *ln1_b, *ln2_w, *ln2_b;
+  const void* w_o;
+  void* workspace;
+  int64_t workspace_bytes, batch, seq_len, d_model, heads;
+  float eps;
+};
+
+cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv, const float* b_qkv, const void* w_o,
+                                     const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
+                                     const float* ln2_b, void* workspace, int64_t workspace_bytes, int64_t batch,
+                                     int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps) {
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked);
+  if (plan < 0 || !is_dtype(x_dtype)) return nullptr;
+  const void* must[] = {w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b};
+  for (const void* p : must)
+    if (!p || !aligned16(p)) return nullptr;
+  if (!opt_aligned16(workspace)) return nullptr;
+  const int64_t need = cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, masked);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return nullptr;
+  auto* h = new (std::nothrow) cobra_layer_launch;
+  if (!h) return nullptr;
+  *h = cobra_layer_launch{x_dtype, masked ? 1 : 0, causal ? 1 : 0, w_qkv, b_qkv, b_o, ln1_w, ln1_b, ln2_w, ln2_b,
+                          w_o, workspace, workspace_bytes, batch, seq_len, d_model, heads, eps};
+  return h;
+}
+
+int cobra_layer_run(const cobra_layer_launch* h, const void* x, const uint8_t* valid_mask, void* y, float* resid_out,
+                    void* stream) {
+  if (!h || (valid_mask && !h->masked)) return kBad;
+  return cobra_layer_fwd(x, h->x_dtype, valid_mask, h->w_qkv, h->b_qkv, h->w_o, h->b_o, h->ln1_w, h->ln1_b, h->ln2_w,
+                         h->ln2_b, y, resid_out, h->workspace, h->workspace_bytes, h->batch, h->seq_len, h->d_model,
+                         h->heads, h->causal, h->eps, stream);
+}
+
+void cobra_layer_unbind(cobra_layer_launch* h) { delete h; }
 
 }  // extern "C"

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 2
+#define COBRA_ABI_VERSION 3
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
 
@@ -173,6 +173,27 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
                     const float* ln2_b, void* y, float* resid_out, void* workspace, int64_t workspace_bytes,
                     int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
                     void* stream);
+
+/*
+ * A prepared cobra_layer_fwd: everything but the activations and the stream is
+ * validated and bound once, so a steady-state forward crosses the ABI with six
+ * arguments.  cobra_layer_bind returns NULL for arguments cobra_layer_fwd would
+ * reject (workspace sized for `masked`); the handle is host memory only, owns
+ * none of the buffers it names, and is released with cobra_layer_unbind.
+ * cobra_layer_run(h, x, valid_mask, y, resid_out, stream) equals
+ * cobra_layer_fwd with the bound arguments; valid_mask must be NULL unless the
+ * handle was bound with masked = 1.  The counterpart of the reference's
+ * per-signature _prepare followed by a graph replay per forward
+ * (TTB:948-1081, 1331-1360).
+ */
+typedef struct cobra_layer_launch cobra_layer_launch;
+cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv, const float* b_qkv, const void* w_o,
+                                     const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
+                                     const float* ln2_b, void* workspace, int64_t workspace_bytes, int64_t batch,
+                                     int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps);
+int cobra_layer_run(const cobra_layer_launch* h, const void* x, const uint8_t* valid_mask, void* y, float* resid_out,
+                    void* stream);
+void cobra_layer_unbind(cobra_layer_launch* h);
 
 #ifdef __cplusplus
 }

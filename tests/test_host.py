@@ -54,6 +54,30 @@ def test_argument_validation_rejects_before_any_launch():
     assert lib.cobra_layer_plan(2, 16, 128, 4, 1) == _lib.PLAN_FUSED  # the fused kernels take token masks
 
 
+def test_layer_bind_validates_and_releases():
+    """cobra_layer_bind checks what cobra_layer_fwd would check, once; run rejects a
+    mask on a handle bound without one, before any launch."""
+    from cobra_amd import _lib
+
+    lib = _lib.lib()
+    w = [256 * (i + 1) for i in range(8)]  # aligned stand-in addresses: bind dereferences nothing
+    assert not lib.cobra_layer_bind(0, 0, 12, *w[1:], None, 0, 2, 16, 128, 4, 0, 1e-5)   # misaligned w_qkv
+    assert not lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 120, 10, 0, 1e-5)          # head_dim 12
+    assert not lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 128, 16, 0, 1e-5)          # staged: needs workspace
+    assert not lib.cobra_layer_bind(5, 0, *w, None, 0, 2, 16, 128, 4, 0, 1e-5)           # dtype code
+    h = lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 128, 4, 0, 1e-5)                  # fused: no workspace
+    assert h
+    assert lib.cobra_layer_run(h, 256, 512, 768, None, None) != 0  # mask on an unmasked handle
+    assert lib.cobra_layer_run(None, 256, None, 768, None, None) != 0
+    lib.cobra_layer_unbind(h)
+    lib.cobra_layer_unbind(None)
+    ws = lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 1)
+    h = lib.cobra_layer_bind(0, 1, *w, 4096, ws, 2, 16, 128, 16, 0, 1e-5)
+    assert h
+    lib.cobra_layer_unbind(h)
+    assert not lib.cobra_layer_bind(0, 1, *w, 4096, ws - 1, 2, 16, 128, 16, 0, 1e-5)
+
+
 def test_workspace_size_formula():
     from cobra_amd import ops
 
