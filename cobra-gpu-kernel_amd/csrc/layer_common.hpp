@@ -120,6 +120,26 @@ struct XChunks<float> {
   using c4 = f32x4;
 };
 
+// The value `v` of the partner lane (lane ^ 32), any 4-byte-multiple type, through
+// v_permlane32_swap: of the swap's two results one is this lane's own value, the
+// other the partner's (which is which depends on the half; equal bits either way).
+template <typename V>
+__device__ __forceinline__ V partner_value(const V& v) {
+  constexpr int NDW = sizeof(V) / 4;
+  static_assert(NDW * 4 == sizeof(V), "whole dwords");
+  struct Dw {
+    uint32_t u[NDW];
+  };
+  const Dw in = __builtin_bit_cast(Dw, v);
+  Dw out;
+#pragma unroll
+  for (int d = 0; d < NDW; ++d) {
+    const auto r = __builtin_amdgcn_permlane32_swap(in.u[d], in.u[d], false, false);
+    out.u[d] = r[0] == in.u[d] ? r[1] : r[0];
+  }
+  return __builtin_bit_cast(V, out);
+}
+
 // Query-split variant of the fused kernel (layer_split.hip): fp16
 // activations at d_model 64 / 128, while batch * ceil(S/32) workgroups take at
 // most two rounds of the chip.

@@ -41,8 +41,9 @@
 
 namespace cobra {
 
-// LDS plan of the fused kernel, in 16-byte chunks.
-template <int D, int HD>
+// LDS plan of the fused kernel, in 16-byte chunks.  G sequence groups (four
+// waves each) share the staged weights and have a K/V area each.
+template <int D, int HD, int G = 1>
 struct SmallLds {
   static constexpr int KD = D / 16;
   static constexpr int NDT = HD / 32;
@@ -52,7 +53,7 @@ struct SmallLds {
   static constexpr int WO = (D / 32) * KD * 64;
   static constexpr int KCH = MAXT * KSH * 64;
   static constexpr int VCH = MAXT * NDT * 2 * 64;
-  static constexpr int CORE = WQKV + WO + KCH + VCH;
+  static constexpr int CORE = WQKV + WO + G * (KCH + VCH);
   // Biases and LayerNorm parameters [b_qkv 3D | b_o | g1 | b1 | g2 | b2] = 8D
   // floats, kept in LDS too when they fit (otherwise read from global memory).
   static constexpr int PCH = 8 * D * 4 / 16;
@@ -62,15 +63,30 @@ struct SmallLds {
   static_assert(CORE * 16 <= kLdsBytes, "weights + K/V must fit the workgroup's LDS");
 };
 
-template <int D, int HD, bool CAUSAL, bool MASKED, typename TX>
-__global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
+// Two sequences per workgroup (eight waves, two per SIMD) when the weights and
+// two K/V areas fit the LDS: while one sequence's waves wait on a dependent
+// product or a load, the other's issue -- a lone wave per SIMD leaves the matrix
+// cores idle through every softmax and the vector ALUs idle through every product.
+template <int D, int HD, typename TX>
+constexpr int small_groups() {
+  using L1 = SmallLds<D, HD, 1>;
+  constexpr bool fits = (L1::WQKV + L1::WO + 2 * (L1::KCH + L1::VCH)) * 16 <= kLdsBytes;
+  // fp32 activations need more registers than two waves per SIMD leave (they spill).
+  // Wider models need more registers than two waves per SIMD leave (d_model 96
+  // spills; at 128 the second K/V area also pushes the parameters out of the LDS,
+  // and the pair measured slower than one sequence at a time).
+  return sizeof(TX) == 2 && fits && D <= 64 ? 2 : 1;
+}
+
+template <int D, int HD, bool CAUSAL, bool MASKED, typename TX, int G>
+__global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
                                                           const float* __restrict__ bqkv, const f16* __restrict__ wo,
                                                           const float* __restrict__ bo, const float* __restrict__ g1,
                                                           const float* __restrict__ be1, const float* __restrict__ g2,
                                                           const float* __restrict__ be2, TX* __restrict__ y,
                                                           float* __restrict__ resid_out, int B, int S, float c2,
                                                           float eps, const uint8_t* __restrict__ vmask) {
-  using L = SmallLds<D, HD>;
+  using L = SmallLds<D, HD, G>;
   constexpr int KD = L::KD;     // k-steps over d_model
   constexpr int NH = D / HD;    // heads
   constexpr int NDT = L::NDT;   // 32-row d-tiles per head
@@ -78,15 +94,16 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
   constexpr int NNT = D / 32;   // 32-column output tiles
   constexpr int MAXT = L::MAXT;
 
-  // [W_qkv chunks | W_o chunks | K^T of head j | V of head j], all operand-ready.
+  // [W_qkv chunks | W_o chunks | per group: K^T of head j | V of head j], all operand-ready.
   __shared__ f16x8 lds[L::TOTAL];
   f16x8* const Wl = lds;
   f16x8* const Wol = Wl + L::WQKV;
-  f16x8* const Kl = Wol + L::WO;
-  f16x8* const Vl = Kl + L::KCH;
 
   const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, provably uniform
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, provably uniform
+  const int w = wid % kSmallWaves, grp = wid / kSmallWaves;          // wave within its sequence group
+  f16x8* const Kl = Wol + L::WO + grp * (L::KCH + L::VCH);
+  f16x8* const Vl = Kl + L::KCH;
   const int li = lane & 31, g = lane >> 5;
   const int tok = w * 32 + li;
   const bool tok_ok = tok < S;
@@ -97,20 +114,21 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
   // W_o row (nt, ks):   lane -> W_o[32nt + lane%32][16ks + 4(lane/32) + {0..3, 8..11}]
   {
     constexpr int ROWS_Q = L::WQKV / 64, ROWS_O = L::WO / 64;
-    constexpr int RQ = (ROWS_Q + kSmallWaves - 1) / kSmallWaves, RO = (ROWS_O + kSmallWaves - 1) / kSmallWaves;
+    constexpr int NW = kSmallWaves * G;
+    constexpr int RQ = (ROWS_Q + NW - 1) / NW, RO = (ROWS_O + NW - 1) / NW;
     const f16* wq_lane = wqkv + (int64_t)(lane & 31) * D + 8 * (lane >> 5);
     const f16* wo_lane = wo + (int64_t)(lane & 31) * D + 4 * (lane >> 5);
     f16x8 tq[RQ], to[RO];
 #pragma unroll
     for (int u = 0; u < RQ; ++u) {
-      const int r = w + kSmallWaves * u;
-      if (ROWS_Q % kSmallWaves == 0 || r < ROWS_Q)
+      const int r = wid + NW * u;
+      if (ROWS_Q % NW == 0 || r < ROWS_Q)
         tq[u] = *reinterpret_cast<const f16x8*>(wq_lane + (int64_t)(32 * (r / KD)) * D + 16 * (r % KD));
     }
 #pragma unroll
     for (int u = 0; u < RO; ++u) {
-      const int r = w + kSmallWaves * u;
-      if (ROWS_O % kSmallWaves == 0 || r < ROWS_O) {
+      const int r = wid + NW * u;
+      if (ROWS_O % NW == 0 || r < ROWS_O) {
         const f16* p = wo_lane + (int64_t)(32 * (r / KD)) * D + 16 * (r % KD);
         const f16x4 lo = *reinterpret_cast<const f16x4*>(p);
         const f16x4 hi = *reinterpret_cast<const f16x4*>(p + 8);
@@ -119,10 +137,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
     }
 #pragma unroll
     for (int u = 0; u < RQ; ++u)
-      if (ROWS_Q % kSmallWaves == 0 || w + kSmallWaves * u < ROWS_Q) Wl[(w + kSmallWaves * u) * 64 + lane] = tq[u];
+      if (ROWS_Q % NW == 0 || wid + NW * u < ROWS_Q) Wl[(wid + NW * u) * 64 + lane] = tq[u];
 #pragma unroll
     for (int u = 0; u < RO; ++u)
-      if (ROWS_O % kSmallWaves == 0 || w + kSmallWaves * u < ROWS_O) Wol[(w + kSmallWaves * u) * 64 + lane] = to[u];
+      if (ROWS_O % NW == 0 || wid + NW * u < ROWS_O) Wol[(wid + NW * u) * 64 + lane] = to[u];
   }
   float* const Pf = reinterpret_cast<float*>(lds + L::CORE);
   if constexpr (L::PARAMS) {
@@ -131,7 +149,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
     int off = 0;
 #pragma unroll
     for (int v = 0; v < 6; ++v) {
-      for (int i = 4 * (int)threadIdx.x; i < len[v]; i += 4 * 64 * kSmallWaves)
+      for (int i = 4 * (int)threadIdx.x; i < len[v]; i += 4 * 64 * kSmallWaves * G)
         *reinterpret_cast<f32x4*>(Pf + off + i) = *reinterpret_cast<const f32x4*>(src[v] + i);
       off += len[v];
     }
@@ -158,13 +176,18 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
       }
     }
   };
-  load_ln1_input(blockIdx.x);
+  // Workgroup blk takes sequence groups blk, blk + gridDim.x, ...; group grp of it
+  // handles sequence G * that + grp.  Every wave runs every trip (the barriers are
+  // workgroup-wide): a group past the batch computes on zeros and stores nothing.
+  const int ngroups = (B + G - 1) / G;
+  load_ln1_input((int)blockIdx.x * G + grp);
 
-  for (int seq = blockIdx.x; seq < B; seq += gridDim.x) {
+  for (int sg = blockIdx.x; sg < ngroups; sg += gridDim.x) {
+    const int seq = sg * G + grp;
+    const bool live = G == 1 || seq < B;
     const int64_t row = (int64_t)seq * S + tok;
     KeyBits kbits{~0ull, ~0ull};
     if constexpr (MASKED) kbits = key_bits_of(kpre, S, lane);
-    const TX* xrow = x + row * D;
     const float *gamma1, *beta1, *gamma2, *beta2, *bias_o, *bias_qkv;
     if constexpr (L::PARAMS) {
       bias_qkv = Pf;
@@ -227,8 +250,22 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
       f16x8 qB[KSH];
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        f32x16 qa = zero16(), ka = zero16(), va = zero16();
         const int d0 = j * HD + dt * 32;
+        // The biases start the accumulators (C operand of the first product).
+        f32x16 qa, ka, va;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4 tq = *reinterpret_cast<const f32x4*>(bias_qkv + d0 + 8 * qd + 4 * g);
+          const f32x4 tk = *reinterpret_cast<const f32x4*>(bias_qkv + D + d0 + 8 * qd + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            qa[4 * qd + e] = tq[e];
+            ka[4 * qd + e] = tk[e];
+          }
+        }
+        const float bvl = bias_qkv[2 * D + d0 + li];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) va[r] = bvl;
         const f16x8* wq = Wl + (d0 / 32) * KD * 64 + lane;
         const f16x8* wk = wq + (D / 32) * KD * 64;
         const f16x8* wv = wk + (D / 32) * KD * 64;
@@ -241,104 +278,68 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
           ka = mfma32x32x16(ak, hB[kk], ka);
           va = mfma32x32x16(hB[kk], bv, va);
         }
-        float bq[16], bk[16], bvv[16];
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const f32x4 tq = *reinterpret_cast<const f32x4*>(bias_qkv + d0 + 8 * qd + 4 * g);
-          const f32x4 tk = *reinterpret_cast<const f32x4*>(bias_qkv + D + d0 + 8 * qd + 4 * g);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            bq[4 * qd + e] = tq[e];
-            bk[4 * qd + e] = tk[e];
-          }
-        }
-        const float bvl = bias_qkv[2 * D + d0 + li];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) bvv[r] = bvl;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          qB[2 * dt + half] = half_to_f16(qa, half, bq);
-          Kl[(w * KSH + 2 * dt + half) * 64 + lane] = half_to_f16(ka, half, bk);
-          Vl[((w * NDT + dt) * 2 + half) * 64 + lane] = half_to_f16(va, half, bvv);
+          qB[2 * dt + half] = acc_f16(qa, half);
+          Kl[(w * KSH + 2 * dt + half) * 64 + lane] = acc_f16(ka, half);
+          Vl[((w * NDT + dt) * 2 + half) * 64 + lane] = acc_f16(va, half);
         }
       }
       __syncthreads();
 
-      // ---- S^T = K Q^T, softmax and O^T = V^T P^T over two blocks of two key
-      // tiles (64 keys): the running max / sum rescale happens once, between the
-      // blocks, and only half of the scores are live at a time.
-      f32x16 ot[NDT];
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) ot[dt] = zero16();
-      float m_run = MASKED ? kNegInf : 0.f, l = 0.f;
+      // ---- S^T = K Q^T for all (at most 128) keys, one exact softmax pass (no
+      // running max, no rescale), O^T = V^T P^T.
       // Every key tile is computed, branch-free: all four waves always write their
       // K/V slots (finite values, also past S), and masked keys get p = 0.  The
       // wasted tiles cost no latency -- the slowest wave bounds every barrier.
+      f32x16 sacc[MAXT];
+      float mx = kNegInf;
 #pragma unroll
-      for (int blk = 0; blk < MAXT / 2; ++blk) {
-        f32x16 sacc[2];
-        float mx = kNegInf;
+      for (int t = 0; t < MAXT; ++t) {
+        sacc[t] = zero16();
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int t = 2 * blk + u;
-          sacc[u] = zero16();
+        for (int ks = 0; ks < KSH; ++ks) sacc[t] = mfma32x32x16(Kl[(t * KSH + ks) * 64 + lane], qB[ks], sacc[t]);
+        // Keys past S (last tile) and keys after the query (diagonal and later
+        // tiles).  The bound is made opaque per head so that the 16 per-register
+        // lane masks are formed here rather than hoisted (and spilled) across loops.
+        if (32 * t + 32 > S || (CAUSAL && t >= w)) {
+          int lim = S - 32 * t - 4 * g + opaque_zero();  // valid: offset < lim
+          if (CAUSAL) lim = min(lim, tok - 32 * t - 4 * g + 1);
 #pragma unroll
-          for (int ks = 0; ks < KSH; ++ks) sacc[u] = mfma32x32x16(Kl[(t * KSH + ks) * 64 + lane], qB[ks], sacc[u]);
-          // Keys past S (last tile) and keys after the query (diagonal and later
-          // tiles).  The bound is made opaque per head so that the 16 per-register
-          // lane masks are formed here rather than hoisted (and spilled) across loops.
-          if (32 * t + 32 > S || (CAUSAL && t >= w)) {
-            int lim = S - 32 * t - 4 * g + opaque_zero();  // valid: offset < lim
-            if (CAUSAL) lim = min(lim, tok - 32 * t - 4 * g + 1);
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              if (8 * (r >> 2) + (r & 3) >= lim) sacc[u][r] = kNegInf;
-          }
-          if constexpr (MASKED) {
-            if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc[u], kbits.tile(t), g);
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[u][r]);
+          for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) >= lim) sacc[t][r] = kNegInf;
         }
-        mx = max_xor32(mx);
-        float m_new, alpha;
         if constexpr (MASKED) {
-          const SoftmaxStep st = masked_softmax_step(m_run, mx * c2);
-          m_new = st.m_use;
-          alpha = st.alpha;
-        } else {
-          m_new = blk == 0 ? mx * c2 : fmaxf(m_run, mx * c2);  // block 0 always holds key 0
-          alpha = blk == 0 ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-          m_run = m_new;
+          if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc[t], kbits.tile(t), g);
         }
-        f16x8 pB[2][2];
-        float ps = 0.f;
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
+      }
+      mx = max_xor32(mx);
+      // Unmasked, key 0 is valid for every query (finite max); a query whose keys
+      // are all padded gets max -inf, all-zero probabilities and a zero row.
+      float m = mx * c2;
+      if constexpr (MASKED) m = mx == kNegInf ? 0.f : m;
+      f32x16 ot[NDT];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[u][r], c2, -m_new));
-            ps += pv;
-            pB[u][r >> 3][r & 7] = (f16)pv;
-          }
-        if (blk == 0) {
-          l = ps;
-        } else {
-          l = l * alpha + ps;
+      for (int dt = 0; dt < NDT; ++dt) ot[dt] = zero16();
+      float lp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) {
+        f16x8 pB[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
+          lp[r & 3] += pv;
+          pB[r >> 3][r & 7] = (f16)pv;
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) ot[dt][r] *= alpha;
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int half = 0; half < 2; ++half)
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-              ot[dt] = mfma32x32x16(Vl[(((2 * blk + u) * NDT + dt) * 2 + half) * 64 + lane], pB[u][half], ot[dt]);
+            ot[dt] = mfma32x32x16(Vl[((t * NDT + dt) * 2 + half) * 64 + lane], pB[half], ot[dt]);
       }
-      l = sum_xor32(l);
+      const float l = sum_xor32((lp[0] + lp[1]) + (lp[2] + lp[3]));
       // A query with no valid key (only a padded one) gets a zero row.
       const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
 #pragma unroll
@@ -349,25 +350,33 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- prefetch: this sequence's residual, the next sequence's LN1 input -------
+    // ---- this sequence's residual, from the LN1 input still in registers: lane
+    // (tok, g) holds columns 16kk + 8g + {0..7}; the out-projection layout wants
+    // 32nt + 8qd + 4g + {0..3}, whose other half sits in the partner lane (tok, 1 - g).
+    // Rows past S (and groups past the batch) were loaded as zeros.
     Raw4 xres[NNT][4];
+#pragma unroll
+    for (int kk = 0; kk < KD; ++kk) {
+      const Raw4 lo = {xpre[kk][0], xpre[kk][1], xpre[kk][2], xpre[kk][3]};
+      const Raw4 hi = {xpre[kk][4], xpre[kk][5], xpre[kk][6], xpre[kk][7]};
+      const Raw4 recv = partner_value(g ? lo : hi);  // the half the partner lacks, both ways
+      const int nt = kk / 2, j = kk % 2;             // columns 16kk.. = tile nt, qd 2j and 2j + 1
+      xres[nt][2 * j] = g ? recv : lo;
+      xres[nt][2 * j + 1] = g ? hi : recv;
+    }
+    // ---- prefetch: the next sequence's LN1 input --------------------------------------
+    load_ln1_input((sg + (int)gridDim.x) * G + grp);
+
+    // ---- out^T = W_o ctx^T over all heads, started from b_o ---------------------------
+    f32x16 oacc[NNT];  // lane (tok, g), reg r -> column 32nt + 8(r/4) + 4g + r%4
 #pragma unroll
     for (int nt = 0; nt < NNT; ++nt)
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        if (tok_ok) {
-          xres[nt][qd] = *reinterpret_cast<const Raw4*>(xrow + 32 * nt + 8 * qd + 4 * g);
-        } else {
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(bias_o + 32 * nt + 8 * qd + 4 * g);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) xres[nt][qd][e] = (TX)0.0f;
-        }
+        for (int e = 0; e < 4; ++e) oacc[nt][4 * qd + e] = bb[e];
       }
-    load_ln1_input(seq + gridDim.x);
-
-    // ---- out^T = W_o ctx^T over all heads -----------------------------------------
-    f32x16 oacc[NNT];  // lane (tok, g), reg r -> column 32nt + 8(r/4) + 4g + r%4
-#pragma unroll
-    for (int nt = 0; nt < NNT; ++nt) oacc[nt] = zero16();
 #pragma unroll
     for (int ks = 0; ks < KD; ++ks)
 #pragma unroll
@@ -381,15 +390,12 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
 #pragma unroll
     for (int nt = 0; nt < NNT; ++nt)
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int n0 = 32 * nt + 8 * qd + 4 * g;
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(bias_o + n0);
+      for (int qd = 0; qd < 4; ++qd)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[nt][qd][e] = (tv ? oacc[nt][4 * qd + e] + bb[e] : 0.f) + (float)xres[nt][qd][e];
+          v[nt][qd][e] = (tv ? oacc[nt][4 * qd + e] : 0.f) + (float)xres[nt][qd][e];
           s += v[nt][qd][e];
         }
-      }
     const float mean = sum_xor32(s) * (1.0f / D);
     float q = 0.f;
 #pragma unroll
@@ -402,21 +408,57 @@ __global__ __launch_bounds__(64 * kSmallWaves) void layer_small_kernel(const TX*
           q += t * t;
         }
     const float rstd = rsqrtf(sum_xor32(q) * (1.0f / D) + eps);
-    if (tok_ok) {
-      TX* yrow = y + row * D;
+    float o[NNT][4][4];
+#pragma unroll
+    for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n0 = 32 * nt + 8 * qd + 4 * g;
+        const f32x4 gg = *reinterpret_cast<const f32x4*>(gamma2 + n0);
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(beta2 + n0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[nt][qd][e] = (v[nt][qd][e] - mean) * rstd * gg[e] + bb[e];
+      }
+    // fp16 rows leave as 16-byte pieces: for each pair of quads (qd = 2p, 2p + 1)
+    // lane g = 0 collects columns 32nt + 16p + {0..7} and lane g = 1 columns
+    // 32nt + 16p + 8 + {0..7}, one exchange with the partner lane each.
+    if constexpr (sizeof(TX) == 2) {
+      f16x8 yo[NNT][2];
 #pragma unroll
       for (int nt = 0; nt < NNT; ++nt)
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int n0 = 32 * nt + 8 * qd + 4 * g;
-          const f32x4 gg = *reinterpret_cast<const f32x4*>(gamma2 + n0);
-          const f32x4 bb = *reinterpret_cast<const f32x4*>(beta2 + n0);
-          float o[4];
+        for (int pr = 0; pr < 2; ++pr) {
+          f16x4 h0, h1;  // this lane's quads 2pr and 2pr + 1
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = (v[nt][qd][e] - mean) * rstd * gg[e] + bb[e];
-          store4(yrow + n0, o);
-          if (resid_out) store4(resid_out + row * D + n0, v[nt][qd]);
+          for (int e = 0; e < 4; ++e) {
+            h0[e] = (f16)o[nt][2 * pr][e];
+            h1[e] = (f16)o[nt][2 * pr + 1][e];
+          }
+          const f16x4 recv = partner_value(g ? h0 : h1);
+          const f16x4 a = g ? recv : h0, b = g ? h1 : recv;
+          yo[nt][pr] = f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
         }
+      if (tok_ok && live) {
+        TX* yrow = y + row * D;
+#pragma unroll
+        for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr) *reinterpret_cast<f16x8*>(yrow + 32 * nt + 16 * pr + 8 * g) = yo[nt][pr];
+      }
+    } else {
+      if (tok_ok && live) {
+        TX* yrow = y + row * D;
+#pragma unroll
+        for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) store4(yrow + 32 * nt + 8 * qd + 4 * g, o[nt][qd]);
+      }
+    }
+    if (resid_out && tok_ok && live) {
+#pragma unroll
+      for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) store4(resid_out + row * D + 32 * nt + 8 * qd + 4 * g, v[nt][qd]);
     }
   }  // sequence loop
 }
@@ -436,14 +478,16 @@ bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads) {
 // share the weight staging (and compute masked tiles nobody reads).
 template <int D, int HD, bool CAUSAL, typename TX>
 static hipError_t launch_small(const SmallLayerArgs& a, float c2) {
-  const int64_t grid = a.batch < compute_units() ? a.batch : compute_units();
+  constexpr int G = small_groups<D, HD, TX>();
+  const int64_t groups = (a.batch + G - 1) / G;
+  const int64_t grid = groups < compute_units() ? groups : compute_units();
   if (a.valid_mask)
-    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, true, TX>), dim3((unsigned)grid), dim3(64 * kSmallWaves), 0,
+    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, true, TX, G>), dim3((unsigned)grid), dim3(64 * kSmallWaves * G), 0,
                        a.stream, static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
                        static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
                        static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps, a.valid_mask);
   else
-    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, false, TX>), dim3((unsigned)grid), dim3(64 * kSmallWaves), 0,
+    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, false, TX, G>), dim3((unsigned)grid), dim3(64 * kSmallWaves * G), 0,
                        a.stream, static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
                        static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
                        static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps, nullptr);

@@ -46,6 +46,7 @@ def token_mask(B, S, seed, left_aligned):
         (4, 128, 64, 2),     # query-split, d_model 64
         (300, 128, 128, 4),  # persistent fused kernel (more than two rounds of slices)
         (3, 17, 96, 3),      # persistent fused kernel, d_model 96
+        (301, 96, 64, 2),    # persistent, d_model 64: two sequences per workgroup, odd batch
         (3, 333, 128, 2),    # hd 64, several key blocks, 8-wave attention
         (3, 100, 256, 2),    # hd 128, D > 128 (separate LN2 pass)
         (3, 40, 512, 2),     # hd 256 (32-key blocks)

@@ -151,6 +151,7 @@ def test_graph_replays_match_eager(D, H):
         (1100, 128, 128, 2, False),
         (2100, 65, 96, 3, False),
         (4200, 40, 64, 1, True),
+        (4201, 128, 64, 2, False),  # two sequences per workgroup; the last one's partner is idle
     ],
 )
 def test_fused_persistent_kernel(B, S, D, H, causal):
