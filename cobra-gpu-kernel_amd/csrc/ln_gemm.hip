@@ -15,6 +15,7 @@
 // accumulator layout would give.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "layer_common.hpp"
 
 namespace cobra {
 
@@ -350,6 +351,175 @@ hipError_t run_gemm_ln_rows(const GemmArgs& a) {
   return y16 ? gemm_ln_rows_shape<f16, f16>(a) : gemm_ln_rows_shape<f16, float>(a);
 }
 
+// ---------------------------------------------------------------------------------------
+// Persistent form for d_model 128 and N = 128 NT columns (the QKV projection: N = 384):
+// a workgroup per CU keeps all of W in LDS and walks blocks of BM rows, so W is read
+// once per CU rather than once per tile, and the next block's rows are loaded into
+// registers while the current block's products run.  Wave w owns output columns
+// 32 NT w .. 32 NT w + 32 NT - 1 of every block (NT x BM/32 accumulators, started
+// from the bias); the fp16 results leave as 16-byte row pieces after one exchange
+// with the partner lane.  The tile-per-workgroup kernel above serialises load,
+// LayerNorm, products and stores inside each workgroup, two per CU.
+template <int NT, int BM, typename TX>
+__global__ __launch_bounds__(kLgThreads) void ln_gemm_p_kernel(const TX* __restrict__ x, const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, const f16* __restrict__ W,
+                                                             const float* __restrict__ bias, f16* __restrict__ C,
+                                                             int64_t M, float eps) {
+  constexpr int D = 128, ROWB = 2 * D, CPR = D / 8;  // 16 chunks of 16 bytes per row
+  constexpr int N = 128 * NT;
+  constexpr int RT = BM / 32;                         // 32-row tiles per block
+  constexpr int PASSES = BM * CPR / kLgThreads;       // LayerNorm rows per thread
+  static_assert(BM % 32 == 0 && PASSES >= 1, "block rows");
+  __shared__ __attribute__((aligned(16))) char smem[N * ROWB + 2 * BM * ROWB];
+  char* const Ws = smem;
+  char* const Hs = smem + N * ROWB;  // two buffers of BM normalised rows
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 31, g = lane >> 5;
+  const int rp = tid / CPR, cl = tid % CPR;  // LayerNorm: row rp of each 16-row pass, chunk cl
+  const int64_t nblk = (M + BM - 1) / BM;
+
+  // W rows, swizzled: chunk c of row r at c ^ (r & 15).
+#pragma unroll
+  for (int b0 = 0; b0 < N * CPR / kLgThreads; b0 += 8) {
+    f16x8 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + kLgThreads * (b0 + i);
+      v[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)(c / CPR) * D + 8 * (c % CPR));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + kLgThreads * (b0 + i), r = c / CPR;
+      *reinterpret_cast<f16x8*>(Ws + r * ROWB + 16 * ((c % CPR) ^ (r & 15))) = v[i];
+    }
+  }
+  float gv[8], bv[8];
+  load8(gamma + 8 * cl, gv);
+  load8(beta + 8 * cl, bv);
+  // Bias of this wave's columns in the accumulator layout: tile t, register r ->
+  // column 32 NT w + 32 t + 8 (r / 4) + 4 g + r % 4.
+  f32x16 bt[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = 32 * NT * w + 32 * t + 8 * q + 4 * g;
+      const f32x4 b4 = bias ? *reinterpret_cast<const f32x4*>(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bt[t][4 * q + e] = b4[e];
+    }
+
+  // Rows of block `blk` for this thread's LayerNorm slots (zeros past M).
+  float xv[PASSES][8];
+  auto load_rows = [&](int64_t blk) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int64_t row = blk * BM + 16 * p + rp;
+      if (blk < nblk && row < M) {
+        load8(x + row * D + 8 * cl, xv[p]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[p][e] = 0.f;
+      }
+    }
+  };
+  load_rows(blockIdx.x);
+  int buf = 0;
+  for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x, buf ^= 1) {
+    char* const H = Hs + buf * BM * ROWB;
+    // ---- LayerNorm of the block's rows into H ----------------------------------------
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += xv[p][e];
+      const float mean = group_sum<CPR>(s) * (1.0f / D);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float t = xv[p][e] - mean;
+        q += t * t;
+      }
+      const float rstd = rsqrtf(group_sum<CPR>(q) * (1.0f / D) + eps);
+      f16x8 h;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[p][e] - mean) * rstd * gv[e] + bv[e]);
+      const int r = 16 * p + rp;
+      *reinterpret_cast<f16x8*>(H + r * ROWB + 16 * (cl ^ (r & 15))) = h;
+    }
+    // One barrier per block: H of this block is complete, and (double buffering)
+    // every wave finished the previous block's reads of the other buffer.
+    __syncthreads();
+    load_rows(blk + gridDim.x);
+
+    // ---- products: NT column tiles x RT row tiles per wave ----------------------------
+    f32x16 acc[NT][RT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < RT; ++i) acc[t][i] = bt[t];
+    const int sw = li & 15;  // rows 32i + li and 32 NT w + 32t + li share this swizzle
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      const int co = 16 * ((2 * kk + g) ^ sw);
+      f16x8 hf[RT], wf[NT];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) hf[i] = *reinterpret_cast<const f16x8*>(H + (32 * i + li) * ROWB + co);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        wf[t] = *reinterpret_cast<const f16x8*>(Ws + (32 * NT * w + 32 * t + li) * ROWB + co);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) acc[t][i] = mfma32x32x16(wf[t], hf[i], acc[t][i]);
+    }
+
+    // ---- fp16 out: lane (li, g) of tile (t, i) holds row 32i + li, columns
+    // 32 NT w + 32t + 8q + 4g + {0..3}; pairs of quads become 16-byte pieces.  (Staging
+    // the block through LDS for whole-row stores measured no faster: the kernel is
+    // bound by how few writes one workgroup per CU keeps in flight, not their shape.)
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const int64_t m = blk * BM + 32 * i + li;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          f16x4 h0, h1;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            h0[e] = (f16)acc[t][i][8 * pr + e];
+            h1[e] = (f16)acc[t][i][8 * pr + 4 + e];
+          }
+          const f16x4 recv = partner_value(g ? h0 : h1);
+          const f16x4 a = g ? recv : h0, b = g ? h1 : recv;
+          if (m < M)
+            *reinterpret_cast<f16x8*>(C + m * N + 32 * NT * w + 32 * t + 16 * pr + 8 * g) =
+                f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        }
+    }
+  }
+}
+
+template <int NT, typename TX>
+static hipError_t launch_ln_gemm_p(const LnGemmArgs& a) {
+  const int64_t cus = compute_units();
+  if (a.M >= (int64_t)64 * 2 * cus) {
+    const int64_t nblk = (a.M + 63) / 64;
+    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 64, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(kLgThreads), 0,
+                       a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
+                       static_cast<f16*>(a.c), a.M, a.eps);
+  } else {
+    const int64_t nblk = (a.M + 31) / 32;
+    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 32, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(kLgThreads), 0,
+                       a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
+                       static_cast<f16*>(a.c), a.M, a.eps);
+  }
+  return hipGetLastError();
+}
+
 template <int D, typename TX>
 static hipError_t launch_ln_gemm(const LnGemmArgs& a) {
   const int64_t tiles = ((a.M + kLgBM - 1) / kLgBM) * (int64_t)((a.N + kLgBN - 1) / kLgBN);
@@ -366,6 +536,7 @@ hipError_t run_ln_gemm(const LnGemmArgs& a) {
   if (!ln_gemm_ok(a.d, a.x_dtype) || a.M < 0 || a.N <= 0 || a.N % 8 != 0 || a.N > 3 * a.d) return hipErrorInvalidValue;
   if (!a.x || !a.w || !a.c || !a.gamma || !a.beta) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;
+  if (a.d == 128 && a.N == 384) return a.x_dtype == kF16 ? launch_ln_gemm_p<3, f16>(a) : launch_ln_gemm_p<3, float>(a);
   if (a.d == 128) return a.x_dtype == kF16 ? launch_ln_gemm<128, f16>(a) : launch_ln_gemm<128, float>(a);
   return a.x_dtype == kF16 ? launch_ln_gemm<64, f16>(a) : launch_ln_gemm<64, float>(a);
 }

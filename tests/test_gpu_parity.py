@@ -397,7 +397,8 @@ def test_ln_linear_op(d, xdt):
     from cobra_amd import ops
 
     torch.manual_seed(d)
-    for M, N in [(8192, 3 * d), (65536, 3 * d), (1000, 3 * d), (77, 2 * d + 8), (3, 8)]:
+    # d 128 with N in {128, 256, 384} takes the persistent kernel (32- and 64-row blocks)
+    for M, N in [(8192, 3 * d), (65536, 3 * d), (1000, 3 * d), (77, 2 * d + 8), (3, 8), (4097, d), (70001, 2 * d)]:
         x = (torch.randn(M, d, device=DEV) * 1.5 + 0.3).to(xdt)
         g = torch.rand(d, device=DEV) + 0.5
         be = torch.randn(d, device=DEV) * 0.2
