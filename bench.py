@@ -104,7 +104,7 @@ def layer_launcher(layer, x, y):
 
     p = layer._packed()
     B, S, D = x.shape
-    ws = torch.empty(ops.layer_workspace_bytes(B, S, D, layer.attention.num_heads), dtype=torch.uint8,
+    ws = torch.empty(ops.layer_workspace_bytes(B, S, D, layer.attention.num_heads, False, x.dtype), dtype=torch.uint8,
                      device=x.device)
 
     def launch():

@@ -17,12 +17,14 @@ mirrors the reference's orchestration (TTB:857-1541):
   parameters.  The pack is rebuilt whenever a parameter changes (in-place
   updates bump its version), which the reference did only on shape changes;
 * the library picks the plan: one fused kernel for the whole sublayer
-  (S <= 128, d_model <= 128) or a staged pipeline of four kernels.  A staged
-  plan on a small input (<= 64 MiB, TTB:1077-1079) is captured once into a
-  hipGraph (``torch.cuda.CUDAGraph`` on ROCm) and replayed, with the output
-  buffer returned without a clone as the reference does (TTB:1356-1360); the
-  fused plan is one direct launch, because replaying a one-node graph costs
-  about four times a direct launch on this runtime (``graph=True`` forces it);
+  (S <= 128, d_model <= 128) or a staged pipeline of four kernels.  Either is
+  launched directly by default: on this runtime a hipGraph replay carries
+  ~13 us of fixed latency against ~2.5 us per direct launch, and the sublayer
+  is one to five launches, so the reference's graph gate (small inputs,
+  TTB:1077-1079) would cost 10-20 us per forward here.  ``graph=True``
+  captures the forward once into a hipGraph (``torch.cuda.CUDAGraph`` on ROCm)
+  for inputs <= 64 MiB and replays it, with the output buffer returned without
+  a clone as the reference does (TTB:1356-1360);
 * inputs that do not fit one device pass are streamed in batch chunks sized
   from ``hipMemGetInfo`` with halve-on-OOM (``streaming``, TTB:1364-1508);
 * ``valid_token_mask`` ([B, S] bool) masks padded keys and zeroes the padded
@@ -102,9 +104,9 @@ class CobraAttentionSublayer(nn.Module):
         self.attention = CobraSelfAttention(d_model, num_heads)
         self.norm2 = nn.LayerNorm(d_model, eps=eps)
         self.causal = causal
-        # hipGraph replay: None = automatic (multi-kernel plans on inputs <= 64 MiB;
-        # a single-kernel plan launches directly, which measures ~4x cheaper than
-        # replaying a one-node graph); True / False force it.
+        # hipGraph replay: None / False = direct launches (cheaper for the one to five
+        # launches of a sublayer on this runtime); True = replay a captured graph for
+        # inputs <= 64 MiB.
         self.graph = graph
         # Upper bound on sequences per device pass when a batch is streamed (None: from free memory).
         self.stream_chunk: Optional[int] = None
@@ -237,13 +239,11 @@ class CobraAttentionSublayer(nn.Module):
         workspace, graph gate.  Never runs on the steady-state path."""
         B, S, D = x.shape
         H = self.attention.num_heads
-        self.plan = ops.layer_plan(B, S, D, H, masked)
-        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H, masked), dtype=torch.uint8, device=x.device)
+        self.plan = ops.layer_plan(B, S, D, H, masked, x.dtype)
+        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H, masked, x.dtype), dtype=torch.uint8,
+                               device=x.device)
         small = x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
-        if self.graph is None:
-            self._graph_ok = small and self.plan != ops.PLAN_FUSED
-        else:
-            self._graph_ok = bool(self.graph) and small
+        self._graph_ok = bool(self.graph) and small
         self._graph = None
         self._static_x = self._static_y = self._static_r = self._static_m = None
         self._fast = None
@@ -290,7 +290,9 @@ class CobraAttentionSublayer(nn.Module):
 
     def _per_seq_bytes(self, x: torch.Tensor, return_residual: bool) -> int:
         B, S, D = x.shape
-        ws = ops.layer_workspace_bytes(1, S, D, self.attention.num_heads, True)
+        # The staged plan's workspace, which is linear in the batch: chunks that
+        # take the fused plan instead need less.
+        ws = -(-ops.layer_workspace_bytes(B, S, D, self.attention.num_heads, True, torch.float32) // B) if B else 0
         return streaming.live_bytes_per_sequence(ws, S, D, x.element_size(), return_residual)
 
     def _stream_needed(self, x: torch.Tensor) -> bool:
@@ -324,7 +326,8 @@ class CobraAttentionSublayer(nn.Module):
         def workspace(n: int) -> torch.Tensor:
             if n not in ws_cache:
                 ws_cache.clear()
-                ws_cache[n] = torch.empty(ops.layer_workspace_bytes(n, S, D, self.attention.num_heads, masked),
+                ws_cache[n] = torch.empty(ops.layer_workspace_bytes(n, S, D, self.attention.num_heads, masked,
+                                                                    x.dtype),
                                           dtype=torch.uint8, device=dev)
             return ws_cache[n]
 

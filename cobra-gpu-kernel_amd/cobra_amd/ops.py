@@ -317,16 +317,26 @@ PLAN_FUSED = _lib.PLAN_FUSED
 PLAN_STAGED = _lib.PLAN_STAGED
 
 
-def layer_plan(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False) -> int:
-    """PLAN_FUSED (one kernel) or PLAN_STAGED for this shape (host-only query)."""
-    p = _lib.lib().cobra_layer_plan(batch, seq_len, d_model, heads, 1 if masked else 0)
+def _dt_of(dtype: torch.dtype) -> int:
+    try:
+        return _DT[dtype]
+    except KeyError:
+        raise TypeError(f"dtype {dtype} not supported (float16 or float32)") from None
+
+
+def layer_plan(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False,
+               dtype: torch.dtype = torch.float16) -> int:
+    """PLAN_FUSED (one kernel) or PLAN_STAGED for this shape and activation dtype
+    (host-only query)."""
+    p = _lib.lib().cobra_layer_plan(batch, seq_len, d_model, heads, 1 if masked else 0, _dt_of(dtype))
     if p < 0:
         raise ValueError(f"unsupported sublayer shape B={batch} S={seq_len} D={d_model} H={heads}")
     return int(p)
 
 
-def layer_workspace_bytes(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False) -> int:
-    n = _lib.lib().cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, 1 if masked else 0)
+def layer_workspace_bytes(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False,
+                          dtype: torch.dtype = torch.float16) -> int:
+    n = _lib.lib().cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, 1 if masked else 0, _dt_of(dtype))
     if n < 0:
         raise ValueError(f"unsupported sublayer shape B={batch} S={seq_len} D={d_model} H={heads}")
     return int(n)

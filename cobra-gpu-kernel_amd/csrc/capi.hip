@@ -137,14 +137,15 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
   return code(cobra::run_attn(a));
 }
 
-int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked) {
-  if (!layer_shape_ok(batch, seq_len, d_model, heads)) return -1;
+int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked, int x_dtype) {
+  if (!layer_shape_ok(batch, seq_len, d_model, heads) || !is_dtype(x_dtype)) return -1;
   (void)masked;  // both plans take a token mask
-  return cobra::layer_small_ok(seq_len, d_model, heads) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
+  return cobra::layer_fused_ok(batch, seq_len, d_model, heads, x_dtype) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
 }
 
-int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked) {
-  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked);
+int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked,
+                                    int x_dtype) {
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked, x_dtype);
   if (plan < 0) return -1;
   return plan == COBRA_PLAN_FUSED ? 0 : layer_buffers(batch, seq_len, d_model, masked != 0).total;
 }
@@ -155,8 +156,8 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
                     int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
                     void* stream) {
   const bool masked = valid_mask != nullptr;
-  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked);
-  if (plan < 0 || !is_dtype(x_dtype)) return kBad;
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked, x_dtype);
+  if (plan < 0) return kBad;
   const void* must[] = {x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y};
   for (const void* p : must)
     if (!p || !aligned16(p)) return kBad;
@@ -233,13 +234,13 @@ cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv,
                                      const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
                                      const float* ln2_b, void* workspace, int64_t workspace_bytes, int64_t batch,
                                      int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps) {
-  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked);
-  if (plan < 0 || !is_dtype(x_dtype)) return nullptr;
+  const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked, x_dtype);
+  if (plan < 0) return nullptr;
   const void* must[] = {w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b};
   for (const void* p : must)
     if (!p || !aligned16(p)) return nullptr;
   if (!opt_aligned16(workspace)) return nullptr;
-  const int64_t need = cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, masked);
+  const int64_t need = cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, masked, x_dtype);
   if (need > 0 && (!workspace || workspace_bytes < need)) return nullptr;
   auto* h = new (std::nothrow) cobra_layer_launch;
   if (!h) return nullptr;

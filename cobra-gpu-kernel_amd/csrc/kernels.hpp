@@ -145,6 +145,9 @@ struct SmallLayerArgs {
   const uint8_t* valid_mask = nullptr;  // optional [B, S] token mask, 0 = padded
 };
 bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads);
+// Whether run_layer_small takes this call: the persistent kernel's shapes, or
+// the query-split kernel's (which adds head_dim 128) when it pays for the batch.
+bool layer_fused_ok(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int x_dtype);
 hipError_t run_layer_small(const SmallLayerArgs& a);
 
 }  // namespace cobra

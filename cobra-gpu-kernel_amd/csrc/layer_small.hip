@@ -513,14 +513,20 @@ static hipError_t small_shape(const SmallLayerArgs& a, float c2) {
   return small_dtype<96, 32, CAUSAL>(a, c2);
 }
 
+bool layer_fused_ok(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int x_dtype) {
+  if (x_dtype != kF16 && x_dtype != kF32) return false;
+  return layer_small_ok(seq_len, d_model, heads) ||
+         (layer_split_ok(seq_len, d_model, heads) && layer_split_pays(batch, seq_len, d_model, x_dtype));
+}
+
 hipError_t run_layer_small(const SmallLayerArgs& a) {
-  if (!layer_small_ok(a.seq_len, a.d_model, a.heads) || (a.x_dtype != kF16 && a.x_dtype != kF32) ||
-      a.batch < 0 || a.batch > 0x7fffffff)
+  if (a.batch < 0 || a.batch > 0x7fffffff || !layer_fused_ok(a.batch, a.seq_len, a.d_model, a.heads, a.x_dtype))
     return hipErrorInvalidValue;
   if (a.batch == 0) return hipSuccess;
   const double hd = (double)(a.d_model / a.heads);
   const float c2 = (float)(1.0 / sqrt(hd)) * 1.4426950408889634f;
-  if (layer_split_pays(a.batch, a.seq_len, a.d_model, a.x_dtype)) return run_layer_split(a, c2);
+  if (layer_split_ok(a.seq_len, a.d_model, a.heads) && layer_split_pays(a.batch, a.seq_len, a.d_model, a.x_dtype))
+    return run_layer_split(a, c2);
   return a.causal ? small_shape<true>(a, c2) : small_shape<false>(a, c2);
 }
 

@@ -20,7 +20,10 @@
 //      persistent kernel, but no cross-workgroup traffic at all), and Q^T of
 //      the slice for head w;
 //   3. wave h runs the attention of head h over all keys; the softmax is
-//      exact, every key of the sequence is present;
+//      exact, every key of the sequence is present.  With one head of 128
+//      dims the waves split it instead: wave w projects Q^T d-tile w, scores
+//      key tile w, the row max / sum and the probabilities go through LDS,
+//      and wave w forms output d-tile w over all keys;
 //   4. wave n multiplies the gathered attention output by the W_o rows of
 //      output columns 32n .. 32n+31, adds bias and residual, and LN2 combines
 //      the per-wave row sums through LDS.
@@ -54,6 +57,10 @@ struct SplitPlan {
   static constexpr int H = D / HD;
   static constexpr int NDT = HD / 32;  // 32-wide d tiles per head
   static constexpr int KSH = HD / 16;  // k-steps per head
+  // One head wider than a wave's share (head_dim 128): Q^T and the attention are
+  // split across the waves by d-tile / key tile rather than given to wave 0.
+  static constexpr bool QSPLIT = HD > 64;
+  static constexpr int NQT = QSPLIT ? 1 : NDT;  // Q^T d-tiles one wave projects
   static constexpr int ROWB = 2 * D;                   // one fp16 row of d_model
   static constexpr int TILEB = 32 * ROWB;              // 32 such rows
   static constexpr int KVB = 2 * kSplitTiles * KD * 1024;  // K^T then V fragments (1 KB each)
@@ -69,13 +76,15 @@ struct SplitPlan {
   static constexpr int BYTES = OFF_STAT + 2 * kSplitWaves * 32 * 4;
   // DMA instructions of one wave, in issue order: [gamma1|beta1] 1, token tile N_X,
   // other parameters 1, W_k/W_v N_A, W_q N_Q, residual N_R; W_o N_O after barrier 1.
-  static constexpr int N_X = TILEB / 1024, N_A = 2 * TILEB / 1024, N_Q = NDT * TILEB / 1024;
+  static constexpr int N_X = TILEB / 1024, N_A = 2 * TILEB / 1024, N_Q = NQT * TILEB / 1024;
   static constexpr int N_R = RB / 1024, N_O = TILEB / 1024;
   static_assert(D == 64 || D == 128, "swizzle and row geometry");
-  static_assert((HD == 32 || HD == 64) && D % HD == 0, "head geometry");
+  static_assert((HD == 32 || HD == 64 || HD == 128) && D % HD == 0, "head geometry");
+  static_assert(!QSPLIT || (H == 1 && NDT == kSplitWaves), "a split head has one d / key tile per wave");
   static_assert(H <= kSplitWaves && NNT <= kSplitWaves, "one wave per head and per d / output tile");
   static_assert(KD * 1024 == TILEB, "LN1 output fragments of a tile fill its input tile");
-  static_assert(2 * D * 4 <= 1024 && 2 * 32 + HD + 3 * 32 <= 256, "parameter rows");
+  static_assert(!QSPLIT || KSH * 1024 == CX, "the split head's Q^T fragments fit the attention-output area");
+  static_assert(2 * D * 4 <= 1024 && 2 * 32 + NQT * 32 + 3 * 32 <= 256, "parameter rows");
   static_assert(1 + N_X + 1 + N_A + N_Q + N_R < 64, "vmcnt range");
   static_assert(BYTES <= kLdsBytes, "LDS budget");
 };
@@ -140,7 +149,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, f16* __restrict__ y,
     float* __restrict__ resid_out, int S, int NS, float c2, float eps, const uint8_t* __restrict__ vmask) {
   using P = SplitPlan<D, HD>;
-  constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH;
+  constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH, NQT = P::NQT;
 
   __shared__ __attribute__((aligned(1024))) char smem[P::BYTES];
   char* const rA = smem;               // W_k/W_v staging, then K^T | V fragments
@@ -150,6 +159,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   f16x8* const Vl = Kl + kSplitTiles * KD * 64;
   f16x8* const Hb = reinterpret_cast<f16x8*>(rX);
   f16x8* const Cx = reinterpret_cast<f16x8*>(smem + P::OFF_CX);
+  f16x8* const Qx = Cx;  // split head: Q^T fragments of the slice, read before any Cx store
+  f16x8* const Px = Hb;  // split head: probability fragments, once every projection has read Hb
   float* const Stat = reinterpret_cast<float*>(smem + P::OFF_STAT);
 
   // The S/32 slices of a sequence run on one XCD, so its L2 serves the token
@@ -169,7 +180,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   char* const rP = smem + P::OFF_P + w * P::PB;  // [gamma1 | beta1], then the other parameters
   char* const rR = smem + P::OFF_R + w * P::RB;  // residual block of this wave
   char* const rWkv = rA + dq * 2 * P::TILEB;
-  char* const rWq = rQ + hq * NDT * P::TILEB;
+  // W_q rows this wave projects: d-tile dq of the split head, else all of head hq.
+  const int qrow0 = P::QSPLIT ? 32 * dq : HD * hq;
+  char* const rWq = rQ + (P::QSPLIT ? dq : hq * NDT) * P::TILEB;
   char* const rWo = rQ + dq * P::TILEB;
   char* const rTok = rX + w * P::TILEB;
 
@@ -192,12 +205,12 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     dma_span_rows<D, P::N_X>(rTok, reinterpret_cast<const char*>(xs + (int64_t)32 * w * D), spans);
   else
     dma_rows<D, P::N_X>(rTok, lane, [&](int r) { return xs + (int64_t)(32 * w + r < S ? 32 * w + r : 0) * D; });
-  {  // 32-float segments: b_k, b_v of d-tile dq; b_q of head hq (2 x 32); b_o, gamma2, beta2 of tile dq
+  {  // 32-float segments: b_k, b_v of d-tile dq; b_q of the projected Q rows (2 x 32); b_o, gamma2, beta2 of tile dq
     const int seg = lane >> 3, off = 4 * (lane & 7);
     const float* src = seg == 0   ? bqkv + D + 32 * dq + off
                        : seg == 1 ? bqkv + 2 * D + 32 * dq + off
-                       : seg == 2 ? bqkv + HD * hq + off
-                       : seg == 3 ? bqkv + HD * hq + (HD > 32 ? 32 : 0) + off
+                       : seg == 2 ? bqkv + qrow0 + off
+                       : seg == 3 ? bqkv + qrow0 + (NQT > 1 ? 32 : 0) + off
                        : seg == 4 ? bo + 32 * dq + off
                        : seg == 5 ? g2 + 32 * dq + off
                        : seg == 6 ? be2 + 32 * dq + off
@@ -212,8 +225,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   // arithmetic of LN1 overlaps the transfers the CU's load path is still working
   // through instead of waiting behind them.
   auto issue_late = [&]() {
-    // W_q rows of head hq.
-    dma_span_rows<D, P::N_Q>(rWq, wbytes + (int64_t)HD * hq * 2 * D, spans);
+    // W_q rows qrow0 .. qrow0 + 32 NQT - 1.
+    dma_span_rows<D, P::N_Q>(rWq, wbytes + (int64_t)qrow0 * 2 * D, spans);
     // Residual block: queries 32s .. 32s+31, columns 32dq .. 32dq+31, as [32 rows][4
     // chunks] with chunk c of row r at c ^ ((r >> 2) & 3).  Span i covers rows
     // 16i + lane / 4, whose swizzle (lane / 16) & 3 does not depend on i.
@@ -291,9 +304,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     wv[kk] = tile_chunk<D>(rWkv + P::TILEB, li, 2 * kk + g);
   }
   wait_vmcnt<P::N_R>();
-  f16x8 wq[NDT][KD];  // A operand of Q^T = W_q h^T
+  f16x8 wq[NQT][KD];  // A operand of Q^T = W_q h^T
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+  for (int dt = 0; dt < NQT; ++dt)
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) wq[dt][kk] = tile_chunk<D>(rWq, 32 * dt + li, 2 * kk + g);
   const float* pp = reinterpret_cast<const float*>(rP + 1024);  // the 32-float segments above
@@ -368,11 +381,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     fetch(0);
 #pragma unroll
     for (int t = 0; t < kSplitTiles; ++t) products(t);
-    // Q^T of the slice for head w (waves past the last head have none), with the
-    // last K / V tile stored between its products.
-    if (w < H) {
+    // Q^T of the slice for head w (waves past the last head have none), or d-tile w
+    // of the split head, with the last K / V tile stored between its products.
+    if (P::QSPLIT || w < H) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
+      for (int dt = 0; dt < NQT; ++dt) {
         f32x16 qa;
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
@@ -388,7 +401,12 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
             for (int c = kk * 4 / KD; c < (kk + 1) * 4 / KD; ++c) store_part(kSplitTiles - 1, c);
         }
 #pragma unroll
-        for (int half = 0; half < 2; ++half) qB[2 * dt + half] = acc_f16(qa, half);
+        for (int half = 0; half < 2; ++half) {
+          if constexpr (P::QSPLIT)
+            Qx[(2 * w + half) * 64 + lane] = acc_f16(qa, half);  // k-steps 2w, 2w + 1 of the head
+          else
+            qB[2 * dt + half] = acc_f16(qa, half);
+        }
       }
     } else {
 #pragma unroll
@@ -399,7 +417,68 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 
   // ---- attention of head w: S^T = K Q^T for all (at most 128) keys at once, one exact
   // softmax pass (no running max, no rescale), O^T = V^T P^T.
-  if (w < H) {
+  if constexpr (P::QSPLIT) {
+    // One head of 128 dims over four waves: wave w scores key tile w for the slice's
+    // queries, the per-query max and sum of the four tiles meet in LDS, the
+    // probabilities go to LDS as B-operand fragments, and wave w forms output d-tile w
+    // over all keys.  (Stat is free until the LayerNorm below.)
+    const int t = w;
+    f16x8 kf[KSH], qf[KSH];
+#pragma unroll
+    for (int ks = 0; ks < KSH; ++ks) {
+      kf[ks] = Kl[(t * KSH + ks) * 64 + lane];
+      qf[ks] = Qx[ks * 64 + lane];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 sacc = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KSH; ++ks) sacc = mfma32x32x16(kf[ks], qf[ks], sacc);
+    if (32 * t + 32 > S || (CAUSAL && t >= s)) {
+      int lim = S - 32 * t - 4 * g;  // valid: row offset < lim
+      if (CAUSAL) lim = min(lim, qtok - 32 * t - 4 * g + 1);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (8 * (r >> 2) + (r & 3) >= lim) sacc[r] = kNegInf;
+    }
+    if constexpr (MASKED) {
+      if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc, kbits.tile(t), g);
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+    mx = max_xor32(mx);
+    if (g == 0) Stat[w * 32 + li] = mx;
+    lds_barrier();  // every wave's tile max; every Q^T read is done
+    mx = fmaxf(fmaxf(Stat[li], Stat[32 + li]), fmaxf(Stat[64 + li], Stat[96 + li]));
+    // Unmasked, key 0 is valid for every query, so the max is finite; a query whose
+    // keys are all padded gets max -inf, all-zero probabilities and a zero row.
+    float m = mx * c2;
+    if constexpr (MASKED) m = mx == kNegInf ? 0.f : m;
+    f16x8 pB[2];
+    float lp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[r], c2, -m));
+      lp[r & 3] += pv;
+      pB[r >> 3][r & 7] = (f16)pv;
+    }
+    const float lt = sum_xor32((lp[0] + lp[1]) + (lp[2] + lp[3]));
+    if (g == 0) Stat[(kSplitWaves + w) * 32 + li] = lt;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) Px[(2 * t + half) * 64 + lane] = pB[half];
+    lds_barrier();  // probabilities and partial sums of every key tile
+    f32x16 ot = zero16();
+#pragma unroll
+    for (int tt = 0; tt < kSplitTiles; ++tt)
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+        ot = mfma32x32x16(Vl[((tt * NDT + w) * 2 + half) * 64 + lane], Px[(2 * tt + half) * 64 + lane], ot);
+    const float* const ls = Stat + kSplitWaves * 32;
+    const float l = (ls[li] + ls[32 + li]) + (ls[64 + li] + ls[96 + li]);
+    const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) Cx[(2 * w + half) * 64 + lane] = scaled_f16(ot, half, inv);
+  } else if (w < H) {
     const int h = w;
     // Every K and V fragment of the head is requested up front; the scheduling
     // barrier keeps the requests ahead of the products that wait on them.
@@ -539,6 +618,12 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   }
 }
 
+bool layer_split_ok(int64_t seq_len, int64_t d_model, int64_t heads) {
+  if (heads <= 0 || d_model % heads != 0 || seq_len < 1 || seq_len > kSmallMaxS) return false;
+  const int64_t hd = d_model / heads;
+  return (d_model == 128 && (hd == 32 || hd == 64 || hd == 128)) || (d_model == 64 && (hd == 32 || hd == 64));
+}
+
 bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dtype) {
   // fp16 activations at d_model 64 / 128, and at most two rounds of workgroups;
   // beyond that the persistent kernel, which projects K and V once per
@@ -569,11 +654,15 @@ static hipError_t launch_split(const SmallLayerArgs& a, float c2) {
 template <bool CAUSAL>
 static hipError_t split_shape(const SmallLayerArgs& a, float c2) {
   const int64_t hd = a.d_model / a.heads;
-  if (a.d_model == 128) return hd == 32 ? launch_split<128, 32, CAUSAL>(a, c2) : launch_split<128, 64, CAUSAL>(a, c2);
+  if (a.d_model == 128) {
+    if (hd == 32) return launch_split<128, 32, CAUSAL>(a, c2);
+    if (hd == 64) return launch_split<128, 64, CAUSAL>(a, c2);
+    return launch_split<128, 128, CAUSAL>(a, c2);
+  }
   return hd == 32 ? launch_split<64, 32, CAUSAL>(a, c2) : launch_split<64, 64, CAUSAL>(a, c2);
 }
 
-// Shape and dtype checks are the caller's (run_layer_small, layer_split_pays).
+// Shape and dtype checks are the caller's (run_layer_small: layer_split_ok, layer_split_pays).
 hipError_t run_layer_split(const SmallLayerArgs& a, float c2) {
   return a.causal ? split_shape<true>(a, c2) : split_shape<false>(a, c2);
 }

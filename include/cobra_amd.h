@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 3
+#define COBRA_ABI_VERSION 4
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
 
@@ -139,18 +139,21 @@ enum {
 };
 
 /*
- * Which plan cobra_layer_fwd runs for this shape, or -1 if the shape is not
- * supported.  FUSED covers seq_len <= 128 with d_model 128 (head_dim 32 or 64),
- * 64 (32, 64) or 96 (32), with or without a token mask; `masked` (a token mask
- * will be passed) only changes the STAGED plan's workspace.  Host-only: no
- * device work.  The reference's
- * counterpart is the gate set of UserOptimizedTransformer._prepare
- * (TTB:1030-1071).
+ * Which plan cobra_layer_fwd runs for this shape and activation dtype, or -1
+ * if the shape (or x_dtype) is not supported.  FUSED covers seq_len <= 128 with
+ * d_model 128 (head_dim 32 or 64), 64 (32, 64) or 96 (32), with or without a
+ * token mask; and, for fp16 activations while batch * ceil(seq_len / 32) <= 2 x
+ * the device's compute units, d_model 128 at head_dim 128.  `masked` (a token
+ * mask will be passed) only changes the STAGED plan's workspace.  Host-only: no
+ * device work.  The reference's counterpart is the gate set of
+ * UserOptimizedTransformer._prepare (TTB:1030-1071), which also looks at the
+ * dtype (TTB:952-996).
  */
-int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked);
+int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked, int x_dtype);
 
 /* Device workspace (bytes) cobra_layer_fwd needs for this shape (0 for FUSED). */
-int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked);
+int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked,
+                                    int x_dtype);
 
 /*
  * The whole attention sublayer (TTB:141-142 with TTB:88-123):

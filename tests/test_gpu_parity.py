@@ -66,7 +66,9 @@ def test_b10000_sampled_sequences():
         (2, 200, 32, 4, True),      # D 32, hd 8 (case 7 geometry)
         (5, 65, 128, 2, False),     # hd 64, ragged S
         (1, 40, 512, 2, True),      # hd 256
-        (3, 100, 128, 1, False),    # staged, hd 128, ragged S
+        (3, 100, 128, 1, False),    # fused query-split, hd 128 (one head over four waves), ragged S
+        (3, 100, 128, 1, True),     # the same, causal
+        (200, 100, 128, 1, False),  # staged, hd 128 (too many slices for the query-split kernel)
         (2, 128, 64, 2, True),      # fused, D 64, hd 32
         (7, 1, 128, 4, True),       # fused, S = 1 causal
         (2, 96, 64, 1, False),      # fused, D 64, hd 64
@@ -90,15 +92,20 @@ def test_residual_output_matches_oracle():
     assert compare_outputs(want_y, y.float().cpu()).passed
 
 
-def test_fp32_io_against_unrounded_oracle():
+@pytest.mark.parametrize("H", [4, 1])
+def test_fp32_io_against_unrounded_oracle(H):
     """fp32 activations and parameters (the reference's scored setting):
-    fp16 operands inside, fp32 residual/LayerNorm, gated against the plain fp32 layer."""
-    from cobra_amd import CobraAttentionSublayer
+    fp16 operands inside, fp32 residual/LayerNorm, gated against the plain fp32 layer.
+    H4 runs the persistent fused kernel; H1 (head_dim 128) the staged plan, since
+    the query-split kernel takes fp16 activations only."""
+    from cobra_amd import CobraAttentionSublayer, ops
     from oracle import make_sublayer
     from oracle.cases import oracle_forward
 
-    ref = make_sublayer(128, 4, seed=0)
-    mod = CobraAttentionSublayer(128, 4)
+    want_plan = ops.PLAN_FUSED if H == 4 else ops.PLAN_STAGED
+    assert ops.layer_plan(16, 128, 128, H, dtype=torch.float32) == want_plan
+    ref = make_sublayer(128, H, seed=0)
+    mod = CobraAttentionSublayer(128, H)
     mod.load_state_dict(ref.state_dict())
     mod = mod.to(DEV).eval()
     x = make_input(16, 128, 128, seed=5)

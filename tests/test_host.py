@@ -48,10 +48,12 @@ def test_argument_validation_rejects_before_any_launch():
     assert lib.cobra_attn_fwd(16, 16, None, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
     assert lib.cobra_attn_fwd(256, 256, 12, 1, 4, 1, 16, 0.1, 0, None) != 0  # misaligned key bits
     assert lib.cobra_mask_bits(256, 12, 1, 4, None) != 0                   # misaligned key bits
-    assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10, 0) == -1      # head_dim 12
-    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0) > 0     # staged plan (head_dim 8)
-    assert lib.cobra_layer_plan(2, 16, 128, 4, 0) == _lib.PLAN_FUSED
-    assert lib.cobra_layer_plan(2, 16, 128, 4, 1) == _lib.PLAN_FUSED  # the fused kernels take token masks
+    assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10, 0, _lib.F16) == -1      # head_dim 12
+    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0, _lib.F16) > 0     # staged plan (head_dim 8)
+    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 4, 0, 7) == -1           # dtype code
+    assert lib.cobra_layer_plan(2, 16, 128, 4, 0, _lib.F16) == _lib.PLAN_FUSED
+    assert lib.cobra_layer_plan(2, 16, 128, 4, 1, _lib.F16) == _lib.PLAN_FUSED  # the fused kernels take token masks
+    assert lib.cobra_layer_plan(2, 16, 128, 4, 0, 7) == -1
 
 
 def test_layer_bind_validates_and_releases():
@@ -71,7 +73,7 @@ def test_layer_bind_validates_and_releases():
     assert lib.cobra_layer_run(None, 256, None, 768, None, None) != 0
     lib.cobra_layer_unbind(h)
     lib.cobra_layer_unbind(None)
-    ws = lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 1)
+    ws = lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 1, _lib.F16)
     h = lib.cobra_layer_bind(0, 1, *w, 4096, ws, 2, 16, 128, 16, 0, 1e-5)
     assert h
     lib.cobra_layer_unbind(h)
@@ -95,16 +97,29 @@ def test_workspace_size_formula():
 
 
 def test_plan_selection_per_config():
-    """One fused kernel for S <= 128 at d_model 128 with head_dim 32 or 64; staged otherwise."""
+    """One fused kernel for S <= 128 at d_model 128 with head_dim 32 or 64, and with
+    head_dim 128 for fp16 batches the query-split kernel covers in two rounds of
+    workgroups; staged otherwise."""
+    import torch
+
     from cobra_amd import ops
     from oracle import CONFIGS
 
-    fused = {"plumbing", "base", "b1", "b4", "b16", "b128", "b10000", "s32", "h2"}
+    fused = {"plumbing", "base", "b1", "b4", "b16", "b128", "b10000", "s32", "h1", "h2"}
     for name, c in CONFIGS.items():
         want = ops.PLAN_FUSED if name in fused else ops.PLAN_STAGED
         assert ops.layer_plan(c.batch, c.seq_len, c.d_model, c.heads) == want, name
     assert ops.layer_plan(2, 129, 128, 4) == ops.PLAN_STAGED
     assert ops.layer_plan(2, 17, 96, 3) == ops.PLAN_FUSED
+    # head_dim 128: the query-split kernel only (fp16 activations, <= 2 rounds at 256 CUs)
+    assert ops.layer_plan(128, 128, 128, 1) == ops.PLAN_FUSED
+    assert ops.layer_plan(129, 128, 128, 1) == ops.PLAN_STAGED
+    assert ops.layer_plan(64, 128, 128, 1, dtype=torch.float32) == ops.PLAN_STAGED
+    assert ops.layer_plan(64, 128, 128, 4, dtype=torch.float32) == ops.PLAN_FUSED
+    assert ops.layer_workspace_bytes(64, 128, 128, 1) == 0
+    assert ops.layer_workspace_bytes(64, 128, 128, 1, dtype=torch.float32) == 8192 * 128 * 2 + 8192 * 384 * 2
+    with pytest.raises(TypeError):
+        ops.layer_plan(2, 16, 128, 4, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
         ops.layer_plan(2, 16, 120, 10)
 
