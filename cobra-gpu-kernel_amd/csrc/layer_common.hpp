@@ -141,7 +141,7 @@ __device__ __forceinline__ V partner_value(const V& v) {
 }
 
 // Query-split variant of the fused kernel (layer_split.hip): fp16
-// activations at d_model 64 / 128 (head_dim 32 / 64, and 128 at d_model 128),
+// activations at d_model 64 / 128 (head_dim 32 / 64, and 8 or 128 at d_model 128),
 // while batch * ceil(S/32) workgroups take at most two rounds of the chip.
 bool layer_split_ok(int64_t seq_len, int64_t d_model, int64_t heads);
 bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dtype);

@@ -23,7 +23,9 @@
 //      exact, every key of the sequence is present.  With one head of 128
 //      dims the waves split it instead: wave w projects Q^T d-tile w, scores
 //      key tile w, the row max / sum and the probabilities go through LDS,
-//      and wave w forms output d-tile w over all keys;
+//      and wave w forms output d-tile w over all keys.  With 8-dim heads
+//      wave w takes the four heads of d-tile w (each 16-dim k-step holds two
+//      heads: the other head's half of the K fragment is zeroed);
 //   4. wave n multiplies the gathered attention output by the W_o rows of
 //      output columns 32n .. 32n+31, adds bias and residual, and LN2 combines
 //      the per-wave row sums through LDS.
@@ -60,7 +62,11 @@ struct SplitPlan {
   // One head wider than a wave's share (head_dim 128): Q^T and the attention are
   // split across the waves by d-tile / key tile rather than given to wave 0.
   static constexpr bool QSPLIT = HD > 64;
-  static constexpr int NQT = QSPLIT ? 1 : NDT;  // Q^T d-tiles one wave projects
+  // Heads narrower than a k-step (head_dim 8): wave w owns the four heads of d-tile w.
+  static constexpr bool NARROW = HD < 16;
+  // Q^T is projected by d-tile (wave w: rows 32w .. 32w+31 of W_q) rather than by head.
+  static constexpr bool QBYTILE = QSPLIT || NARROW;
+  static constexpr int NQT = QBYTILE ? 1 : NDT;  // Q^T d-tiles one wave projects
   static constexpr int ROWB = 2 * D;                   // one fp16 row of d_model
   static constexpr int TILEB = 32 * ROWB;              // 32 such rows
   static constexpr int KVB = 2 * kSplitTiles * KD * 1024;  // K^T then V fragments (1 KB each)
@@ -79,9 +85,10 @@ struct SplitPlan {
   static constexpr int N_X = TILEB / 1024, N_A = 2 * TILEB / 1024, N_Q = NQT * TILEB / 1024;
   static constexpr int N_R = RB / 1024, N_O = TILEB / 1024;
   static_assert(D == 64 || D == 128, "swizzle and row geometry");
-  static_assert((HD == 32 || HD == 64 || HD == 128) && D % HD == 0, "head geometry");
+  static_assert((HD == 8 || HD == 32 || HD == 64 || HD == 128) && D % HD == 0, "head geometry");
   static_assert(!QSPLIT || (H == 1 && NDT == kSplitWaves), "a split head has one d / key tile per wave");
-  static_assert(H <= kSplitWaves && NNT <= kSplitWaves, "one wave per head and per d / output tile");
+  static_assert(!NARROW || (D == 128 && NNT == kSplitWaves), "narrow heads: four per wave, one d-tile per wave");
+  static_assert((NARROW || H <= kSplitWaves) && NNT <= kSplitWaves, "one wave per head and per d / output tile");
   static_assert(KD * 1024 == TILEB, "LN1 output fragments of a tile fill its input tile");
   static_assert(!QSPLIT || KSH * 1024 == CX, "the split head's Q^T fragments fit the attention-output area");
   static_assert(2 * D * 4 <= 1024 && 2 * 32 + NQT * 32 + 3 * 32 <= 256, "parameter rows");
@@ -181,8 +188,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   char* const rR = smem + P::OFF_R + w * P::RB;  // residual block of this wave
   char* const rWkv = rA + dq * 2 * P::TILEB;
   // W_q rows this wave projects: d-tile dq of the split head, else all of head hq.
-  const int qrow0 = P::QSPLIT ? 32 * dq : HD * hq;
-  char* const rWq = rQ + (P::QSPLIT ? dq : hq * NDT) * P::TILEB;
+  const int qrow0 = P::QBYTILE ? 32 * dq : HD * hq;
+  char* const rWq = rQ + (P::QBYTILE ? dq : hq * NDT) * P::TILEB;
   char* const rWo = rQ + dq * P::TILEB;
   char* const rTok = rX + w * P::TILEB;
 
@@ -325,7 +332,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   if (w >= NNT) dma_span_rows<D, P::N_O>(rWo, wob, spans);
 
   // ---- K^T and V of d-tile w for every token tile; Q^T of the slice for head w ---------
-  f16x8 qB[KSH];
+  f16x8 qB[P::NARROW ? 2 : KSH];  // B operand of S^T = K Q^T (narrow heads: the two k-steps of d-tile w)
   if (w < NNT) {
     // The biases start the accumulators (the first product of each chain reads them
     // as its C operand), so no bias add follows the products.
@@ -339,7 +346,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     const float bvl = pp[32 + li];
 #pragma unroll
     for (int r = 0; r < 16; ++r) bv[r] = bvl;
-    const int h = (32 * w) / HD, t2 = w % NDT;  // head and d tile within the head
+    // Head and d tile within the head (head-major K / V areas); narrow heads keep
+    // K^T by 16-dim k-step of d_model and V by d-tile instead.
+    const int h = P::NARROW ? 0 : (32 * w) / HD, t2 = P::NARROW ? 0 : w % (P::NARROW ? 1 : NDT);
     // Two accumulator pairs: the products of token tile t run on the matrix
     // cores while tile t-1 is converted and stored.
     f32x16 ka[2], va[2];
@@ -356,10 +365,17 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     // would leave the matrix cores idle while they execute.
     auto store_part = [&](int t, int c) {  // c: K half 0, K half 1, V half 0, V half 1
       const int half = c & 1;
-      if (c < 2)
-        Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = acc_f16(ka[t & 1], half);
-      else
-        Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
+      if constexpr (P::NARROW) {
+        if (c < 2)
+          Kl[(t * KD + 2 * w + half) * 64 + lane] = acc_f16(ka[t & 1], half);
+        else
+          Vl[((t * NNT + w) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
+      } else {
+        if (c < 2)
+          Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = acc_f16(ka[t & 1], half);
+        else
+          Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
+      }
     };
     auto products = [&](int t) {
       if (t + 1 < kSplitTiles) fetch(t + 1);
@@ -383,7 +399,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int t = 0; t < kSplitTiles; ++t) products(t);
     // Q^T of the slice for head w (waves past the last head have none), or d-tile w
     // of the split head, with the last K / V tile stored between its products.
-    if (P::QSPLIT || w < H) {
+    if (P::QBYTILE || w < H) {
 #pragma unroll
       for (int dt = 0; dt < NQT; ++dt) {
         f32x16 qa;
@@ -478,6 +494,63 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
 #pragma unroll
     for (int half = 0; half < 2; ++half) Cx[(2 * w + half) * 64 + lane] = scaled_f16(ot, half, inv);
+  } else if constexpr (P::NARROW) {
+    // Four 8-dim heads per wave: head 4w + j lives in k-step 2w + j/2, elements 0-3
+    // (j even) or 4-7 (j odd) of each lane's fragment (dims 4g .. 4g+3 and 8 + 4g ..
+    // 8 + 4g + 3 of the k-step).  Zeroing the other head's elements of the K
+    // fragment leaves this head's scores; the output rows of head j of the d-tile
+    // are accumulator registers 4j .. 4j+3, taken from that head's O^T.
+    f32x16 ofin;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      __builtin_amdgcn_sched_barrier(0);  // one head at a time (register pressure)
+      const int ks = 2 * w + (j >> 1);
+      f32x16 sacc[kSplitTiles];
+      float mx = kNegInf;
+#pragma unroll
+      for (int t = 0; t < kSplitTiles; ++t) {
+        f16x8 kf = Kl[(t * KD + ks) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kf[(j & 1) ? e : 4 + e] = (f16)0.0f;
+        sacc[t] = mfma32x32x16(kf, qB[j >> 1], zero16());
+        if (32 * t + 32 > S || (CAUSAL && t >= s)) {
+          int lim = S - 32 * t - 4 * g;  // valid: row offset < lim
+          if (CAUSAL) lim = min(lim, qtok - 32 * t - 4 * g + 1);
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) >= lim) sacc[t][r] = kNegInf;
+        }
+        if constexpr (MASKED) {
+          if (kbits.tile(t) != 0xffffffffu) mask_key_tile(sacc[t], kbits.tile(t), g);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
+      }
+      mx = max_xor32(mx);
+      float m = mx * c2;
+      if constexpr (MASKED) m = mx == kNegInf ? 0.f : m;
+      f32x16 ot = zero16();
+      float lp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < kSplitTiles; ++t) {
+        f16x8 pB[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
+          lp[r & 3] += pv;
+          pB[r >> 3][r & 7] = (f16)pv;
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+          ot = mfma32x32x16(Vl[((t * NNT + w) * 2 + half) * 64 + lane], pB[half], ot);
+      }
+      const float l = sum_xor32((lp[0] + lp[1]) + (lp[2] + lp[3]));
+      const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ofin[4 * j + e] = ot[4 * j + e] * inv;
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) Cx[(2 * w + half) * 64 + lane] = acc_f16(ofin, half);
   } else if (w < H) {
     const int h = w;
     // Every K and V fragment of the head is requested up front; the scheduling
@@ -621,7 +694,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 bool layer_split_ok(int64_t seq_len, int64_t d_model, int64_t heads) {
   if (heads <= 0 || d_model % heads != 0 || seq_len < 1 || seq_len > kSmallMaxS) return false;
   const int64_t hd = d_model / heads;
-  return (d_model == 128 && (hd == 32 || hd == 64 || hd == 128)) || (d_model == 64 && (hd == 32 || hd == 64));
+  return (d_model == 128 && (hd == 8 || hd == 32 || hd == 64 || hd == 128)) ||
+         (d_model == 64 && (hd == 32 || hd == 64));
 }
 
 bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dtype) {
@@ -655,6 +729,7 @@ template <bool CAUSAL>
 static hipError_t split_shape(const SmallLayerArgs& a, float c2) {
   const int64_t hd = a.d_model / a.heads;
   if (a.d_model == 128) {
+    if (hd == 8) return launch_split<128, 8, CAUSAL>(a, c2);
     if (hd == 32) return launch_split<128, 32, CAUSAL>(a, c2);
     if (hd == 64) return launch_split<128, 64, CAUSAL>(a, c2);
     return launch_split<128, 128, CAUSAL>(a, c2);

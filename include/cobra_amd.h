@@ -143,7 +143,7 @@ enum {
  * if the shape (or x_dtype) is not supported.  FUSED covers seq_len <= 128 with
  * d_model 128 (head_dim 32 or 64), 64 (32, 64) or 96 (32), with or without a
  * token mask; and, for fp16 activations while batch * ceil(seq_len / 32) <= 2 x
- * the device's compute units, d_model 128 at head_dim 128.  `masked` (a token
+ * the device's compute units, d_model 128 at head_dim 8 or 128.  `masked` (a token
  * mask will be passed) only changes the STAGED plan's workspace.  Host-only: no
  * device work.  The reference's counterpart is the gate set of
  * UserOptimizedTransformer._prepare (TTB:1030-1071), which also looks at the

@@ -45,6 +45,7 @@ def token_mask(B, S, seed, left_aligned):
         (5, 80, 128, 2),     # query-split, head_dim 64, ragged S
         (4, 128, 64, 2),     # query-split, d_model 64
         (5, 100, 128, 1),    # query-split, one head of 128 dims over four waves, ragged S
+        (5, 100, 128, 16),   # query-split, four 8-dim heads per wave, ragged S
         (300, 128, 128, 4),  # persistent fused kernel (more than two rounds of slices)
         (3, 17, 96, 3),      # persistent fused kernel, d_model 96
         (301, 96, 64, 2),    # persistent, d_model 64: two sequences per workgroup, odd batch
@@ -92,7 +93,8 @@ def test_masked_graph_replays_with_new_masks():
     assert mod._graph is not None
 
 
-@pytest.mark.parametrize("B,S,D,H", [(8, 128, 128, 4), (300, 128, 128, 4), (4, 200, 128, 4), (8, 128, 128, 1)])
+@pytest.mark.parametrize("B,S,D,H", [(8, 128, 128, 4), (300, 128, 128, 4), (4, 200, 128, 4), (8, 128, 128, 1),
+                                     (8, 128, 128, 16)])
 def test_all_valid_mask_equals_no_mask(B, S, D, H):
     """An all-true mask gives the unmasked result bit for bit (fused kernels, both
     variants, and the staged plan)."""

@@ -69,6 +69,8 @@ def test_b10000_sampled_sequences():
         (3, 100, 128, 1, False),    # fused query-split, hd 128 (one head over four waves), ragged S
         (3, 100, 128, 1, True),     # the same, causal
         (200, 100, 128, 1, False),  # staged, hd 128 (too many slices for the query-split kernel)
+        (3, 100, 128, 16, True),    # fused query-split, hd 8 (four heads per wave), ragged S, causal
+        (200, 100, 128, 16, False), # staged, hd 8
         (2, 128, 64, 2, True),      # fused, D 64, hd 32
         (7, 1, 128, 4, True),       # fused, S = 1 causal
         (2, 96, 64, 1, False),      # fused, D 64, hd 64
@@ -92,12 +94,12 @@ def test_residual_output_matches_oracle():
     assert compare_outputs(want_y, y.float().cpu()).passed
 
 
-@pytest.mark.parametrize("H", [4, 1])
+@pytest.mark.parametrize("H", [4, 1, 16])
 def test_fp32_io_against_unrounded_oracle(H):
     """fp32 activations and parameters (the reference's scored setting):
     fp16 operands inside, fp32 residual/LayerNorm, gated against the plain fp32 layer.
-    H4 runs the persistent fused kernel; H1 (head_dim 128) the staged plan, since
-    the query-split kernel takes fp16 activations only."""
+    H4 runs the persistent fused kernel; H1 and H16 (head_dim 128, 8) the staged
+    plan, since the query-split kernel takes fp16 activations only."""
     from cobra_amd import CobraAttentionSublayer, ops
     from oracle import make_sublayer
     from oracle.cases import oracle_forward
@@ -131,10 +133,10 @@ def test_bit_repeatable():
     assert torch.equal(a, b) and torch.equal(a, c)
 
 
-@pytest.mark.parametrize("D,H", [(128, 4), (128, 16)])
+@pytest.mark.parametrize("D,H", [(128, 4), (256, 4)])
 def test_graph_replays_match_eager(D, H):
     """hipGraph replays with fresh inputs, eager work in between, each equal to
-    the eager result (fused plan at H4, staged plan at H16)."""
+    the eager result (fused plan at d_model 128, staged plan at 256)."""
     _, mod = build_pair(D, H, graph=True)
     xs = [make_input(16, 128, D, seed=s).half().to(DEV) for s in range(4)]
     with torch.inference_mode():
@@ -181,7 +183,7 @@ def test_base_config_runs_fused_single_kernel():
     assert mod.plan == ops.PLAN_FUSED and mod._ws.numel() == 0 and not mod._graph_ok
 
 
-@pytest.mark.parametrize("H,causal", [(4, False), (4, True), (2, False), (1, True)])
+@pytest.mark.parametrize("H,causal", [(4, False), (4, True), (2, False), (1, True), (16, False)])
 def test_staged_pipeline_at_fused_shapes(H, causal):
     """The staged kernels (LN, QKV GEMM, attention, GEMM+LN), composed through
     the op wrappers exactly as cobra_layer_fwd's staged plan does, at a shape

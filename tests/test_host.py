@@ -49,7 +49,7 @@ def test_argument_validation_rejects_before_any_launch():
     assert lib.cobra_attn_fwd(256, 256, 12, 1, 4, 1, 16, 0.1, 0, None) != 0  # misaligned key bits
     assert lib.cobra_mask_bits(256, 12, 1, 4, None) != 0                   # misaligned key bits
     assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10, 0, _lib.F16) == -1      # head_dim 12
-    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0, _lib.F16) > 0     # staged plan (head_dim 8)
+    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0, _lib.F32) > 0     # staged plan (head_dim 8, fp32)
     assert lib.cobra_layer_workspace_bytes(2, 16, 128, 4, 0, 7) == -1           # dtype code
     assert lib.cobra_layer_plan(2, 16, 128, 4, 0, _lib.F16) == _lib.PLAN_FUSED
     assert lib.cobra_layer_plan(2, 16, 128, 4, 1, _lib.F16) == _lib.PLAN_FUSED  # the fused kernels take token masks
@@ -65,7 +65,7 @@ def test_layer_bind_validates_and_releases():
     w = [256 * (i + 1) for i in range(8)]  # aligned stand-in addresses: bind dereferences nothing
     assert not lib.cobra_layer_bind(0, 0, 12, *w[1:], None, 0, 2, 16, 128, 4, 0, 1e-5)   # misaligned w_qkv
     assert not lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 120, 10, 0, 1e-5)          # head_dim 12
-    assert not lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 128, 16, 0, 1e-5)          # staged: needs workspace
+    assert not lib.cobra_layer_bind(1, 0, *w, None, 0, 2, 16, 128, 16, 0, 1e-5)          # staged: needs workspace
     assert not lib.cobra_layer_bind(5, 0, *w, None, 0, 2, 16, 128, 4, 0, 1e-5)           # dtype code
     h = lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 128, 4, 0, 1e-5)                  # fused: no workspace
     assert h
@@ -73,11 +73,11 @@ def test_layer_bind_validates_and_releases():
     assert lib.cobra_layer_run(None, 256, None, 768, None, None) != 0
     lib.cobra_layer_unbind(h)
     lib.cobra_layer_unbind(None)
-    ws = lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 1, _lib.F16)
-    h = lib.cobra_layer_bind(0, 1, *w, 4096, ws, 2, 16, 128, 16, 0, 1e-5)
+    ws = lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 1, _lib.F32)
+    h = lib.cobra_layer_bind(1, 1, *w, 4096, ws, 2, 16, 128, 16, 0, 1e-5)
     assert h
     lib.cobra_layer_unbind(h)
-    assert not lib.cobra_layer_bind(0, 1, *w, 4096, ws - 1, 2, 16, 128, 16, 0, 1e-5)
+    assert not lib.cobra_layer_bind(1, 1, *w, 4096, ws - 1, 2, 16, 128, 16, 0, 1e-5)
 
 
 def test_workspace_size_formula():
@@ -86,14 +86,15 @@ def test_workspace_size_formula():
     # fused plan: no workspace
     assert ops.layer_workspace_bytes(64, 128, 128, 4) == 0
     # staged: h fp16 [T, D] + qkv fp16 [T, 3D] (+ fp32 residual for D > 128), 256-B aligned
-    assert ops.layer_workspace_bytes(64, 128, 128, 16) == 8192 * 128 * 2 + 8192 * 384 * 2
+    f32 = torch.float32
+    assert ops.layer_workspace_bytes(64, 128, 128, 16, dtype=f32) == 8192 * 128 * 2 + 8192 * 384 * 2
     t, d = 32 * 100000, 1024
     assert ops.layer_workspace_bytes(32, 100000, 1024, 16) == t * d * 2 + t * 3 * d * 2 + t * d * 4
     # a token mask adds the packed key bits, [B][ceil(S/64)] u64, 256-B aligned
     bits = -(-(32 * 1563 * 8) // 256) * 256
     assert ops.layer_workspace_bytes(32, 100000, 1024, 16, masked=True) == t * d * 2 + t * 3 * d * 2 + t * d * 4 + bits
     assert ops.layer_workspace_bytes(64, 128, 128, 4, masked=True) == 0  # fused: the kernel reads the mask bytes
-    assert ops.layer_workspace_bytes(64, 128, 128, 16, masked=True) == 8192 * 128 * 2 + 8192 * 384 * 2 + 1024
+    assert ops.layer_workspace_bytes(64, 128, 128, 16, masked=True, dtype=f32) == 8192 * 128 * 2 + 8192 * 384 * 2 + 1024
 
 
 def test_plan_selection_per_config():
@@ -105,7 +106,7 @@ def test_plan_selection_per_config():
     from cobra_amd import ops
     from oracle import CONFIGS
 
-    fused = {"plumbing", "base", "b1", "b4", "b16", "b128", "b10000", "s32", "h1", "h2"}
+    fused = {"plumbing", "base", "b1", "b4", "b16", "b128", "b10000", "s32", "h1", "h2", "h16"}
     for name, c in CONFIGS.items():
         want = ops.PLAN_FUSED if name in fused else ops.PLAN_STAGED
         assert ops.layer_plan(c.batch, c.seq_len, c.d_model, c.heads) == want, name
@@ -115,6 +116,8 @@ def test_plan_selection_per_config():
     assert ops.layer_plan(128, 128, 128, 1) == ops.PLAN_FUSED
     assert ops.layer_plan(129, 128, 128, 1) == ops.PLAN_STAGED
     assert ops.layer_plan(64, 128, 128, 1, dtype=torch.float32) == ops.PLAN_STAGED
+    assert ops.layer_plan(64, 128, 128, 16, dtype=torch.float32) == ops.PLAN_STAGED
+    assert ops.layer_plan(129, 128, 128, 16) == ops.PLAN_STAGED
     assert ops.layer_plan(64, 128, 128, 4, dtype=torch.float32) == ops.PLAN_FUSED
     assert ops.layer_workspace_bytes(64, 128, 128, 1) == 0
     assert ops.layer_workspace_bytes(64, 128, 128, 1, dtype=torch.float32) == 8192 * 128 * 2 + 8192 * 384 * 2
