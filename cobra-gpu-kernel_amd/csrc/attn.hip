@@ -156,14 +156,38 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
 #pragma unroll
   for (int i = 0; i < QPT; ++i) dma_tile(qtile, w + NW * i, qbase, qb * BM);
 
-  // K/V stages: ST tiles deep, one barrier per key block.
+  // K/V stages: ST tiles deep, one barrier per key block.  A block that lies wholly
+  // inside the sequence needs no row clamp, so its sources are this lane's fixed
+  // pointers (row and chunk within the tile, K or V) plus the block's wave-uniform
+  // offset: no per-block 64-bit address arithmetic on the vector ALU.  The block
+  // reaching past S takes the clamped path.
+  const f16* kv_src[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int span = w + NW * i;
+    const bool v = span >= NI / 2;
+    const int o = (v ? span - NI / 2 : span) * 1024 + 16 * lane;
+    const int row = o / (2 * HD), pos = (o % (2 * HD)) / 16;
+    const int d0 = 8 * (pos ^ swz<HD>(row));
+    kv_src[i] = (v ? vbase : kbase) + (int64_t)row * ld + (d0 < hd ? d0 : 0);
+  }
   auto issue = [&](int stage, int kb) {
     char* sbase = smem + stage * SB;
+    if (kb + BN <= S) {
+      const int64_t step = (int64_t)kb * ld;
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int span = w + NW * i;
-      const bool v = span >= NI / 2;
-      dma_tile(sbase + (v ? TB : 0), v ? span - NI / 2 : span, v ? vbase : kbase, kb);
+      for (int i = 0; i < LPT; ++i) {
+        const int span = w + NW * i;
+        const bool v = span >= NI / 2;
+        dma16(kv_src[i] + step, sbase + (v ? TB : 0) + (v ? span - NI / 2 : span) * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        const int span = w + NW * i;
+        const bool v = span >= NI / 2;
+        dma_tile(sbase + (v ? TB : 0), v ? span - NI / 2 : span, v ? vbase : kbase, kb);
+      }
     }
   };
 
