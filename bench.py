@@ -23,6 +23,7 @@ Also on the same line:
   * ``graph``: the same forward replayed as a hipGraph, and an empty-graph floor.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-long] [--no-cpu] [--no-sweep]
+       python bench.py --only gemm,s1024   (just those sweep entries, one JSON line; for profiling)
 """
 
 from __future__ import annotations
@@ -195,9 +196,11 @@ SWEEP = [  # name, B, S, D, H  (BASELINE configs other than the headline one)
 ]
 
 
-def sweep(dev):
+def sweep(dev, only=None):
     out = {}
     for name, B, S, D, H in SWEEP:
+        if only and name not in only:
+            continue
         layer = make_layer(D, H, dev)
         x = torch.randn(B, S, D, device=dev, dtype=torch.float16)
         with torch.inference_mode():
@@ -344,6 +347,8 @@ def main() -> int:
     ap.add_argument("--no-long", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--only", default="", help="comma-separated sweep entries to time alone (" +
+                    ", ".join(n for n, *_ in SWEEP) + ")")
     ap.add_argument("--matrix", action="store_true",
                     help="time CobraTransformer on the reference's whole-model case matrix and exit")
     args = ap.parse_args()
@@ -361,6 +366,14 @@ def main() -> int:
         return 0
     if args.pmc_driver:
         pmc_driver(dev)
+        return 0
+    if args.only:
+        names = [n for n in args.only.split(",") if n]
+        unknown = [n for n in names if n not in {s[0] for s in SWEEP}]
+        if unknown:
+            print(f"unknown sweep entries {unknown}", file=sys.stderr)
+            return 2
+        print(json.dumps({"sweep": sweep(dev, set(names))}), flush=True)
         return 0
     B, S, D, H = 64, 128, 128, 4
     x = synthetic_input(B, S, D, seed=0).half().to(dev)

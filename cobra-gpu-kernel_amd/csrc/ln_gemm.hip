@@ -360,38 +360,51 @@ hipError_t run_gemm_ln_rows(const GemmArgs& a) {
 // from the bias); the fp16 results leave as 16-byte row pieces after one exchange
 // with the partner lane.  The tile-per-workgroup kernel above serialises load,
 // LayerNorm, products and stores inside each workgroup, two per CU.
-template <int NT, int BM, typename TX>
-__global__ __launch_bounds__(kLgThreads) void ln_gemm_p_kernel(const TX* __restrict__ x, const float* __restrict__ gamma,
-                                                             const float* __restrict__ beta, const f16* __restrict__ W,
-                                                             const float* __restrict__ bias, f16* __restrict__ C,
-                                                             int64_t M, float eps) {
+//
+// NWV waves: with 8, waves w and w + 4 own the same columns and split the block's
+// row tiles, so twice the loads and stores are in flight per CU (all of W in LDS
+// leaves room for one workgroup per CU, and the kernel is bound by how many
+// memory operations that workgroup keeps outstanding).
+template <int NT, int BM, int NWV, typename TX>
+__global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restrict__ x, const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta, const f16* __restrict__ W,
+                                                           const float* __restrict__ bias, f16* __restrict__ C,
+                                                           int64_t M, float eps) {
   constexpr int D = 128, ROWB = 2 * D, CPR = D / 8;  // 16 chunks of 16 bytes per row
   constexpr int N = 128 * NT;
-  constexpr int RT = BM / 32;                         // 32-row tiles per block
-  constexpr int PASSES = BM * CPR / kLgThreads;       // LayerNorm rows per thread
-  static_assert(BM % 32 == 0 && PASSES >= 1, "block rows");
+  constexpr int THREADS = 64 * NWV;
+  constexpr int CG = NWV / 4;                         // wave groups splitting the row tiles
+  constexpr int RT = BM / 32 / CG;                    // 32-row tiles per wave
+  constexpr int PASSES = BM * CPR / THREADS;          // LayerNorm rows per thread
+  constexpr int RPP = THREADS / CPR;                  // rows per LayerNorm pass
+  constexpr int WCH = N * CPR / THREADS;              // W chunks per thread
+  static_assert(NWV == 4 || NWV == 8 || NWV == 16, "four column groups of waves, one, two or four row groups");
+  static_assert(BM % (32 * CG) == 0 && RT >= 1 && PASSES >= 1 && PASSES * THREADS == BM * CPR, "block rows");
+  constexpr int SG = WCH % 4 == 0 ? 4 : 2;           // W chunks per staging group
+  static_assert(WCH * THREADS == N * CPR && WCH % SG == 0, "W staging");
   __shared__ __attribute__((aligned(16))) char smem[N * ROWB + 2 * BM * ROWB];
   char* const Ws = smem;
   char* const Hs = smem + N * ROWB;  // two buffers of BM normalised rows
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, w4 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = w4 % 4, rg = w4 / 4;         // column group, row group of this wave
   const int li = lane & 31, g = lane >> 5;
-  const int rp = tid / CPR, cl = tid % CPR;  // LayerNorm: row rp of each 16-row pass, chunk cl
+  const int rp = tid / CPR, cl = tid % CPR;  // LayerNorm: row rp of each RPP-row pass, chunk cl
   const int64_t nblk = (M + BM - 1) / BM;
 
   // W rows, swizzled: chunk c of row r at c ^ (r & 15).
 #pragma unroll
-  for (int b0 = 0; b0 < N * CPR / kLgThreads; b0 += 8) {
-    f16x8 v[8];
+  for (int b0 = 0; b0 < WCH; b0 += SG) {
+    f16x8 v[SG];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + kLgThreads * (b0 + i);
+    for (int i = 0; i < SG; ++i) {
+      const int c = tid + THREADS * (b0 + i);
       v[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)(c / CPR) * D + 8 * (c % CPR));
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + kLgThreads * (b0 + i), r = c / CPR;
+    for (int i = 0; i < SG; ++i) {
+      const int c = tid + THREADS * (b0 + i), r = c / CPR;
       *reinterpret_cast<f16x8*>(Ws + r * ROWB + 16 * ((c % CPR) ^ (r & 15))) = v[i];
     }
   }
@@ -416,7 +429,7 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_p_kernel(const TX* __restr
   auto load_rows = [&](int64_t blk) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      const int64_t row = blk * BM + 16 * p + rp;
+      const int64_t row = blk * BM + RPP * p + rp;
       if (blk < nblk && row < M) {
         load8(x + row * D + 8 * cl, xv[p]);
       } else {
@@ -446,7 +459,7 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_p_kernel(const TX* __restr
       f16x8 h;
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[p][e] - mean) * rstd * gv[e] + bv[e]);
-      const int r = 16 * p + rp;
+      const int r = RPP * p + rp;
       *reinterpret_cast<f16x8*>(H + r * ROWB + 16 * (cl ^ (r & 15))) = h;
     }
     // One barrier per block: H of this block is complete, and (double buffering)
@@ -466,7 +479,7 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_p_kernel(const TX* __restr
       const int co = 16 * ((2 * kk + g) ^ sw);
       f16x8 hf[RT], wf[NT];
 #pragma unroll
-      for (int i = 0; i < RT; ++i) hf[i] = *reinterpret_cast<const f16x8*>(H + (32 * i + li) * ROWB + co);
+      for (int i = 0; i < RT; ++i) hf[i] = *reinterpret_cast<const f16x8*>(H + (32 * (RT * rg + i) + li) * ROWB + co);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         wf[t] = *reinterpret_cast<const f16x8*>(Ws + (32 * NT * w + 32 * t + li) * ROWB + co);
@@ -482,7 +495,7 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_p_kernel(const TX* __restr
     // bound by how few writes one workgroup per CU keeps in flight, not their shape.)
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
-      const int64_t m = blk * BM + 32 * i + li;
+      const int64_t m = blk * BM + 32 * (RT * rg + i) + li;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -508,12 +521,12 @@ static hipError_t launch_ln_gemm_p(const LnGemmArgs& a) {
   const int64_t cus = compute_units();
   if (a.M >= (int64_t)64 * 2 * cus) {
     const int64_t nblk = (a.M + 63) / 64;
-    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 64, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(kLgThreads), 0,
+    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 64, 8, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(512), 0,
                        a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
                        static_cast<f16*>(a.c), a.M, a.eps);
   } else {
     const int64_t nblk = (a.M + 31) / 32;
-    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 32, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(kLgThreads), 0,
+    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 32, 4, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(kLgThreads), 0,
                        a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
                        static_cast<f16*>(a.c), a.M, a.eps);
   }
