@@ -47,6 +47,7 @@ def token_mask(B, S, seed, left_aligned):
         (5, 100, 128, 1),    # query-split, one head of 128 dims over four waves, ragged S
         (5, 100, 128, 16),   # query-split, four 8-dim heads per wave, ragged S
         (300, 128, 128, 4),  # persistent fused kernel (more than two rounds of slices)
+        (601, 96, 128, 4),   # persistent fused kernel, odd batch, ragged S
         (3, 17, 96, 3),      # persistent fused kernel, d_model 96
         (301, 96, 64, 2),    # persistent, d_model 64: two sequences per workgroup, odd batch
         (3, 333, 128, 2),    # hd 64, several key blocks, 8-wave attention
