@@ -15,7 +15,7 @@ from typing import Optional
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcobra_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F16 = 0
 F32 = 1

@@ -69,20 +69,30 @@ class CobraSelfAttention(nn.Module):
 
 
 class _Pack:
-    """Kernel-ready copies of the parameters (never registered on the module)."""
+    """Kernel-ready copies of the parameters (never registered on the module).
+
+    LN1's elementwise affine is folded into the QKV projection, which consumes
+    nothing else of LN1's output:
+        (n * g1 + b1) W^T + b = n (W diag(g1))^T + (b + W b1),   n = (x - mean) * rstd,
+    so the kernels normalise without reading g1 / b1 (``ln1_w = ln1_b = None``
+    selects that form of ``cobra_layer_fwd``).  W diag(g1) is rounded to fp16 once,
+    as W itself is; the bias term is formed in fp64 and stored in fp32.
+    """
 
     __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "versions")
 
     def __init__(self, m: "CobraAttentionSublayer", versions) -> None:
         att = m.attention
         with torch.no_grad():
-            self.w_qkv = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(
-                torch.float16).contiguous()
-            self.b_qkv = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).float().contiguous()
+            w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).float()
+            b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).double()
+            g1 = m.norm1.weight.float()
+            self.w_qkv = (w * g1).to(torch.float16).contiguous()
+            self.b_qkv = (b + w.double() @ m.norm1.bias.double()).float().contiguous()
+            self.ln1_w = None
+            self.ln1_b = None
             self.w_o = att.out_proj.weight.to(torch.float16).contiguous()
             self.b_o = att.out_proj.bias.float().contiguous()
-            self.ln1_w = m.norm1.weight.float().contiguous()
-            self.ln1_b = m.norm1.bias.float().contiguous()
             self.ln2_w = m.norm2.weight.float().contiguous()
             self.ln2_b = m.norm2.bias.float().contiguous()
         self.versions = versions

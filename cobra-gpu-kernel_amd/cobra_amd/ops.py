@@ -85,8 +85,8 @@ def add_ln(
     resid: torch.Tensor,
     branch: Optional[torch.Tensor],
     mask_row: Optional[torch.Tensor],
-    w: torch.Tensor,
-    b: torch.Tensor,
+    w: Optional[torch.Tensor],
+    b: Optional[torch.Tensor],
     cast_fp16: bool = True,
     eps: float = 1e-5,
     store_resid: bool = True,
@@ -97,7 +97,8 @@ def add_ln(
     Mirrors ``_tl_add_ln`` (TTB:539-569), including its mask rule: with a
     ``mask_row``, the residual is multiplied by the mask whenever it is stored
     or the output is masked, and ``mask_out`` also masks the normalised output.
-    The stored residual is always fp32.
+    The stored residual is always fp32.  ``w = b = None``: no elementwise affine
+    (weight 1, bias 0, which leaves the normalised value exact).
     """
     _dev(resid, "resid")
     if resid.dim() != 2:
@@ -114,7 +115,13 @@ def add_ln(
         _dev(branch, "branch")
         if branch.shape != resid.shape:
             raise ValueError("branch must match resid")
-    gw, gb = _f32_param(w, N, "w"), _f32_param(b, N, "b")
+    if (w is None) != (b is None):
+        raise ValueError("w and b must both be given or both be None")
+    if w is None:
+        gw = torch.ones(N, device=resid.device, dtype=torch.float32)
+        gb = torch.zeros(N, device=resid.device, dtype=torch.float32)
+    else:
+        gw, gb = _f32_param(w, N, "w"), _f32_param(b, N, "b")
     out_r = torch.empty((M, N), device=resid.device, dtype=torch.float32) if store_resid else None
     out_n = torch.empty((M, N), device=resid.device, dtype=torch.float16 if cast_fp16 else torch.float32)
     call(
@@ -348,8 +355,8 @@ def layer_fwd(
     b_qkv: torch.Tensor,
     w_o: torch.Tensor,
     b_o: torch.Tensor,
-    ln1_w: torch.Tensor,
-    ln1_b: torch.Tensor,
+    ln1_w: Optional[torch.Tensor],
+    ln1_b: Optional[torch.Tensor],
     ln2_w: torch.Tensor,
     ln2_b: torch.Tensor,
     y: torch.Tensor,
@@ -363,6 +370,7 @@ def layer_fwd(
     """Enqueue the whole sublayer into caller-provided buffers (no allocation).
 
     x, y: [B, S, D] (same dtype); packed weights as produced by ``CobraAttentionSublayer``;
+    ln1_w = ln1_b = None: LN1 without elementwise affine (already folded into w_qkv / b_qkv);
     valid_mask: optional [B, S] uint8 (0 = padded token) -- the workspace must then be
     sized with ``masked=True``.
     """
@@ -375,7 +383,7 @@ def layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, wor
     """The argument list of ``cobra_layer_fwd``."""
     B, S, D = x.shape
     return [x.data_ptr(), _dtype_code(x, "x"), _ptr(valid_mask), w_qkv.data_ptr(), b_qkv.data_ptr(),
-            w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(), ln2_w.data_ptr(),
+            w_o.data_ptr(), b_o.data_ptr(), _ptr(ln1_w), _ptr(ln1_b), ln2_w.data_ptr(),
             ln2_b.data_ptr(), y.data_ptr(), _ptr(resid_out), workspace.data_ptr(), workspace.numel(),
             B, S, D, heads, 1 if causal else 0, float(eps), _stream(x)]
 
@@ -391,7 +399,7 @@ class LayerLaunch:
         lib = _lib.lib()
         self.handle = None
         h = lib.cobra_layer_bind(_DT[x_dtype], 1 if masked else 0, w_qkv.data_ptr(), b_qkv.data_ptr(),
-                                 w_o.data_ptr(), b_o.data_ptr(), ln1_w.data_ptr(), ln1_b.data_ptr(),
+                                 w_o.data_ptr(), b_o.data_ptr(), _ptr(ln1_w), _ptr(ln1_b),
                                  ln2_w.data_ptr(), ln2_b.data_ptr(), workspace.data_ptr(), workspace.numel(),
                                  batch, seq_len, d_model, heads, 1 if causal else 0, float(eps))
         if not h:

@@ -43,6 +43,11 @@ LayerBuffers layer_buffers(int64_t batch, int64_t seq_len, int64_t d, bool maske
   return b;
 }
 
+// LN1's elementwise affine: both parameters, or neither (LayerNorm without affine).
+bool ln1_affine_ok(const float* w, const float* b) {
+  return (w == nullptr) == (b == nullptr) && opt_aligned16(w) && opt_aligned16(b);
+}
+
 bool layer_shape_ok(int64_t batch, int64_t seq_len, int64_t d, int64_t heads) {
   if (batch < 0 || seq_len < 0 || d <= 0 || heads <= 0 || d % heads != 0) return false;
   const int64_t hd = d / heads;
@@ -158,10 +163,10 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
   const bool masked = valid_mask != nullptr;
   const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked, x_dtype);
   if (plan < 0) return kBad;
-  const void* must[] = {x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y};
+  const void* must[] = {x, w_qkv, b_qkv, w_o, b_o, ln2_w, ln2_b, y};
   for (const void* p : must)
     if (!p || !aligned16(p)) return kBad;
-  if (!opt_aligned16(resid_out) || !opt_aligned16(workspace)) return kBad;
+  if (!ln1_affine_ok(ln1_w, ln1_b) || !opt_aligned16(resid_out) || !opt_aligned16(workspace)) return kBad;
   const int64_t T = batch * seq_len;
   const int64_t D = d_model;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -209,13 +214,18 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     out.epi = masked ? cobra::kEpiMaskBranch : 0;
     return code(cobra::run_gemm(out));
   }
-  float* r = resid_out ? resid_out : reinterpret_cast<float*>(ws + lb.r_off);
-  cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, r, kF32, T, (int)D, (int)D,
+  // r goes to memory between the projection and LayerNorm.  It is kept in fp32 when
+  // the caller asks for it (resid_out) or the activations are fp32; otherwise it is
+  // rounded to fp16, where the reference's fp16 `x + attn_out` (TTB:141) rounds it,
+  // which halves its write and read.
+  const int r_dtype = resid_out || x_dtype == kF32 ? kF32 : kF16;
+  void* r = resid_out ? static_cast<void*>(resid_out) : static_cast<void*>(ws + lb.r_off);
+  cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, r, r_dtype, T, (int)D, (int)D,
                       nullptr, nullptr, nullptr, kF16, eps, s};
   out.row_mask = valid_mask;
   out.epi = masked ? cobra::kEpiMaskBranch : 0;
   if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
-  cobra::LnArgs ln2{r, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
+  cobra::LnArgs ln2{r, r_dtype, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
   return code(cobra::run_ln(ln2));
 }
 
@@ -236,10 +246,10 @@ cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv,
                                      int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps) {
   const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked, x_dtype);
   if (plan < 0) return nullptr;
-  const void* must[] = {w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b};
+  const void* must[] = {w_qkv, b_qkv, w_o, b_o, ln2_w, ln2_b};
   for (const void* p : must)
     if (!p || !aligned16(p)) return nullptr;
-  if (!opt_aligned16(workspace)) return nullptr;
+  if (!ln1_affine_ok(ln1_w, ln1_b) || !opt_aligned16(workspace)) return nullptr;
   const int64_t need = cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, masked, x_dtype);
   if (need > 0 && (!workspace || workspace_bytes < need)) return nullptr;
   auto* h = new (std::nothrow) cobra_layer_launch;

@@ -47,6 +47,17 @@ __device__ __forceinline__ f16x8 acc_f16(const f32x16& acc, int half) {
   return o;
 }
 
+// Adds the eight fp16 probabilities of `p` into two fp32 partial sums (v_dot2 against
+// ones: half the instructions of fp32 adds).  The row sum is thereby taken over the
+// rounded values that the P.V product consumes.
+__device__ __forceinline__ void add_probs(const f16x8& p, float& a, float& b) {
+  const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+  a = __builtin_amdgcn_fdot2(f16x2{p[0], p[1]}, one2, a, false);
+  b = __builtin_amdgcn_fdot2(f16x2{p[2], p[3]}, one2, b, false);
+  a = __builtin_amdgcn_fdot2(f16x2{p[4], p[5]}, one2, a, false);
+  b = __builtin_amdgcn_fdot2(f16x2{p[6], p[7]}, one2, b, false);
+}
+
 // Registers 8*half .. 8*half+7 of a 32x32 accumulator (+ per-register bias), as fp16.
 __device__ __forceinline__ f16x8 half_to_f16(const f32x16& acc, int half, const float (&bias)[16]) {
   f16x8 o;

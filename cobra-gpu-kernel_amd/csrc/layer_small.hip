@@ -143,14 +143,16 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
       if (ROWS_O % NW == 0 || wid + NW * u < ROWS_O) Wol[(wid + NW * u) * 64 + lane] = to[u];
   }
   float* const Pf = reinterpret_cast<float*>(lds + L::CORE);
+  const bool aff1 = g1 != nullptr;  // LN1 with elementwise affine
   if constexpr (L::PARAMS) {
     const float* src[6] = {bqkv, bo, g1, be1, g2, be2};
     const int len[6] = {3 * D, D, D, D, D, D};
     int off = 0;
 #pragma unroll
     for (int v = 0; v < 6; ++v) {
-      for (int i = 4 * (int)threadIdx.x; i < len[v]; i += 4 * 64 * kSmallWaves * G)
-        *reinterpret_cast<f32x4*>(Pf + off + i) = *reinterpret_cast<const f32x4*>(src[v] + i);
+      if (src[v])  // null gamma1 / beta1: no LN1 affine, nothing to stage
+        for (int i = 4 * (int)threadIdx.x; i < len[v]; i += 4 * 64 * kSmallWaves * G)
+          *reinterpret_cast<f32x4*>(Pf + off + i) = *reinterpret_cast<const f32x4*>(src[v] + i);
       off += len[v];
     }
   }
@@ -229,13 +231,20 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
           q += t * t;
         }
       const float rstd = rsqrtf(sum_xor32(q) * (1.0f / D) + eps);
+      if (aff1) {
 #pragma unroll
-      for (int kk = 0; kk < KD; ++kk) {
-        float gv[8], bv[8];
-        load8(gamma1 + 16 * kk + 8 * g, gv);
-        load8(beta1 + 16 * kk + 8 * g, bv);
+        for (int kk = 0; kk < KD; ++kk) {
+          float gv[8], bv[8];
+          load8(gamma1 + 16 * kk + 8 * g, gv);
+          load8(beta1 + 16 * kk + 8 * g, bv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hB[kk][e] = (f16)((xv[kk][e] - mean) * rstd * gv[e] + bv[e]);
+          for (int e = 0; e < 8; ++e) hB[kk][e] = (f16)((xv[kk][e] - mean) * rstd * gv[e] + bv[e]);
+        }
+      } else {  // no elementwise affine (folded into W_qkv / b_qkv by the caller)
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hB[kk][e] = (f16)((xv[kk][e] - mean) * rstd);
       }
     }
 
@@ -328,11 +337,9 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
       for (int t = 0; t < MAXT; ++t) {
         f16x8 pB[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
-          lp[r & 3] += pv;
-          pB[r >> 3][r & 7] = (f16)pv;
-        }
+        for (int r = 0; r < 16; ++r) pB[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
+        add_probs(pB[0], lp[0], lp[1]);
+        add_probs(pB[1], lp[2], lp[3]);
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll

@@ -202,7 +202,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 
   // ---- DMA, in the order the data is needed -------------------------------------------
   const RowSpans<D> spans(lane);
-  {  // [gamma1 | beta1]
+  const bool aff1 = g1 != nullptr;  // LN1 with elementwise affine
+  if (aff1) {  // [gamma1 | beta1] (later vmcnt waits count only what follows the token tile)
     const int c = 4 * lane;
     dma16(c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0), rP);
   }
@@ -276,10 +277,12 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     // below so one wait covers them.
     const float* pg = reinterpret_cast<const float*>(rP);
     float gv[KD][8], bv[KD][8];
+    if (aff1) {
 #pragma unroll
-    for (int kk = 0; kk < KD; ++kk) {
-      load8(pg + 16 * kk + 8 * g, gv[kk]);
-      load8(pg + D + 16 * kk + 8 * g, bv[kk]);
+      for (int kk = 0; kk < KD; ++kk) {
+        load8(pg + 16 * kk + 8 * g, gv[kk]);
+        load8(pg + D + 16 * kk + 8 * g, bv[kk]);
+      }
     }
     float xv[KD][8];
     float qp[2] = {0.f, 0.f};
@@ -297,7 +300,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int kk = 0; kk < KD; ++kk) {
       f16x8 h;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = (f16)fmaf(xv[kk][e] * rstd, gv[kk][e], bv[kk][e]);
+      for (int e = 0; e < 8; ++e)
+        h[e] = (f16)(aff1 ? fmaf(xv[kk][e] * rstd, gv[kk][e], bv[kk][e]) : xv[kk][e] * rstd);
       Hb[(w * KD + kk) * 64 + lane] = h;
     }
   }

@@ -6,7 +6,8 @@
 // row held in registers (mean, then centred biased variance, /N), eps inside
 // the square root, affine, cast on store.  The row mask m (0 for a padded row,
 // 1 otherwise) multiplies the residual (MASK_RESID) and/or the output
-// (MASK_OUT) as the reference kernel does (TTB:511-534).
+// (MASK_OUT) as the reference kernel does (TTB:511-534).  A null gamma (and beta)
+// means a LayerNorm without elementwise affine.
 //
 // Layout: LPR lanes own one row, each lane holds NCH chunks of 8 consecutive
 // elements (16 B of fp16, 32 B of fp32), so every global access is a full
@@ -83,15 +84,20 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 8 : 1) void ln_rows_kernel(const TX
     const int ch = li + c * LPR;
     if (!(active && ch < nch)) continue;
     if (resid_out) store8(resid_out + base + ch * 8, v[c]);
-    const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + ch * 8);
-    const f32x4 g1 = *reinterpret_cast<const f32x4*>(gamma + ch * 8 + 4);
-    const f32x4 b0 = *reinterpret_cast<const f32x4*>(beta + ch * 8);
-    const f32x4 b1 = *reinterpret_cast<const f32x4*>(beta + ch * 8 + 4);
     float o[8];
+    if (gamma) {
+      const f32x4 g0 = *reinterpret_cast<const f32x4*>(gamma + ch * 8);
+      const f32x4 g1 = *reinterpret_cast<const f32x4*>(gamma + ch * 8 + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(beta + ch * 8);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(beta + ch * 8 + 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o[i] = (v[c][i] - mean) * rstd * g0[i] + b0[i];
-      o[i + 4] = (v[c][i + 4] - mean) * rstd * g1[i] + b1[i];
+      for (int i = 0; i < 4; ++i) {
+        o[i] = (v[c][i] - mean) * rstd * g0[i] + b0[i];
+        o[i + 4] = (v[c][i + 4] - mean) * rstd * g1[i] + b1[i];
+      }
+    } else {  // no elementwise affine
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (v[c][i] - mean) * rstd;
     }
     if (mask_out) {
 #pragma unroll

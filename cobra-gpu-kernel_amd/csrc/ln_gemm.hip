@@ -28,6 +28,22 @@ __device__ __forceinline__ int lg_swz(int r) {
   return D == 128 ? (r & 15) : ((r >> 1) & 7);  // 16 / 8 chunks per row
 }
 
+// gamma / beta of 8 columns; null (LayerNorm without elementwise affine) reads
+// as gamma 1, beta 0, which leaves the normalised value exact.
+__device__ __forceinline__ void load_affine8(const float* gamma, const float* beta, int c0, float (&gv)[8],
+                                             float (&bv)[8]) {
+  if (gamma) {
+    load8(gamma + c0, gv);
+    load8(beta + c0, bv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gv[e] = 1.f;
+      bv[e] = 0.f;
+    }
+  }
+}
+
 }  // namespace
 
 template <int D, typename TX>
@@ -74,8 +90,7 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
     load8(x + min(m0 + r, M - 1) * D + 8 * cl, xv[p]);
   }
   float gv[8], bv[8];
-  load8(gamma + 8 * cl, gv);
-  load8(beta + 8 * cl, bv);
+  load_affine8(gamma, beta, 8 * cl, gv, bv);
 #pragma unroll
   for (int i = 0; i < WCH; ++i) {
     const int c = tid + i * kLgThreads;
@@ -267,8 +282,7 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
   static_assert(BM % RPP == 0, "row pass covers the block");
   const int cl = tid % LPR;
   float gv[8], bv[8];
-  load8(gamma + 8 * cl, gv);
-  load8(beta + 8 * cl, bv);
+  load_affine8(gamma, beta, 8 * cl, gv, bv);
 #pragma unroll
   for (int rr0 = 0; rr0 < BM; rr0 += RPP) {
     const int row = rr0 + tid / LPR;
@@ -409,8 +423,7 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
     }
   }
   float gv[8], bv[8];
-  load8(gamma + 8 * cl, gv);
-  load8(beta + 8 * cl, bv);
+  load_affine8(gamma, beta, 8 * cl, gv, bv);
   // Bias of this wave's columns in the accumulator layout: tile t, register r ->
   // column 32 NT w + 32 t + 8 (r / 4) + 4 g + r % 4.
   f32x16 bt[NT];
@@ -547,7 +560,7 @@ bool ln_gemm_ok(int64_t d, int x_dtype) { return (d == 64 || d == 128) && (x_dty
 
 hipError_t run_ln_gemm(const LnGemmArgs& a) {
   if (!ln_gemm_ok(a.d, a.x_dtype) || a.M < 0 || a.N <= 0 || a.N % 8 != 0 || a.N > 3 * a.d) return hipErrorInvalidValue;
-  if (!a.x || !a.w || !a.c || !a.gamma || !a.beta) return hipErrorInvalidValue;
+  if (!a.x || !a.w || !a.c || (a.gamma == nullptr) != (a.beta == nullptr)) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;
   if (a.d == 128 && a.N == 384) return a.x_dtype == kF16 ? launch_ln_gemm_p<3, f16>(a) : launch_ln_gemm_p<3, float>(a);
   if (a.d == 128) return a.x_dtype == kF16 ? launch_ln_gemm<128, f16>(a) : launch_ln_gemm<128, float>(a);

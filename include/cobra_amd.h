@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 4
+#define COBRA_ABI_VERSION 5
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
 
@@ -166,7 +166,10 @@ int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_mo
  * x, y: [batch*seq_len, d_model] in x_dtype; w_qkv: [3*d_model, d_model] fp16
  * (rows: q_proj, k_proj, v_proj weights, in that order); b_qkv: [3*d_model]
  * fp32; w_o: [d_model, d_model] fp16; b_o and the LayerNorm parameters fp32.
- * resid_out (optional): r in fp32.  workspace: cobra_layer_workspace_bytes()
+ * ln1_w and ln1_b may both be NULL: LN1 without elementwise affine, for a
+ * caller that has folded it into the projection (w_qkv . diag(ln1_w) and
+ * b_qkv + w_qkv . ln1_b), which spares the kernels those reads; exactly one
+ * of them NULL is rejected.  resid_out (optional): r in fp32.  workspace: cobra_layer_workspace_bytes()
  * bytes (may be NULL when that is 0).  One launch for the FUSED plan.
  * Replaces the attention half of UserOptimizedTransformer._run_fused
  * (TTB:1216-1268), which is what its CUDA graph replays (TTB:1331-1360).

@@ -1,0 +1,121 @@
+"""GPU tests of the LayerNorm parameters on every plan.
+
+The reference initialises both LayerNorms to weight 1, bias 0 (TTB:129-131), so
+the other parity cases leave the affine parts untested.  Here LN1 / LN2 weights
+and biases and the projection biases are random, through the module (whose
+packed weights carry LN1's affine, folded into W_qkv / b_qkv) against the fp32
+oracle, and ``cobra_layer_fwd`` with LN1's affine left out (NULL) is checked
+against the same call with weight 1 / bias 0.
+"""
+
+import pytest
+import torch
+
+from oracle import compare_outputs, make_input
+
+from _gpu_util import DEV, build_pair, log, oracle_on
+
+pytestmark = pytest.mark.gpu
+
+
+def _randomise_affine(ref, seed):
+    """Non-trivial LayerNorm and bias parameters, fp16-representable."""
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for ln in (ref.norm1, ref.norm2):
+            ln.weight.copy_((torch.rand(ln.weight.shape, generator=g) + 0.5).half().float())
+            ln.bias.copy_(((torch.rand(ln.bias.shape, generator=g) - 0.5) * 0.6).half().float())
+        att = ref.attention
+        for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj):
+            lin.bias.copy_(((torch.rand(lin.bias.shape, generator=g) - 0.5) * 0.2).half().float())
+
+
+def _pair(D, H, dtype=torch.float16, seed=0):
+    ref, mod = build_pair(D, H, seed=seed, dtype=dtype)
+    _randomise_affine(ref, seed + 100)
+    mod.load_state_dict(ref.state_dict(), strict=True)
+    return ref, mod
+
+
+# (B, S, D, H, causal, masked, x dtype, expected plan, compared sequences)
+CASES = [
+    (4, 128, 128, 4, False, False, torch.float16, "fused", None),    # query-split, head_dim 32
+    (4, 128, 128, 16, False, False, torch.float16, "fused", None),   # query-split, head_dim 8
+    (4, 128, 128, 1, True, False, torch.float16, "fused", None),     # query-split, one 128-dim head
+    (3, 100, 64, 2, False, True, torch.float16, "fused", None),      # query-split d_model 64, masked
+    (1100, 100, 128, 4, False, False, torch.float16, "fused", [0, 549, 1099]),  # persistent
+    (1100, 100, 128, 4, True, True, torch.float16, "fused", [0, 1099]),         # persistent, causal + mask
+    (8, 128, 128, 4, False, False, torch.float32, "fused", None),    # persistent, fp32 activations
+    (8, 128, 128, 16, False, False, torch.float32, "staged", None),  # LN1 in the QKV GEMM's prologue
+    (2, 128, 1024, 16, False, True, torch.float16, "staged", None),  # LayerNorm pass + LDS-DMA GEMMs
+]
+
+
+def _mask(B, S, seed):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.rand(B, S, generator=g) > 0.2
+    m[:, 0] = True
+    return m
+
+
+@pytest.mark.parametrize("B,S,D,H,causal,masked,dtype,plan,rows", CASES,
+                         ids=[f"B{c[0]}-S{c[1]}-D{c[2]}-H{c[3]}-{'c' if c[4] else 'n'}{'m' if c[5] else ''}-"
+                              f"{'f32' if c[6] == torch.float32 else 'f16'}" for c in CASES])
+def test_random_layernorm_parameters_match_oracle(B, S, D, H, causal, masked, dtype, plan, rows):
+    ref, mod = _pair(D, H, dtype=dtype)
+    x = make_input(B, S, D, seed=5)
+    if dtype == torch.float16:
+        x = x.half()
+    m = _mask(B, S, 9) if masked else None
+    log(f"[ln affine] B{B} S{S} D{D} H{H} causal={causal} masked={masked} {dtype}")
+    with torch.inference_mode():
+        y = mod(x.to(DEV), valid_token_mask=None if m is None else m.to(DEV), causal=causal)
+        torch.cuda.synchronize()
+    assert mod.plan == (0 if plan == "fused" else 1)
+    sel = list(range(B)) if rows is None else rows
+    want = oracle_on(ref, x[sel].float(), causal, "cpu", mask=None if m is None else m[sel])
+    res = compare_outputs(want, y.float().cpu()[sel])
+    log(f"[ln affine] plan={plan} max_abs={res.max_abs_error:.3e} failed={res.failed_elements}")
+    assert res.passed, res
+
+
+@pytest.mark.parametrize("B,S,D,H,causal,masked,dtype,plan,rows", CASES,
+                         ids=[f"B{c[0]}-S{c[1]}-D{c[2]}-H{c[3]}-{'c' if c[4] else 'n'}{'m' if c[5] else ''}-"
+                              f"{'f32' if c[6] == torch.float32 else 'f16'}" for c in CASES])
+def test_null_ln1_affine_equals_unit_affine(B, S, D, H, causal, masked, dtype, plan, rows):
+    """cobra_layer_fwd with ln1_w = ln1_b = NULL (LayerNorm without affine) on the
+    folded weights computes the reference sublayer, as does the same call with
+    weight 1 / bias 0; the two differ only where the normalised value is rounded
+    (the compiler may round (x - mean) * rstd to fp16 in one step where weight /
+    bias go through an fp32 multiply-add first), i.e. in few elements."""
+    from cobra_amd import ops
+
+    ref, mod = _pair(D, H, dtype=dtype)
+    x = make_input(B, S, D, seed=6)
+    if dtype == torch.float16:
+        x = x.half()
+    m = _mask(B, S, 10) if masked else None
+    log(f"[null ln1] B{B} S{S} D{D} H{H} causal={causal} masked={masked} {dtype}")
+    xd = x.to(DEV)
+    md = None if m is None else m.to(DEV).to(torch.uint8)
+    with torch.inference_mode():
+        p = mod._packed()
+        ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H, masked, dtype), dtype=torch.uint8, device=DEV)
+        ones = torch.ones(D, device=DEV)
+        zeros = torch.zeros(D, device=DEV)
+        outs = []
+        for w1, b1 in ((None, None), (ones, zeros)):
+            y = torch.empty_like(xd)
+            ops.layer_fwd(xd, p.w_qkv, p.b_qkv, p.w_o, p.b_o, w1, b1, p.ln2_w, p.ln2_b, y, ws, H, causal,
+                          valid_mask=md)
+            outs.append(y.float().cpu())
+        torch.cuda.synchronize()
+    assert ops.layer_plan(B, S, D, H, masked, dtype) == (0 if plan == "fused" else 1)
+    sel = list(range(B)) if rows is None else rows
+    want = oracle_on(ref, x[sel].float(), causal, "cpu", mask=None if m is None else m[sel])
+    for y in outs:
+        res = compare_outputs(want, y[sel])
+        assert res.passed, res
+    frac = (outs[0] != outs[1]).float().mean().item()
+    log(f"[null ln1] plan={plan} null vs unit affine: differing fraction {frac:.2e}")
+    assert frac < 1e-3

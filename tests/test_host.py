@@ -78,6 +78,46 @@ def test_layer_bind_validates_and_releases():
     assert h
     lib.cobra_layer_unbind(h)
     assert not lib.cobra_layer_bind(1, 1, *w, 4096, ws - 1, 2, 16, 128, 16, 0, 1e-5)
+    # LN1's affine: both parameters (w[4], w[5]) or neither; one alone, or misaligned, is rejected
+    h = lib.cobra_layer_bind(0, 0, *w[:4], None, None, *w[6:], None, 0, 2, 16, 128, 4, 0, 1e-5)
+    assert h
+    lib.cobra_layer_unbind(h)
+    assert not lib.cobra_layer_bind(0, 0, *w[:4], None, w[5], *w[6:], None, 0, 2, 16, 128, 4, 0, 1e-5)
+    assert not lib.cobra_layer_bind(0, 0, *w[:4], w[4], None, *w[6:], None, 0, 2, 16, 128, 4, 0, 1e-5)
+    assert not lib.cobra_layer_bind(0, 0, *w[:4], w[4] + 4, w[5], *w[6:], None, 0, 2, 16, 128, 4, 0, 1e-5)
+    # the same check in cobra_layer_fwd, before any launch (x = 4096, y = 8192)
+    assert lib.cobra_layer_fwd(4096, 0, None, *w[:4], None, w[5], *w[6:], 8192, None, None, 0, 2, 16, 128, 4, 0,
+                               1e-5, None) != 0
+
+
+def test_ln1_fold_matches_layernorm_then_projection():
+    """The module's packed QKV weights carry LN1's affine: LayerNorm without affine
+    followed by the folded projection equals LayerNorm with affine followed by the
+    original projection (fp64, up to the fp16 rounding of W diag(g1)).  Weights and
+    LayerNorm parameters are non-uniform, so scaling the wrong axis of W, dropping
+    the W b1 term or its sign fails."""
+    from cobra_amd import CobraAttentionSublayer
+    from cobra_amd.layer import _Pack
+
+    torch.manual_seed(3)
+    D = 64
+    m = CobraAttentionSublayer(D, 4)
+    with torch.no_grad():
+        m.norm1.weight.uniform_(0.5, 1.5)
+        m.norm1.bias.uniform_(-0.5, 0.5)
+        for lin in (m.attention.q_proj, m.attention.k_proj, m.attention.v_proj):
+            lin.bias.uniform_(-0.1, 0.1)
+    p = _Pack(m, None)
+    assert p.ln1_w is None and p.ln1_b is None
+    assert p.w_qkv.dtype == torch.float16 and p.b_qkv.dtype == torch.float32
+    x = torch.randn(32, D, dtype=torch.float64) * 2 + 0.3
+    att = m.attention
+    w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).double()
+    b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).double()
+    want = torch.nn.functional.layer_norm(x, (D,), m.norm1.weight.double(), m.norm1.bias.double()) @ w.T + b
+    got = torch.nn.functional.layer_norm(x, (D,)) @ p.w_qkv.double().T + p.b_qkv.double()
+    assert torch.allclose(got, want, rtol=0, atol=2e-3), (got - want).abs().max()
+    assert (got - want).abs().max() > 0  # the fp16 rounding of W diag(g1) is visible, not skipped
 
 
 def test_workspace_size_formula():
