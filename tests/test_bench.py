@@ -1,0 +1,75 @@
+"""CPU tests of bench.py's accounting and its command-line contract."""
+
+import os
+import subprocess
+import sys
+
+import pytest
+import torch
+from torch.utils.flop_counter import FlopCounterMode
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+from oracle import make_input, make_sublayer  # noqa: E402
+from oracle.cases import oracle_forward  # noqa: E402
+
+
+@pytest.mark.parametrize("B,S,D,H,causal", [(2, 16, 32, 4, False), (1, 24, 64, 2, False), (3, 8, 16, 1, False)])
+def test_layer_flops_equal_an_independent_count(B, S, D, H, causal):
+    """bench's FLOP formula (8 T D^2 + 4 B S^2 D) against torch's own count of the
+    matrix products the oracle layer runs (four projections, q k^T, p v)."""
+    layer = make_sublayer(D, H, seed=0)
+    x = make_input(B, S, D, seed=0)
+    with FlopCounterMode(display=False) as fc, torch.no_grad():
+        oracle_forward(layer, x, causal=causal)
+    assert fc.get_total_flops() == bench.layer_flops(B, S, D, causal)
+
+
+def test_layer_bytes_match_the_committed_traffic_file():
+    """The algorithmic bytes in the committed counter summary are bench's formula for
+    the headline workload, and the measured traffic is at least that."""
+    fields = {}
+    with open(bench.TRAFFIC_FILE) as f:
+        for line in f:
+            if "=" in line and not line.startswith("#"):
+                k, v = line.strip().split("=", 1)
+                fields[k] = float(v)
+    assert fields["algorithmic_bytes_per_launch"] == bench.layer_bytes(64, 128, 128)
+    assert bench.committed_traffic() == fields["traffic_bytes_per_launch"]
+    assert fields["traffic_bytes_per_launch"] >= fields["algorithmic_bytes_per_launch"]
+    kib = 1024
+    want = (fields["kernel_fetch_kib_per_dispatch"] * fields["fetch_scale"]
+            + fields["kernel_write_kib_per_dispatch"] * fields["write_scale"]) * kib
+    assert abs(want - fields["traffic_bytes_per_launch"]) <= 16 * kib  # scale rounded to 4 places
+
+
+def test_roofline_picks_the_bound_by_arithmetic_intensity():
+    ridge = bench.PEAK_FP16_TFLOPS * 1e12 / (bench.PEAK_HBM_GBS * 1e9)
+    r = bench.roofline("k", flops=ridge * 2e6, nbytes=1e6, ms=1.0)
+    assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s"
+    assert r["achieved"] == pytest.approx(ridge * 2e6 / 1e-3 / 1e12)
+    r = bench.roofline("k", flops=ridge * 0.5e6, nbytes=1e6, ms=1.0)
+    assert r["bound"] == "hbm" and r["unit"] == "GB/s"
+    assert r["frac"] == pytest.approx(1e6 / 1e-3 / 1e9 / bench.PEAK_HBM_GBS)
+
+
+def _run_bench(*args):
+    return subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], capture_output=True, text=True,
+                          timeout=300, cwd=ROOT)
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    res = _run_bench("--gpus", "2")
+    assert res.returncode == 2
+    assert "one GPU" in res.stderr
+    assert res.stdout == ""
+
+
+def test_without_a_gpu_bench_exits_with_a_message():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    res = _run_bench("--steps", "1", "--warmup", "0")
+    assert res.returncode == 2
+    assert "GPU" in res.stderr
