@@ -367,6 +367,30 @@ def test_add_ln_op():
         assert torch.allclose(y, want, atol=2e-5, rtol=1e-4), (M, N, (y - want).abs().max())
 
 
+@pytest.mark.parametrize("N", [512, 1024])
+@pytest.mark.parametrize("x_dtype,out16", [(torch.float16, True), (torch.float32, True), (torch.float16, False),
+                                           (torch.float32, False)])
+def test_add_ln_plain_rows(N, x_dtype, out16):
+    """Rows of 512 / 1024 with no branch, mask or stored residual (the staged sublayer's
+    LayerNorm passes, which take a kernel of their own): ragged row counts, every
+    in / out dtype, with and without the elementwise affine, against torch in fp32."""
+    from cobra_amd import ops
+
+    torch.manual_seed(N)
+    for M in (1, 3, 4097):
+        x = (torch.randn(M, N, device=DEV) * 2 + 0.5).to(x_dtype)
+        g = torch.rand(N, device=DEV) + 0.5
+        be = torch.randn(N, device=DEV) * 0.3
+        for w, b in ((g, be), (None, None)):
+            r, y = ops.add_ln(x, None, None, w, b, cast_fp16=out16, store_resid=False)
+            assert r is None and y.dtype == (torch.float16 if out16 else torch.float32)
+            want = torch.nn.functional.layer_norm(x.float(), (N,), w, b, 1e-5)
+            if out16:
+                assert torch.allclose(y.float(), want, atol=2e-3, rtol=1e-3), (M, (y.float() - want).abs().max())
+            else:
+                assert torch.allclose(y, want, atol=2e-5, rtol=1e-4), (M, (y - want).abs().max())
+
+
 @pytest.mark.parametrize("hd", [8, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 def test_attn_op(hd, causal):
