@@ -30,6 +30,19 @@ def build_pair(d_model: int, heads: int, seed: int = 0, dtype: torch.dtype = tor
     return ref, mod
 
 
+def randomise_affine(ref, seed: int) -> None:
+    """Non-trivial LayerNorm weights / biases and projection biases, fp16-representable
+    (the reference initialises LayerNorms to 1 / 0 and draws the biases with the weights)."""
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for ln in (ref.norm1, ref.norm2):
+            ln.weight.copy_((torch.rand(ln.weight.shape, generator=g) + 0.5).half().float())
+            ln.bias.copy_(((torch.rand(ln.bias.shape, generator=g) - 0.5) * 0.6).half().float())
+        att = ref.attention
+        for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj):
+            lin.bias.copy_(((torch.rand(lin.bias.shape, generator=g) - 0.5) * 0.2).half().float())
+
+
 def oracle_on(ref, x: torch.Tensor, causal: bool, device, block_q=None, return_residual=False, mask=None):
     """Run the fp32 oracle on ``device`` (CPU for small cases, the GPU for big ones)."""
     layer = ref.to(device)

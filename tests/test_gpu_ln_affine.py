@@ -13,26 +13,14 @@ import torch
 
 from oracle import compare_outputs, make_input
 
-from _gpu_util import DEV, build_pair, log, oracle_on
+from _gpu_util import DEV, build_pair, log, oracle_on, randomise_affine
 
 pytestmark = pytest.mark.gpu
 
 
-def _randomise_affine(ref, seed):
-    """Non-trivial LayerNorm and bias parameters, fp16-representable."""
-    g = torch.Generator().manual_seed(seed)
-    with torch.no_grad():
-        for ln in (ref.norm1, ref.norm2):
-            ln.weight.copy_((torch.rand(ln.weight.shape, generator=g) + 0.5).half().float())
-            ln.bias.copy_(((torch.rand(ln.bias.shape, generator=g) - 0.5) * 0.6).half().float())
-        att = ref.attention
-        for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj):
-            lin.bias.copy_(((torch.rand(lin.bias.shape, generator=g) - 0.5) * 0.2).half().float())
-
-
 def _pair(D, H, dtype=torch.float16, seed=0):
     ref, mod = build_pair(D, H, seed=seed, dtype=dtype)
-    _randomise_affine(ref, seed + 100)
+    randomise_affine(ref, seed + 100)
     mod.load_state_dict(ref.state_dict(), strict=True)
     return ref, mod
 

@@ -14,7 +14,7 @@ import torch
 
 from oracle import compare_outputs, make_input
 
-from _gpu_util import DEV, build_pair, log, oracle_on
+from _gpu_util import DEV, build_pair, log, oracle_on, randomise_affine
 
 pytestmark = pytest.mark.gpu
 
@@ -37,24 +37,13 @@ def _cases(n=24, seed=20261202):
     return out
 
 
-def _randomise(ref, seed):
-    g = torch.Generator().manual_seed(seed)
-    with torch.no_grad():
-        for ln in (ref.norm1, ref.norm2):
-            ln.weight.copy_((torch.rand(ln.weight.shape, generator=g) + 0.5).half().float())
-            ln.bias.copy_(((torch.rand(ln.bias.shape, generator=g) - 0.5) * 0.6).half().float())
-        att = ref.attention
-        for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj):
-            lin.bias.copy_(((torch.rand(lin.bias.shape, generator=g) - 0.5) * 0.2).half().float())
-
-
 @pytest.mark.parametrize("i,B,S,D,H,causal,masked,dtype", _cases(),
                          ids=[f"{c[0]:02d}-B{c[1]}-S{c[2]}-D{c[3]}-H{c[4]}-{'c' if c[5] else 'n'}"
                               f"{'m' if c[6] else ''}-{'f32' if c[7] == torch.float32 else 'f16'}" for c in _cases()])
 def test_random_config_matches_oracle(i, B, S, D, H, causal, masked, dtype):
     log(f"[random {i:02d}] B{B} S{S} D{D} H{H} causal={causal} masked={masked} {dtype}")
     ref, mod = build_pair(D, H, seed=i, dtype=dtype)
-    _randomise(ref, 1000 + i)
+    randomise_affine(ref, 1000 + i)
     mod.load_state_dict(ref.state_dict(), strict=True)
     x = make_input(B, S, D, seed=i)
     if dtype == torch.float16:
