@@ -38,6 +38,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "layer_common.hpp"
+#include "lds_dma.hpp"
 
 namespace cobra {
 
@@ -78,7 +79,14 @@ constexpr int small_groups() {
   return sizeof(TX) == 2 && fits && D <= 64 ? 2 : 1;
 }
 
-template <int D, int HD, bool CAUSAL, bool MASKED, typename TX, int G>
+// FULL: every lane's token is in range -- S equals the 32 * kSmallWaves token slots of a
+// sequence's waves (a shorter S leaves the last wave's lanes past it, whose rows belong
+// to the next sequence) -- one sequence per workgroup and no residual output, so the
+// stores of a sequence are unconditional.  The compiler then
+// counts them and waits at the next sequence's LN1 only for that sequence's prefetched
+// input; behind a per-lane condition it waits for every store to complete as well
+// (~1 us per sequence at B10000).
+template <int D, int HD, bool CAUSAL, bool MASKED, typename TX, int G, bool FULL>
 __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
                                                           const float* __restrict__ bqkv, const f16* __restrict__ wo,
                                                           const float* __restrict__ bo, const float* __restrict__ g1,
@@ -106,7 +114,8 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
   f16x8* const Vl = Kl + L::KCH;
   const int li = lane & 31, g = lane >> 5;
   const int tok = w * 32 + li;
-  const bool tok_ok = tok < S;
+  static_assert(!FULL || G == 1, "FULL takes one sequence per workgroup");
+  const bool tok_ok = FULL || tok < S;
 
   // ---- stage the weights: 64-chunk row r (one k-step of one 32-row tile) goes
   // to wave r % 4, so every trip count below is a compile-time constant:
@@ -164,6 +173,15 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
   Raw8 xpre[KD];
   KeyBytes kpre{1, 1};
   auto load_ln1_input = [&](int sq) {
+    if constexpr (FULL) {
+      // Unconditional (see FULL): past the batch, sequence B - 1 is read again and unused.
+      const int sqc = sq < B ? sq : B - 1;
+      if constexpr (MASKED) kpre = load_key_bytes(vmask + (int64_t)sqc * S, S, lane);
+      const TX* xr = x + ((int64_t)sqc * S + tok) * D + 8 * g;
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) xpre[kk] = *reinterpret_cast<const Raw8*>(xr + 16 * kk);
+      return;
+    }
     if constexpr (MASKED) {
       if (sq < B) kpre = load_key_bytes(vmask + (int64_t)sq * S, S, lane);
     }
@@ -183,6 +201,10 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
   // workgroup-wide): a group past the batch computes on zeros and stores nothing.
   const int ngroups = (B + G - 1) / G;
   load_ln1_input((int)blockIdx.x * G + grp);
+  // FULL: the first sequence's input is waited for here, and each later one right after
+  // the previous sequence's 2 NNT stores (below), so that on both edges into the loop it
+  // is known complete and no wait for outstanding stores lands at the loop's head.
+  if constexpr (FULL) wait_vmcnt<0>();
 
   for (int sg = blockIdx.x; sg < ngroups; sg += gridDim.x) {
     const int seq = sg * G + grp;
@@ -461,12 +483,13 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
           for (int qd = 0; qd < 4; ++qd) store4(yrow + 32 * nt + 8 * qd + 4 * g, o[nt][qd]);
       }
     }
-    if (resid_out && tok_ok && live) {
+    if (!FULL && resid_out && tok_ok && live) {
 #pragma unroll
       for (int nt = 0; nt < NNT; ++nt)
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) store4(resid_out + row * D + 32 * nt + 8 * qd + 4 * g, v[nt][qd]);
     }
+    if constexpr (FULL) wait_vmcnt<2 * NNT>();  // the prefetch, not the stores behind it
   }  // sequence loop
 }
 
@@ -483,22 +506,32 @@ bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads) {
 
 // Always four waves: the waves past the sequence's last 32-token tile still
 // share the weight staging (and compute masked tiles nobody reads).
+template <int D, int HD, bool CAUSAL, typename TX, int G, bool FULL>
+static hipError_t launch_small_kernel(const SmallLayerArgs& a, float c2, int64_t grid) {
+  if (a.valid_mask)
+    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, true, TX, G, FULL>), dim3((unsigned)grid),
+                       dim3(64 * kSmallWaves * G), 0, a.stream, static_cast<const TX*>(a.x),
+                       static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w,
+                       a.ln1_b, a.ln2_w, a.ln2_b, static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len,
+                       c2, a.eps, a.valid_mask);
+  else
+    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, false, TX, G, FULL>), dim3((unsigned)grid),
+                       dim3(64 * kSmallWaves * G), 0, a.stream, static_cast<const TX*>(a.x),
+                       static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w,
+                       a.ln1_b, a.ln2_w, a.ln2_b, static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len,
+                       c2, a.eps, nullptr);
+  return hipGetLastError();
+}
+
 template <int D, int HD, bool CAUSAL, typename TX>
 static hipError_t launch_small(const SmallLayerArgs& a, float c2) {
   constexpr int G = small_groups<D, HD, TX>();
   const int64_t groups = (a.batch + G - 1) / G;
   const int64_t grid = groups < compute_units() ? groups : compute_units();
-  if (a.valid_mask)
-    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, true, TX, G>), dim3((unsigned)grid), dim3(64 * kSmallWaves * G), 0,
-                       a.stream, static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
-                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
-                       static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps, a.valid_mask);
-  else
-    hipLaunchKernelGGL((layer_small_kernel<D, HD, CAUSAL, false, TX, G>), dim3((unsigned)grid), dim3(64 * kSmallWaves * G), 0,
-                       a.stream, static_cast<const TX*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
-                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
-                       static_cast<TX*>(a.y), a.resid_out, (int)a.batch, (int)a.seq_len, c2, a.eps, nullptr);
-  return hipGetLastError();
+  if constexpr (G == 1 && sizeof(TX) == 2) {
+    if (a.seq_len == 32 * kSmallWaves && !a.resid_out) return launch_small_kernel<D, HD, CAUSAL, TX, G, true>(a, c2, grid);
+  }
+  return launch_small_kernel<D, HD, CAUSAL, TX, G, false>(a, c2, grid);
 }
 
 template <int D, int HD, bool CAUSAL>

@@ -445,3 +445,31 @@ def test_ln_linear_op(d, xdt):
         want = h @ w.float().t() + b
         err = (got.float() - want).abs().max().item()
         assert torch.allclose(got.float(), want, atol=4e-3, rtol=4e-3), (d, xdt, M, N, err)
+
+
+@pytest.mark.parametrize("B,S,causal,masked", [(600, 128, False, False), (601, 128, True, True), (777, 96, False, True)])
+def test_persistent_store_variants_agree(B, S, causal, masked):
+    """The persistent kernel at S = 128 (every token slot of its four waves in use)
+    without a residual output takes a variant with unconditional stores and prefetches
+    (past the batch it re-reads the last sequence); asking for the residual selects the
+    general one.  Same arithmetic, so y is bit-identical.  S = 96 (the last wave's lanes
+    past S) must take the general variant both ways."""
+    from cobra_amd import ops
+
+    assert ops.layer_plan(B, S, 128, 4, masked) == 0
+    ref, mod = build_pair(128, 4, seed=3)
+    x = make_input(B, S, 128, seed=4).half().to(DEV)
+    m = None
+    if masked:
+        g = torch.Generator().manual_seed(5)
+        m = (torch.rand(B, S, generator=g) > 0.25)
+        m[:, 0] = True
+        m = m.to(DEV)
+    log(f"[persistent variants] B{B} S{S} causal={causal} masked={masked}")
+    with torch.inference_mode():
+        y_full = mod(x, valid_token_mask=m, causal=causal)
+        r, y_gen = mod(x, valid_token_mask=m, causal=causal, return_residual=True)
+        torch.cuda.synchronize()
+    assert torch.equal(y_full, y_gen)
+    want = oracle_on(ref, x[[0, B - 1]].float().cpu(), causal, "cpu", mask=None if m is None else m[[0, B - 1]].cpu())
+    assert compare_outputs(want, y_full[[0, B - 1]].float().cpu()).passed
