@@ -82,10 +82,10 @@ constexpr int small_groups() {
 // FULL: every lane's token is in range -- S equals the 32 * kSmallWaves token slots of a
 // sequence's waves (a shorter S leaves the last wave's lanes past it, whose rows belong
 // to the next sequence) -- one sequence per workgroup and no residual output, so the
-// stores of a sequence are unconditional.  The compiler then
-// counts them and waits at the next sequence's LN1 only for that sequence's prefetched
-// input; behind a per-lane condition it waits for every store to complete as well
-// (~1 us per sequence at B10000).
+// stores of a sequence are unconditional.  The compiler can
+// then count them: at the next sequence's LN1 it waits for the prefetched input and for
+// the stores whose data registers LN1 reuses, where behind a per-lane condition it
+// waited for every store (~1 us per sequence at B10000).
 template <int D, int HD, bool CAUSAL, bool MASKED, typename TX, int G, bool FULL>
 __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const TX* __restrict__ x, const f16* __restrict__ wqkv,
                                                           const float* __restrict__ bqkv, const f16* __restrict__ wo,
