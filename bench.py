@@ -15,7 +15,9 @@ Also on the same line:
     bytes) per launch / average launch time;
   * ``cpu_baseline``: the fp32 oracle (this repo's restatement of the
     reference PyTorch layer) on the host cores, on a bounded sample;
-  * ``long``: BASELINE config 5, B=32 d=1024 H=16 S=100000 (``--no-long`` skips);
+  * ``long``: BASELINE config 5, B=32 d=1024 H=16 S=100000 (``--no-long`` skips), its
+    input built per sequence from seeds (``synthetic_sequence``), with its own CPU
+    baseline (the query-blocked oracle on one sequence, x32 extrapolated);
   * ``sweep``: every other BASELINE configuration, ms and TFLOP/s per forward;
   * ``model``: the whole ``CobraTransformer`` stack on three of the reference's
     model cases (tools/sweep.py:31-47), causal, fp16;
@@ -65,6 +67,14 @@ def synthetic_input(B, S, D, seed=0):
     """x ~ N(0, 1) from a seeded CPU generator, fp32."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     return torch.randn(B, S, D, generator=g, dtype=torch.float32)
+
+
+def synthetic_sequence(b, S, D, seed=0):
+    """Sequence b of a per-sequence-seeded batch: [S, D] fp32 from a
+    CPU generator seeded (seed << 32) | b, so any one sequence regenerates alone and a
+    checker can rebuild exactly the sequences it samples."""
+    g = torch.Generator(device="cpu").manual_seed((seed << 32) | b)
+    return torch.randn(1, S, D, generator=g, dtype=torch.float32)[0]
 
 
 def make_layer(D, H, dev, graph=None):
@@ -167,6 +177,23 @@ def graph_floor_us(iters=500):
     return event_ms(g.replay, iters) * 1e3
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_info() -> dict:
+    """The host CPU the baselines ran on.  `cores` on the baselines is the thread count
+    torch used (the box's CPU share: OMP_NUM_THREADS), not the machine's core count."""
+    return {"cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+
+
 def cpu_baseline(B, S, D, H, budget_s=10.0):
     """fp32 oracle forward on the host cores; median over a ~budget_s sample."""
     from oracle import make_input, make_sublayer
@@ -184,9 +211,60 @@ def cpu_baseline(B, S, D, H, budget_s=10.0):
             samples.append((time.perf_counter_ns() - t0) / 1e6)
     ms = statistics.median(samples)
     return {"value": layer_flops(B, S, D) / (ms / 1e3) / 1e12, "unit": "TFLOP/s", "cores": threads,
-            "kind": "port", "ms_per_forward": ms,
+            "kind": "port", "ms_per_forward": ms, **host_info(),
             "sample": f"full B{B} S{S} D{D} H{H} batch, fp32 oracle layer (torch CPU, {threads} threads), "
                       f"median of {len(samples)} forwards in ~{budget_s:.0f}s"}
+
+
+def cpu_baseline_long(budget_s=20.0, block_q=2048):
+    """BASELINE config 5 on the host cores: the query-blocked fp32 oracle
+    (tools/reference_chunked.py:73-128 restated) on one full S = 100000 sequence.
+
+    Bounded sample: LN1, the three projections, the out-projection and LN2 run whole
+    on the sequence; of its 16 heads x ceil(S / block_q) attention blocks, as many as
+    fit in ~budget_s are timed (spread over heads and query positions) and their mean
+    is scaled to all blocks.  s/sequence is that sum; the B = 32 forward is x32, which
+    is exact for a batch of independent sequences (TTB:1446-1450).
+    """
+    from oracle import make_sublayer
+
+    B, S, D, H = 32, 100000, 1024, 16
+    threads = torch.get_num_threads()
+    layer = make_sublayer(D, H, seed=0)
+    att = layer.attention
+    x = synthetic_sequence(0, S, D)[None]
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        h = layer.norm1(x)
+        q, k, v = att._heads(att.q_proj(h)), att._heads(att.k_proj(h)), att._heads(att.v_proj(h))
+        t_proj = time.perf_counter() - t0
+        nblk = -(-S // block_q)
+        order = [(hh, (hh * 7 + i * 13) % nblk) for i in range(nblk) for hh in range(H)]
+        times = []
+        t_end = time.perf_counter() + budget_s
+        for hh, blk in order:
+            if times and time.perf_counter() > t_end:
+                break
+            q0 = blk * block_q
+            q1 = min(q0 + block_q, S)
+            t0 = time.perf_counter()
+            att._probs_times_v(q[:, hh:hh + 1, q0:q1], k[:, hh:hh + 1], v[:, hh:hh + 1], q0, None, False, x.dtype)
+            times.append((time.perf_counter() - t0) * (block_q / (q1 - q0)))
+        ctx = torch.randn(1, S, D)
+        t0 = time.perf_counter()
+        layer.norm2(x + att.out_proj(ctx))
+        t_out = time.perf_counter() - t0
+    t_attn = statistics.mean(times) * H * nblk
+    s_seq = t_proj + t_attn + t_out
+    fl = layer_flops(B, S, D)
+    return {"value": fl / (s_seq * B) / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "s_per_sequence": s_seq, "s_per_forward_x32_extrapolated": s_seq * B,
+            "parts_s": {"ln1_qkv": t_proj, "attention_all_blocks": t_attn, "out_proj_ln2": t_out},
+            **host_info(),
+            "sample": f"one S={S} D={D} H={H} sequence (seed (0<<32)|0), fp32 query-blocked oracle "
+                      f"(block_q {block_q}); projections and LayerNorms timed whole, {len(times)} of "
+                      f"{H * nblk} attention blocks timed and scaled; forward = 32 x s/sequence "
+                      f"(labelled extrapolation)"}
 
 
 SWEEP = [  # name, B, S, D, H  (BASELINE configs other than the headline one)
@@ -228,9 +306,9 @@ def bench_long(dev, steps=2, warmup=1):
 
     B, S, D, H = 32, 100000, 1024, 16
     layer = make_layer(D, H, dev)
-    g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    x = torch.randn(B, S, D, device=dev, dtype=torch.float16, generator=g)
+    x = torch.empty(B, S, D, device=dev, dtype=torch.float16)
+    for b in range(B):  # per-sequence seeds: any sequence of the timed input can be rebuilt alone
+        x[b].copy_(synthetic_sequence(b, S, D).half())
     with torch.inference_mode():
         for _ in range(warmup):
             layer(x)
@@ -447,6 +525,8 @@ def main() -> int:
             line["long"] = {"error": f"OOM: {e}"}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(B, S, D, H)
+        if not args.no_long:
+            line["long"]["cpu_baseline"] = cpu_baseline_long()
     print(json.dumps(line), flush=True)
     return 0
 

@@ -138,6 +138,11 @@ def stream_host(x, mask, outs, step: int, run, dev, is_oom, on_oom) -> None:
     while c0 < B:
         if not slots or slots[0]["n"] < step:
             slots = [new_slot(step), new_slot(step)]
+            # The slots were allocated on the compute stream (the allocator may hand
+            # out blocks that work already queued there still uses), and a device
+            # mask may have been produced there just before this call: the copy
+            # stream writes the slots and reads the mask only after all of it.
+            copy.wait_stream(compute)
         i = 0
         try:
             while c0 < B:

@@ -73,3 +73,22 @@ def test_without_a_gpu_bench_exits_with_a_message():
     res = _run_bench("--steps", "1", "--warmup", "0")
     assert res.returncode == 2
     assert "GPU" in res.stderr
+
+
+def test_long_input_sequences_are_the_oracles():
+    """The long leg builds its timed input per sequence; each must be exactly the
+    sequence ``oracle.make_sequence`` regenerates for the same index (shortened S)."""
+    from oracle import make_sequence
+
+    for b in (0, 5, 31):
+        assert torch.equal(bench.synthetic_sequence(b, 300, 64), make_sequence(b, 300, 64)[0])
+
+
+def test_long_cpu_baseline_scales_a_bounded_sample():
+    """The S = 1e5 CPU baseline times a bounded sample and reports a labelled x32
+    extrapolation; run here at a tiny budget (it stops after the first block)."""
+    out = bench.cpu_baseline_long(budget_s=0.0)
+    assert out["kind"] == "port" and out["cores"] == torch.get_num_threads()
+    assert out["s_per_forward_x32_extrapolated"] == pytest.approx(32 * out["s_per_sequence"])
+    assert "1 of 784 attention blocks" in out["sample"]
+    assert out["cpu_model"] and out["os_cpu_count"] == os.cpu_count()

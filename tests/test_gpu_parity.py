@@ -447,8 +447,16 @@ def test_ln_linear_op(d, xdt):
         assert torch.allclose(got.float(), want, atol=4e-3, rtol=4e-3), (d, xdt, M, N, err)
 
 
-@pytest.mark.parametrize("B,S,causal,masked", [(600, 128, False, False), (601, 128, True, True), (777, 96, False, True)])
-def test_persistent_store_variants_agree(B, S, causal, masked):
+@pytest.mark.parametrize(
+    "B,S,D,H,causal,masked",
+    [
+        (600, 128, 128, 4, False, False), (601, 128, 128, 4, True, True), (777, 96, 128, 4, False, True),
+        # the other two instantiations of the S = 128 variant: head_dim 64 and d_model 96
+        (300, 128, 128, 2, False, False), (300, 128, 128, 2, True, True),
+        (5, 128, 96, 3, False, False), (5, 128, 96, 3, True, True),
+    ],
+)
+def test_persistent_store_variants_agree(B, S, D, H, causal, masked):
     """The persistent kernel at S = 128 (every token slot of its four waves in use)
     without a residual output takes a variant with unconditional stores and prefetches
     (past the batch it re-reads the last sequence); asking for the residual selects the
@@ -456,16 +464,16 @@ def test_persistent_store_variants_agree(B, S, causal, masked):
     past S) must take the general variant both ways."""
     from cobra_amd import ops
 
-    assert ops.layer_plan(B, S, 128, 4, masked) == 0
-    ref, mod = build_pair(128, 4, seed=3)
-    x = make_input(B, S, 128, seed=4).half().to(DEV)
+    assert ops.layer_plan(B, S, D, H, masked) == 0
+    ref, mod = build_pair(D, H, seed=3)
+    x = make_input(B, S, D, seed=4).half().to(DEV)
     m = None
     if masked:
         g = torch.Generator().manual_seed(5)
         m = (torch.rand(B, S, generator=g) > 0.25)
         m[:, 0] = True
         m = m.to(DEV)
-    log(f"[persistent variants] B{B} S{S} causal={causal} masked={masked}")
+    log(f"[persistent variants] B{B} S{S} D{D} H{H} causal={causal} masked={masked}")
     with torch.inference_mode():
         y_full = mod(x, valid_token_mask=m, causal=causal)
         r, y_gen = mod(x, valid_token_mask=m, causal=causal, return_residual=True)

@@ -41,6 +41,31 @@ def test_sublayer_host_input_streams(pinned, masked):
     assert compare_outputs(want_r, r).passed
 
 
+def test_host_input_with_mask_just_made_on_the_gpu():
+    """Host x, and a device mask whose producing kernels are still queued on the
+    compute stream when the call starts: the copy stream must read it only after them."""
+    ref, mod = build_pair(128, 4)
+    mod.stream_chunk = 4
+    B, S = 13, 128
+    x = make_input(B, S, 128, seed=21).half()
+    lengths = torch.randint(1, S + 1, (B,), generator=torch.Generator().manual_seed(8))
+    want_m = torch.arange(S)[None, :] < lengths[:, None]
+    with torch.inference_mode():
+        # A long queue ahead of the mask's producer, so a copy that did not wait
+        # for it would read the buffer before it is written.
+        big = torch.randn(4096, 4096, device=DEV)
+        for _ in range(20):
+            big = big @ big * 1e-3
+        m = torch.zeros(B, S, dtype=torch.bool, device=DEV)
+        m |= torch.arange(S, device=DEV)[None, :] < lengths.to(DEV)[:, None]
+        y = mod(x, m)
+        torch.cuda.synchronize()
+    want = oracle_on(ref, x.float(), False, "cpu", mask=want_m)
+    res = compare_outputs(want, y.float())
+    log(f"[stream fresh device mask] max_abs={res.max_abs_error:.3e} failed={res.failed_elements}")
+    assert res.passed, res
+
+
 def test_model_host_input_streams():
     from cobra_amd import CobraTransformer, TransformerConfig
 
