@@ -388,6 +388,40 @@ def layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, wor
             B, S, D, heads, 1 if causal else 0, float(eps), _stream(x)]
 
 
+NOALLOC_MAX_BYTES = _lib.NOALLOC_MAX_BYTES
+
+
+def layer_fwd_noalloc(
+    x: torch.Tensor,
+    w_qkv: torch.Tensor,
+    b_qkv: torch.Tensor,
+    w_o: torch.Tensor,
+    b_o: torch.Tensor,
+    ln1_w: Optional[torch.Tensor],
+    ln1_b: Optional[torch.Tensor],
+    ln2_w: torch.Tensor,
+    ln2_b: torch.Tensor,
+    y: torch.Tensor,
+    heads: int,
+    causal: bool,
+    eps: float = 1e-5,
+    resid_out: Optional[torch.Tensor] = None,
+    valid_mask: Optional[torch.Tensor] = None,
+) -> None:
+    """``layer_fwd`` without a workspace (``cobra_layer_fwd_noalloc``): the library's
+    per-device scratch of ``NOALLOC_MAX_BYTES`` holds the intermediates, so nothing is
+    allocated.  Calls that overlap on one GPU (several streams or threads) race."""
+    B, S, D = x.shape
+    need = layer_workspace_bytes(B, S, D, heads, valid_mask is not None, x.dtype)
+    if need > NOALLOC_MAX_BYTES:
+        raise ValueError(f"B={B} S={S} D={D} H={heads} needs {need} bytes of scratch; the allocation-free "
+                         f"entry point holds {NOALLOC_MAX_BYTES}: use layer_fwd with a workspace")
+    args = layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, x, heads, causal, eps,
+                          resid_out, valid_mask)
+    del args[13:15]  # no workspace pointer / size
+    call("cobra_layer_fwd_noalloc", *args)
+
+
 class LayerLaunch:
     """A bound ``cobra_layer_fwd`` (``cobra_layer_bind``): ``run(x, y, stream)``
     launches with every other argument fixed.  Keeps the buffers it names alive."""

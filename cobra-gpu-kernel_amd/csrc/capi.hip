@@ -2,6 +2,7 @@
 // orchestration of the whole attention sublayer.
 #include "cobra_amd.h"
 
+#include <mutex>
 #include <new>
 
 #include "common.hpp"
@@ -52,6 +53,38 @@ bool layer_shape_ok(int64_t batch, int64_t seq_len, int64_t d, int64_t heads) {
   if (batch < 0 || seq_len < 0 || d <= 0 || heads <= 0 || d % heads != 0) return false;
   const int64_t hd = d / heads;
   return d % 8 == 0 && hd % 8 == 0 && hd <= 256 && d <= cobra::kLnMaxD && seq_len <= 0x7fffffff;
+}
+
+}  // namespace
+
+// The workspace of cobra_layer_fwd_noalloc: one copy per device, in the code
+// object's zero-initialised data, so it costs no file size and no allocation
+// call.  In host code `scratch` names a host-side stand-in, not device memory:
+// kernels get the per-device address that hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[COBRA_NOALLOC_MAX_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (each device holds its own copy).
+hipError_t scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+  });
+  if (g_scratch_err[dev] != hipSuccess) return g_scratch_err[dev];
+  *out = g_scratch_ptr[dev];
+  return *out ? hipSuccess : hipErrorInvalidSymbol;
 }
 
 }  // namespace
@@ -268,5 +301,28 @@ int cobra_layer_run(const cobra_layer_launch* h, const void* x, const uint8_t* v
 }
 
 void cobra_layer_unbind(cobra_layer_launch* h) { delete h; }
+
+int cobra_layer_fwd_noalloc(const void* x, int x_dtype, const uint8_t* valid_mask, const void* w_qkv,
+                            const float* b_qkv, const void* w_o, const float* b_o, const float* ln1_w,
+                            const float* ln1_b, const float* ln2_w, const float* ln2_b, void* y, float* resid_out,
+                            int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
+                            void* stream) {
+  const int64_t need =
+      cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, valid_mask != nullptr, x_dtype);
+  if (need < 0 || need > COBRA_NOALLOC_MAX_BYTES) return kBad;
+  void* ws = nullptr;
+  if (need > 0) {
+    int cur = -1, sdev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return code(e);
+    if (stream) {
+      if ((e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev)) != hipSuccess) return code(e);
+      if (sdev != cur) return kBad;
+    }
+    if ((e = scratch_of_current_device(&ws)) != hipSuccess) return code(e);
+  }
+  return cobra_layer_fwd(x, x_dtype, valid_mask, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, resid_out,
+                         ws, need, batch, seq_len, d_model, heads, causal, eps, stream);
+}
 
 }  // extern "C"

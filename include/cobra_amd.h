@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 5
+#define COBRA_ABI_VERSION 6
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
 
@@ -200,6 +200,36 @@ cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv,
 int cobra_layer_run(const cobra_layer_launch* h, const void* x, const uint8_t* valid_mask, void* y, float* resid_out,
                     void* stream);
 void cobra_layer_unbind(cobra_layer_launch* h);
+
+/*
+ * Size of the device scratch that cobra_layer_fwd_noalloc uses in place of a
+ * workspace: 128 MiB, one copy per GPU the library runs on, held until the
+ * process ends.
+ */
+#define COBRA_NOALLOC_MAX_BYTES (128ll << 20)
+
+/*
+ * cobra_layer_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * Same arguments, plans and results as cobra_layer_fwd (bit for bit); the
+ * STAGED plan's intermediates go to a file-scope device array of
+ * COBRA_NOALLOC_MAX_BYTES instead of a caller-provided workspace.  Nothing is
+ * allocated or freed, here or in any callee.
+ *   - Shapes whose cobra_layer_workspace_bytes() exceeds COBRA_NOALLOC_MAX_BYTES
+ *     are rejected with hipErrorInvalidValue before anything is enqueued (at
+ *     d_model 128, S 1024 up to 128 sequences fit, 127 with a token mask; at
+ *     d_model 1024, S 128 up to 85).  The FUSED plan needs no scratch at all.
+ *   - `stream` must belong to the current device (the array is per device).
+ *   - Every call on one GPU shares that GPU's array, and nothing in it
+ *     outlives a call: calls that overlap on one GPU (two streams, two host
+ *     threads) race.  Calls on one stream are ordered and safe.
+ */
+int cobra_layer_fwd_noalloc(const void* x, int x_dtype, const uint8_t* valid_mask, const void* w_qkv,
+                            const float* b_qkv, const void* w_o, const float* b_o, const float* ln1_w,
+                            const float* ln1_b, const float* ln2_w, const float* ln2_b, void* y, float* resid_out,
+                            int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
+                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -294,3 +294,16 @@ def test_oracle_and_product_share_parameter_names():
     a = dict(OracleAttentionSublayer(64, 2).named_parameters())
     b = dict(CobraAttentionSublayer(64, 2).named_parameters())
     assert {k: v.shape for k, v in a.items()} == {k: v.shape for k, v in b.items()}
+
+
+def test_noalloc_scratch_size_matches_the_header():
+    """The Python wrapper's size check uses the header's COBRA_NOALLOC_MAX_BYTES."""
+    from cobra_amd import _lib, ops
+
+    m = re.search(r"#define COBRA_NOALLOC_MAX_BYTES \((\d+)ll << (\d+)\)", open(HEADER).read())
+    assert m, "COBRA_NOALLOC_MAX_BYTES not found"
+    assert _lib.NOALLOC_MAX_BYTES == ops.NOALLOC_MAX_BYTES == int(m.group(1)) << int(m.group(2))
+    lib = _lib.lib()
+    # rejected on the host, before any device call: a shape beyond the scratch
+    assert lib.cobra_layer_fwd_noalloc(256, _lib.F16, None, 256, 256, 256, 256, None, None, 256, 256, 256, None,
+                                       200, 1024, 128, 4, 0, 1e-5, None) != 0
