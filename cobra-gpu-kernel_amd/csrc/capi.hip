@@ -247,11 +247,11 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     out.epi = masked ? cobra::kEpiMaskBranch : 0;
     return code(cobra::run_gemm(out));
   }
-  // r goes to memory between the projection and LayerNorm.  It is kept in fp32 when
-  // the caller asks for it (resid_out) or the activations are fp32; otherwise it is
-  // rounded to fp16, where the reference's fp16 `x + attn_out` (TTB:141) rounds it,
-  // which halves its write and read.
-  const int r_dtype = resid_out || x_dtype == kF32 ? kF32 : kF16;
+  // r goes to memory between the projection and LayerNorm in fp32, as the reference's
+  // fused path stores it (TTB:1274-1283): rounded to fp16 it would carry an error of
+  // half an fp16 step of |r| into LN2, amplified by 1/std (visible for inputs whose
+  // mean is large against their spread).
+  const int r_dtype = kF32;
   void* r = resid_out ? static_cast<void*>(resid_out) : static_cast<void*>(ws + lb.r_off);
   cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, r, r_dtype, T, (int)D, (int)D,
                       nullptr, nullptr, nullptr, kF16, eps, s};

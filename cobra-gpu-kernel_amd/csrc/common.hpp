@@ -33,6 +33,27 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const f16x8& a, const f16x8& b, c
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// a - b on both fp16 halves as one v_pk_add_f16 (with the second operand
+// negated): the compiler lowers fp16 vector arithmetic to one instruction per
+// half on this target.
+__device__ __forceinline__ f16x2 pk_sub_f16(f16x2 a, f16x2 b) {
+  f16x2 r;
+  asm("v_pk_add_f16 %0, %1, %2 neg_lo:[0,1] neg_hi:[0,1]" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// (x - hi) - lo elementwise, in packed fp16 (two roundings, each relative to the result).
+__device__ __forceinline__ f16x8 sub2_f16(const f16x8& x, _Float16 hi, _Float16 lo) {
+  struct Pairs {
+    f16x2 p[4];
+  };
+  const f16x2 h2 = {hi, hi}, l2 = {lo, lo};
+  Pairs q = __builtin_bit_cast(Pairs, x);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q.p[i] = pk_sub_f16(pk_sub_f16(q.p[i], h2), l2);
+  return __builtin_bit_cast(f16x8, q);
+}
+
 __device__ __forceinline__ f16x8 zero8() {
   f16x8 z;
 #pragma unroll

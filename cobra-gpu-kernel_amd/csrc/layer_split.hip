@@ -13,8 +13,10 @@
 // sequence and walks the heads one after another; here the S/32 workgroups of a
 // sequence run side by side, and inside a workgroup the waves split every
 // phase four ways:
-//   1. wave w normalises tokens 32w .. 32w+31 (LN1) while the W_k / W_v rows
-//      of d-tile w and the W_q rows of head w arrive;
+//   1. wave w normalises tokens 32w .. 32w+31 (LN1, mean and variance in one
+//      pass) while the W_k / W_v rows of d-tile w and the W_q rows of head w
+//      arrive; the wave whose tile holds the slice's own queries keeps a raw
+//      copy of it, the residual;
 //   2. wave w projects K^T and V of d-tile w for ALL tokens (every workgroup
 //      of the sequence recomputes them: twice the projection FLOPs of the
 //      persistent kernel, but no cross-workgroup traffic at all), and Q^T of
@@ -28,7 +30,7 @@
 //      heads: the other head's half of the K fragment is zeroed);
 //   4. wave n multiplies the gathered attention output by the W_o rows of
 //      output columns 32n .. 32n+31, adds bias and residual, and LN2 combines
-//      the per-wave row sums through LDS.
+//      the per-wave row sums and sums of squares through LDS in one exchange.
 //
 // Every global read is an LDS-DMA (global_load_lds_dwordx4) of whole 1 KB
 // spans: matrix rows land row-major in LDS with 16-byte chunks XOR-swizzled by
@@ -75,15 +77,15 @@ struct SplitPlan {
   static constexpr int X = kSplitWaves * TILEB;        // token tiles, then LN1 output fragments
   static constexpr int Q = D * ROWB;                   // W_q rows, then W_o rows
   static constexpr int CX = KD * 1024;                 // attention output fragments
-  static constexpr int RB = 32 * 64;                   // residual block of one wave (32 x 32 fp16)
-  static constexpr int PB = 2048;                      // parameter rows of one wave
+  static constexpr int RAWB = KD * 1024;               // raw fragments of the slice's token tile (the residual)
+  static constexpr int PB = 2048;                      // parameter rows of one wave, then [gamma1 | beta1]
   static constexpr int OFF_X = A, OFF_Q = OFF_X + X, OFF_CX = OFF_Q + Q, OFF_R = OFF_CX + CX;
-  static constexpr int OFF_P = OFF_R + kSplitWaves * RB, OFF_STAT = OFF_P + kSplitWaves * PB;
+  static constexpr int OFF_P = OFF_R + RAWB, OFF_STAT = OFF_P + kSplitWaves * PB;
   static constexpr int BYTES = OFF_STAT + 2 * kSplitWaves * 32 * 4;
-  // DMA instructions of one wave, in issue order: [gamma1|beta1] 1, token tile N_X,
-  // other parameters 1, W_k/W_v N_A, W_q N_Q, residual N_R; W_o N_O after barrier 1.
+  // DMA instructions of one wave, in issue order: [gamma1|beta1] 1 (affine LN1 only),
+  // token tile N_X, other parameters 1, W_k/W_v N_A, W_q N_Q; W_o N_O after barrier 1.
   static constexpr int N_X = TILEB / 1024, N_A = 2 * TILEB / 1024, N_Q = NQT * TILEB / 1024;
-  static constexpr int N_R = RB / 1024, N_O = TILEB / 1024;
+  static constexpr int N_O = TILEB / 1024;
   static_assert(D == 64 || D == 128, "swizzle and row geometry");
   static_assert((HD == 8 || HD == 32 || HD == 64 || HD == 128) && D % HD == 0, "head geometry");
   static_assert(!QSPLIT || (H == 1 && NDT == kSplitWaves), "a split head has one d / key tile per wave");
@@ -92,7 +94,7 @@ struct SplitPlan {
   static_assert(KD * 1024 == TILEB, "LN1 output fragments of a tile fill its input tile");
   static_assert(!QSPLIT || KSH * 1024 == CX, "the split head's Q^T fragments fit the attention-output area");
   static_assert(2 * D * 4 <= 1024 && 2 * 32 + NQT * 32 + 3 * 32 <= 256, "parameter rows");
-  static_assert(1 + N_X + 1 + N_A + N_Q + N_R < 64, "vmcnt range");
+  static_assert(1 + N_X + 1 + N_A + N_Q < 64, "vmcnt range");
   static_assert(BYTES <= kLdsBytes, "LDS budget");
 };
 
@@ -168,6 +170,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   f16x8* const Cx = reinterpret_cast<f16x8*>(smem + P::OFF_CX);
   f16x8* const Qx = Cx;  // split head: Q^T fragments of the slice, read before any Cx store
   f16x8* const Px = Hb;  // split head: probability fragments, once every projection has read Hb
+  f16x8* const Raw = reinterpret_cast<f16x8*>(smem + P::OFF_R);  // x rows of the slice, unnormalised
   float* const Stat = reinterpret_cast<float*>(smem + P::OFF_STAT);
 
   // The S/32 slices of a sequence run on one XCD, so its L2 serves the token
@@ -184,8 +187,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   // Waves past the last d-tile / head issue the same transfers for tile / head 0
   // (identical bytes to the same place), so every wave's wait counts are equal.
   const int dq = w < NNT ? w : 0, hq = w < H ? w : 0;
-  char* const rP = smem + P::OFF_P + w * P::PB;  // [gamma1 | beta1], then the other parameters
-  char* const rR = smem + P::OFF_R + w * P::RB;  // residual block of this wave
+  char* const rP = smem + P::OFF_P + w * P::PB;  // the 32-float parameter segments, then [gamma1 | beta1]
   char* const rWkv = rA + dq * 2 * P::TILEB;
   // W_q rows this wave projects: d-tile dq of the split head, else all of head hq.
   const int qrow0 = P::QBYTILE ? 32 * dq : HD * hq;
@@ -205,7 +207,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   const bool aff1 = g1 != nullptr;  // LN1 with elementwise affine
   if (aff1) {  // [gamma1 | beta1] (later vmcnt waits count only what follows the token tile)
     const int c = 4 * lane;
-    dma16(c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0), rP);
+    dma16(c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0), rP + 1024);
   }
   // Token tile w.  Rows past S fetch row 0 (S >= 1): finite values whose keys the
   // softmax masks and whose queries are never stored.
@@ -223,104 +225,129 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
                        : seg == 5 ? g2 + 32 * dq + off
                        : seg == 6 ? be2 + 32 * dq + off
                                   : bo + off;
-    dma16(src, rP + 1024);
+    dma16(src, rP);
   }
-  // W_k rows 32dq .. 32dq+31, then the W_v rows.
+  // W_k rows 32dq .. 32dq+31, in flight while the token tile is still on its way.
   const char* const wbytes = reinterpret_cast<const char*>(wqkv);
   dma_span_rows<D, P::N_A / 2>(rWkv, wbytes + (int64_t)(D + 32 * dq) * 2 * D, spans);
-  dma_span_rows<D, P::N_A / 2>(rWkv + P::TILEB, wbytes + (int64_t)(2 * D + 32 * dq) * 2 * D, spans);
-  // The W_q rows and the residual block are issued from inside LN1 (below), so the
-  // arithmetic of LN1 overlaps the transfers the CU's load path is still working
-  // through instead of waiting behind them.
-  auto issue_late = [&]() {
-    // W_q rows qrow0 .. qrow0 + 32 NQT - 1.
-    dma_span_rows<D, P::N_Q>(rWq, wbytes + (int64_t)qrow0 * 2 * D, spans);
-    // Residual block: queries 32s .. 32s+31, columns 32dq .. 32dq+31, as [32 rows][4
-    // chunks] with chunk c of row r at c ^ ((r >> 2) & 3).  Span i covers rows
-    // 16i + lane / 4, whose swizzle (lane / 16) & 3 does not depend on i.
-    const uint32_t roff = (uint32_t)((lane >> 2) * 2 * D + 16 * ((lane & 3) ^ ((lane >> 4) & 3)));
-    if (32 * s + 32 <= S) {
-      const char* base = reinterpret_cast<const char*>(xs + (int64_t)32 * s * D + 32 * dq);
+  // The W_v rows and the W_q rows qrow0 .. qrow0 + 32 NQT - 1 are issued from inside
+  // LN1, a span or two between its arithmetic steps.  The CU's load path drains about
+  // one 1 KB transfer per 16 cycles; a wave that issues more than the queue holds
+  // stalls at the issue, so transfers issued in one run ahead of LN1 would hold LN1
+  // back until the load path had worked through them all.  (Issuing W_k from inside
+  // LN1 as well lets the token tile land ~300 cycles sooner but stretches LN1 more.)
+  constexpr int NV = P::N_A / 2, NLATE = NV + P::N_Q, NSLOT = 2 * KD;
+  constexpr int PER_SLOT = (NLATE + NSLOT - 1) / NSLOT;
+  const char* const wvsrc = wbytes + (int64_t)(2 * D + 32 * dq) * 2 * D;
+  const char* const wqsrc = wbytes + (int64_t)qrow0 * 2 * D;
+  auto issue_late = [&](int slot) {  // slot < NSLOT; spans PER_SLOT * slot ..
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < P::N_R; ++i) dma16(base + 16 * 2 * D * i + roff, rR + 1024 * i);
-    } else {
-#pragma unroll
-      for (int i = 0; i < P::N_R; ++i) {
-        const int r = 16 * i + (lane >> 2);
-        const int qr = 32 * s + r < S ? 32 * s + r : 0;
-        dma16(reinterpret_cast<const char*>(xs + (int64_t)qr * D + 32 * dq) + (roff - (lane >> 2) * 2 * D),
-              rR + 1024 * i);
-      }
+    for (int j = PER_SLOT * slot; j < PER_SLOT * (slot + 1) && j < NLATE; ++j) {
+      if (j < NV)
+        dma16(wvsrc + 1024 * j + spans.off[j % RowSpans<D>::NP], rWkv + P::TILEB + 1024 * j);
+      else
+        dma16(wqsrc + 1024 * (j - NV) + spans.off[(j - NV) % RowSpans<D>::NP], rWq + 1024 * (j - NV));
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // ---- LN1 of token 32w + li (columns 16kk + 8g + e): its tile and parameters are in.
-  wait_vmcnt<1 + P::N_A>();
+  // ---- LN1 of token 32w + li (columns 16kk + 8g + e): its tile is in. ------------------
+  wait_vmcnt<1 + NV>();
   KeyBits kbits{~0ull, ~0ull};
   if constexpr (MASKED) kbits = key_bits_of(kbytes, S, lane);
   {
-    // Row sum by fp16 pair dot products with (1, 1) (exact products, fp32
-    // accumulation), in four independent chains; then the centred values in fp32.
     f16x8 xc[KD];
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) xc[kk] = tile_chunk<D>(rTok, li, 2 * kk + g);
+    // The residual rows of the slice, before the tile is overwritten.
+    if (w == s) {
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) Raw[kk * 64 + lane] = xc[kk];
+    }
     const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
-    float part[4] = {0.f, 0.f, 0.f, 0.f};
+    if (!aff1) {
+      // One pass over the tile: row sum and sum of squares by fp16 pair dot products
+      // (exact products, fp32 accumulation, independent chains), variance
+      // E[x^2] - mean^2; then h = x rstd - mean rstd, a mixed-precision fma per element
+      // (fp16 x, fp32 arithmetic) and one rounding to fp16.
+      float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < KD; ++kk)
+      for (int kk = 0; kk < KD; ++kk) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        part[e] = __builtin_amdgcn_fdot2(f16x2{xc[kk][2 * e], xc[kk][2 * e + 1]}, one2, part[e], false);
-    const float mean = sum_xor32((part[0] + part[1]) + (part[2] + part[3])) * (1.0f / D);
-    issue_late();
-    // gamma1 / beta1 of this lane's columns, all requested before the arithmetic
-    // below so one wait covers them.
-    const float* pg = reinterpret_cast<const float*>(rP);
-    float gv[KD][8], bv[KD][8];
-    if (aff1) {
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 pr = {xc[kk][2 * e], xc[kk][2 * e + 1]};
+          s1[e & 1] = __builtin_amdgcn_fdot2(pr, one2, s1[e & 1], false);
+          s2[e & 1] = __builtin_amdgcn_fdot2(pr, pr, s2[e & 1], false);
+        }
+        issue_late(kk);
+      }
+      const float mean = sum_xor32(s1[0] + s1[1]) * (1.0f / D);
+      const float ex2 = sum_xor32(s2[0] + s2[1]) * (1.0f / D);
+      const float rstd = rsqrtf(fmaxf(ex2 - mean * mean, 0.f) + eps);
+      const float nmr = -mean * rstd;
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) {
+        f16x8 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = (f16)fmaf((float)xc[kk][e], rstd, nmr);
+        Hb[(w * KD + kk) * 64 + lane] = h;
+        issue_late(KD + kk);
+      }
+    } else {
+#pragma unroll
+      for (int slot = 0; slot < NSLOT; ++slot) issue_late(slot);
+      float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          part[e] = __builtin_amdgcn_fdot2(f16x2{xc[kk][2 * e], xc[kk][2 * e + 1]}, one2, part[e], false);
+      const float mean = sum_xor32((part[0] + part[1]) + (part[2] + part[3])) * (1.0f / D);
+      const float* pg = reinterpret_cast<const float*>(rP + 1024);
+      float gv[KD][8], bv[KD][8];
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
         load8(pg + 16 * kk + 8 * g, gv[kk]);
         load8(pg + D + 16 * kk + 8 * g, bv[kk]);
       }
-    }
-    float xv[KD][8];
-    float qp[2] = {0.f, 0.f};
+      float xv[KD][8];
+      float qp[2] = {0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < KD; ++kk)
+      for (int kk = 0; kk < KD; ++kk)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xv[kk][e] = (float)xc[kk][e] - mean;
-        qp[e & 1] = fmaf(xv[kk][e], xv[kk][e], qp[e & 1]);
+        for (int e = 0; e < 8; ++e) {
+          xv[kk][e] = (float)xc[kk][e] - mean;
+          qp[e & 1] = fmaf(xv[kk][e], xv[kk][e], qp[e & 1]);
+        }
+      const float r1 = rsqrtf(sum_xor32(qp[0] + qp[1]) * (1.0f / D) + eps);
+#pragma unroll
+      for (int kk = 0; kk < KD; ++kk) {
+        f16x8 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = (f16)fmaf(xv[kk][e] * r1, gv[kk][e], bv[kk][e]);
+        Hb[(w * KD + kk) * 64 + lane] = h;
       }
-    const float rstd = rsqrtf(sum_xor32(qp[0] + qp[1]) * (1.0f / D) + eps);
-    // The output fragments overwrite the token tile in place: every read of it above
-    // feeds the mean, so all of them precede the first write.
-#pragma unroll
-    for (int kk = 0; kk < KD; ++kk) {
-      f16x8 h;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        h[e] = (f16)(aff1 ? fmaf(xv[kk][e] * rstd, gv[kk][e], bv[kk][e]) : xv[kk][e] * rstd);
-      Hb[(w * KD + kk) * 64 + lane] = h;
     }
+    // (The fragments overwrite the token tile in place: every read of it above
+    // precedes the first write.)
   }
 
   // ---- operand fragments of this wave's weights -------------------------------------------
-  wait_vmcnt<P::N_Q + P::N_R>();
+  wait_vmcnt<P::N_Q>();
   f16x8 wk[KD], wv[KD];  // A operand of K^T = W_k h^T; B operand of V = h W_v^T
 #pragma unroll
   for (int kk = 0; kk < KD; ++kk) {
     wk[kk] = tile_chunk<D>(rWkv, li, 2 * kk + g);
     wv[kk] = tile_chunk<D>(rWkv + P::TILEB, li, 2 * kk + g);
   }
-  wait_vmcnt<P::N_R>();
+  wait_vmcnt<0>();
   f16x8 wq[NQT][KD];  // A operand of Q^T = W_q h^T
 #pragma unroll
   for (int dt = 0; dt < NQT; ++dt)
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) wq[dt][kk] = tile_chunk<D>(rWq, 32 * dt + li, 2 * kk + g);
-  const float* pp = reinterpret_cast<const float*>(rP + 1024);  // the 32-float segments above
+  const float* pp = reinterpret_cast<const float*>(rP);  // the 32-float segments above
   lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
 
   // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.  A
@@ -359,9 +386,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     // The h fragments of tile t + 1 are requested before the products of tile t,
     // so the LDS latency hides behind 2 KD matrix instructions.
     f16x8 hf[2][KD];
-    auto fetch = [&](int t) {
+    auto fetch = [&](int t, int buf) {
 #pragma unroll
-      for (int kk = 0; kk < KD; ++kk) hf[t & 1][kk] = Hb[(t * KD + kk) * 64 + lane];
+      for (int kk = 0; kk < KD; ++kk) hf[buf][kk] = Hb[(t * KD + kk) * 64 + lane];
     };
     // Tile t - 1 is converted and stored a quarter at a time between the products of
     // tile t, each quarter pinned after two products (scheduling barriers): the wave
@@ -369,36 +396,41 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     // would leave the matrix cores idle while they execute.
     auto store_part = [&](int t, int c) {  // c: K half 0, K half 1, V half 0, V half 1
       const int half = c & 1;
+      const f16x8 o = acc_f16(c < 2 ? ka[t & 1] : va[t & 1], half);
       if constexpr (P::NARROW) {
         if (c < 2)
-          Kl[(t * KD + 2 * w + half) * 64 + lane] = acc_f16(ka[t & 1], half);
+          Kl[(t * KD + 2 * w + half) * 64 + lane] = o;
         else
-          Vl[((t * NNT + w) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
+          Vl[((t * NNT + w) * 2 + half) * 64 + lane] = o;
       } else {
         if (c < 2)
-          Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = acc_f16(ka[t & 1], half);
+          Kl[((h * kSplitTiles + t) * KSH + 2 * t2 + half) * 64 + lane] = o;
         else
-          Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = acc_f16(va[t & 1], half);
+          Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = o;
       }
     };
     auto products = [&](int t) {
-      if (t + 1 < kSplitTiles) fetch(t + 1);
       if (t >= 1) issue_wo(t);
-      // Keep the requests here: left alone, the scheduler sinks each read next to
-      // its use and the wave then waits out the LDS latency every two products.
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
         const f16x8 hb = hf[t & 1][kk];
         ka[t & 1] = mfma32x32x16(wk[kk], hb, kk == 0 ? bk : ka[t & 1]);
         va[t & 1] = mfma32x32x16(hb, wv[kk], kk == 0 ? bv : va[t & 1]);
+        // The next tile's fragments (after the last tile: those of the slice, for
+        // Q^T) are requested behind this tile's first two products, never ahead of
+        // them.  The first wait for LDS data after an LDS-DMA issue (issue_wo) is
+        // compiled as lgkmcnt(0), i.e. it would also wait for requests just made.
+        if (kk == 0) {
+          __builtin_amdgcn_sched_barrier(0);
+          fetch(t + 1 < kSplitTiles ? t + 1 : s, (t + 1) & 1);
+        }
         if (t >= 1)
 #pragma unroll
           for (int c = kk * 4 / KD; c < (kk + 1) * 4 / KD; ++c) store_part(t - 1, c);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    fetch(0);
+    fetch(0, 0);
 #pragma unroll
     for (int t = 0; t < kSplitTiles; ++t) products(t);
     // Q^T of the slice for head w (waves past the last head have none), or d-tile w
@@ -415,7 +447,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         }
 #pragma unroll
         for (int kk = 0; kk < KD; ++kk) {
-          qa = mfma32x32x16(wq[dt][kk], Hb[(s * KD + kk) * 64 + lane], qa);
+          qa = mfma32x32x16(wq[dt][kk], hf[kSplitTiles & 1][kk], qa);
           if (dt == 0)
 #pragma unroll
             for (int c = kk * 4 / KD; c < (kk + 1) * 4 / KD; ++c) store_part(kSplitTiles - 1, c);
@@ -622,62 +654,60 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int half = 0; half < 2; ++half) Cx[(h * KSH + 2 * dt + half) * 64 + lane] = scaled_f16(ot[dt], half, inv);
   }
-  wait_vmcnt<0>();  // W_o rows and the residual block
+  wait_vmcnt<0>();  // W_o rows (this wave's own transfers: readable without a barrier)
+  // Row li of the W_o tile at the k order of the attention output: columns
+  // 16ks + 4g + {0..3} (chunk 2ks) and 16ks + 8 + 4g + {0..3} (chunk 2ks + 1).
+  f16x8 wof[KD];
+#pragma unroll
+  for (int ks = 0; ks < KD; ++ks) {
+    const char* row = rWo + li * 2 * D + 8 * g;
+    const f16x4 lo = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks) ^ row_swz<D>(li)));
+    const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks + 1) ^ row_swz<D>(li)));
+    wof[ks] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
   lds_barrier();    // attention output of every head is in LDS
 
   // ---- out^T tile w = W_o[32w..32w+31] ctx^T, + b_o + x, then LN2 ----------------------
   float v[4][4];  // query qtok, column 32w + 8qd + 4g + e
-  float sum = 0.f;
+  float sum = 0.f, sq = 0.f;
   if (w < NNT) {
     f32x16 oacc = zero16();
 #pragma unroll
-    for (int ks = 0; ks < KD; ++ks) {
-      // Row li of the W_o tile at the k order of the attention output: columns
-      // 16ks + 4g + {0..3} (chunk 2ks) and 16ks + 8 + 4g + {0..3} (chunk 2ks + 1).
-      const char* row = rWo + li * 2 * D + 8 * g;
-      const f16x4 lo = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks) ^ row_swz<D>(li)));
-      const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks + 1) ^ row_swz<D>(li)));
-      const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      oacc = mfma32x32x16(a, Cx[ks * 64 + lane], oacc);
-    }
+    for (int ks = 0; ks < KD; ++ks) oacc = mfma32x32x16(wof[ks], Cx[ks * 64 + lane], oacc);
     // A padded query's attention output is zero (masked_fill before the residual add).
     const bool qv = !MASKED || kbits.valid(qtok);
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
       const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 128 + 8 * qd + 4 * g);
-      const f16x4 xr = *reinterpret_cast<const f16x4*>(rR + li * 64 + 16 * (qd ^ ((li >> 2) & 3)) + 8 * g);
+      // x[qtok][32w + 8qd + 4g + e]: k-step 2w + qd/2, fragment half qd % 2, elements 4g + e.
+      const f16x4 xr = *reinterpret_cast<const f16x4*>(
+          reinterpret_cast<const char*>(Raw + (2 * w + (qd >> 1)) * 64 + li + 32 * (qd & 1)) + 8 * g);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[qd][e] = (qv ? oacc[4 * qd + e] + bb[e] : 0.f) + (float)xr[e];
         sum += v[qd][e];
+        sq = fmaf(v[qd][e], v[qd][e], sq);
       }
     }
+    // LN2 statistics in one exchange: each wave's row sums and sums of squares over
+    // its 32 columns; variance E[r^2] - mean^2.
     sum = sum_xor32(sum);
-    if (g == 0) Stat[w * 32 + li] = sum;
-  }
-  lds_barrier();
-  float mean = 0.f;
-#pragma unroll
-  for (int n = 0; n < NNT; ++n) mean += Stat[n * 32 + li];
-  mean *= 1.0f / D;
-  if (w < NNT) {
-    float q = 0.f;
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float t = v[qd][e] - mean;
-        q += t * t;
-      }
-    q = sum_xor32(q);
-    if (g == 0) Stat[(kSplitWaves + w) * 32 + li] = q;
+    sq = sum_xor32(sq);
+    if (g == 0) {
+      Stat[w * 32 + li] = sum;
+      Stat[(kSplitWaves + w) * 32 + li] = sq;
+    }
   }
   lds_barrier();
   if (w < NNT) {
-    float var = 0.f;
+    float tot = 0.f, tsq = 0.f;
 #pragma unroll
-    for (int n = 0; n < NNT; ++n) var += Stat[(kSplitWaves + n) * 32 + li];
-    const float rstd = rsqrtf(var * (1.0f / D) + eps);
+    for (int n = 0; n < NNT; ++n) {
+      tot += Stat[n * 32 + li];
+      tsq += Stat[(kSplitWaves + n) * 32 + li];
+    }
+    const float mean = tot * (1.0f / D);
+    const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - mean * mean, 0.f) + eps);
     if (q_ok) {
       const int64_t row = (int64_t)b * S + qtok;
 #pragma unroll

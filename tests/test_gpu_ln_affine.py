@@ -73,9 +73,13 @@ def test_random_layernorm_parameters_match_oracle(B, S, D, H, causal, masked, dt
 def test_null_ln1_affine_equals_unit_affine(B, S, D, H, causal, masked, dtype, plan, rows):
     """cobra_layer_fwd with ln1_w = ln1_b = NULL (LayerNorm without affine) on the
     folded weights computes the reference sublayer, as does the same call with
-    weight 1 / bias 0; the two differ only where the normalised value is rounded
-    (the compiler may round (x - mean) * rstd to fp16 in one step where weight /
-    bias go through an fp32 multiply-add first), i.e. in few elements."""
+    weight 1 / bias 0.  Outside the query-split kernel the two differ only where the
+    normalised value is rounded (the compiler may round (x - mean) * rstd to fp16 in
+    one step where weight / bias go through an fp32 multiply-add first), i.e. in few
+    elements.  The query-split kernel computes the two forms differently (without
+    affine: one pass for mean and variance, x rstd - mean rstd; with it: centred
+    variance, ((x - mean) rstd) gamma + beta), so there the outputs may differ by
+    rounding anywhere, within a few fp16 steps of each other."""
     from cobra_amd import ops
 
     ref, mod = _pair(D, H, dtype=dtype)
@@ -105,5 +109,35 @@ def test_null_ln1_affine_equals_unit_affine(B, S, D, H, causal, masked, dtype, p
         res = compare_outputs(want, y[sel])
         assert res.passed, res
     frac = (outs[0] != outs[1]).float().mean().item()
-    log(f"[null ln1] plan={plan} null vs unit affine: differing fraction {frac:.2e}")
-    assert frac < 1e-3
+    diff = (outs[0] - outs[1]).abs().max().item()
+    log(f"[null ln1] plan={plan} null vs unit affine: differing fraction {frac:.2e}, max |diff| {diff:.2e}")
+    query_split = dtype == torch.float16 and D in (64, 128) and S <= 128 and B * ((S + 31) // 32) <= 512
+    if query_split:
+        assert diff <= 8e-3
+    else:
+        assert frac < 1e-3
+
+
+@pytest.mark.parametrize("B,S,D,H,causal,masked,dtype,plan,rows", CASES,
+                         ids=[f"B{c[0]}-S{c[1]}-D{c[2]}-H{c[3]}-{'c' if c[4] else 'n'}{'m' if c[5] else ''}-"
+                              f"{'f32' if c[6] == torch.float32 else 'f16'}" for c in CASES])
+def test_large_mean_input(B, S, D, H, causal, masked, dtype, plan, rows):
+    """x = 3 + 0.5 N(0, 1): LN1's mean is six standard deviations off zero.  The
+    query-split kernel takes the mean off in fp16 (as a high and a low part) and its
+    variance is E[x^2] - mean^2, so a large mean is where a shortcut in either would
+    show; every plan must still pass the gate against the oracle."""
+    ref, mod = _pair(D, H, dtype=dtype, seed=2)
+    x = 3.0 + 0.5 * make_input(B, S, D, seed=7)
+    if dtype == torch.float16:
+        x = x.half()
+    m = _mask(B, S, 11) if masked else None
+    log(f"[large mean] B{B} S{S} D{D} H{H} causal={causal} masked={masked} {dtype}")
+    with torch.inference_mode():
+        y = mod(x.to(DEV), valid_token_mask=None if m is None else m.to(DEV), causal=causal)
+        torch.cuda.synchronize()
+    sel = list(range(B)) if rows is None else rows
+    want = oracle_on(ref, x[sel].float(), causal, "cpu", mask=None if m is None else m[sel])
+    res = compare_outputs(want, y.float().cpu()[sel])
+    log(f"[large mean] plan={plan} max_abs={res.max_abs_error:.3e} max_rel={res.max_relative_error:.3e} "
+        f"failed={res.failed_elements}")
+    assert res.passed, res
