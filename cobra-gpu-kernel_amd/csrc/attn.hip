@@ -435,6 +435,185 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   }
 }
 
+// Wide heads over short sequences (head_dim 128 / 256, S <= 128): one workgroup
+// per (sequence, head), four waves of 32 queries, every key present at once, so
+// the softmax is exact in one pass (no running max, no rescale, no per-block
+// barrier).  LDS holds K [128][HD] and, in turn, the Q tile and then V [128][HD]
+// (64 KB each at head_dim 256): V streams in while the scores and the softmax
+// run.  Same fragment conventions as attn_fwd_kernel: S^T = K . Q^T with Q
+// pre-scaled by scale * log2(e), O^T = V^T . P^T with V^T read by
+// ds_read_b64_tr_b16.  Rows past S fetch row S-1 (finite; their keys are masked
+// and their queries never stored).
+template <int HD, bool CAUSAL, bool MASKED>
+__global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__ qkv, f16* __restrict__ ctx, int S,
+                                                         int H, float c2, const uint64_t* __restrict__ key_bits,
+                                                         int nwords) {
+  constexpr int NW = 4, BM = 128;
+  constexpr int KS = HD / 16, ND = HD / 32, CPR = HD / 8;
+  constexpr int TB = BM * HD * 2;   // one [128][HD] tile
+  constexpr int NI = TB / 1024;     // 1 KB spans per tile
+  constexpr int LPT = NI / NW;      // spans per wave per tile
+  static_assert(HD == 128 || HD == 256, "wide heads");
+  static_assert(LPT >= 1 && LPT < 32, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * TB];
+  char* const ktile = smem;
+  char* const qvtile = smem + TB;  // Q, then V
+
+  const int bh = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = bh % H;
+  const int64_t b = bh / H;
+  const int D = H * HD;
+  const int64_t ld = 3 * (int64_t)D;
+  const f16* qbase = qkv + b * S * ld + h * HD;
+  const f16* kbase = qbase + D;
+  const f16* vbase = qbase + 2 * D;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5, li = lane & 31;
+  const int qi = w * 32 + li;  // this lane's query
+
+  auto dma_tile = [&](char* tile, int sp, const f16* base) {
+    const int o = sp * 1024 + 16 * lane;
+    const int row = o / (2 * HD), pos = (o % (2 * HD)) / 16;
+    const int r = min(row, S - 1);
+    dma16(base + (int64_t)r * ld + 8 * (pos ^ swz<HD>(row)), tile + sp * 1024);
+  };
+  // Q, then K (wave w: spans w, w + 4, ...); V follows once Q has been read.
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) dma_tile(qvtile, w + NW * i, qbase);
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) dma_tile(ktile, w + NW * i, kbase);
+  // Key validity words (keys 0..63, 64..127; keys past S are dead anyway), as this
+  // lane sees them: shifted by 4g, so that register r of key tile t tests the fixed
+  // bit 32(t % 2) + 8(r / 4) + r % 4 of word t / 2.
+  uint64_t lw0 = ~0ull, lw1 = ~0ull;
+  if constexpr (MASKED) {
+    lw0 = key_bits[b * nwords] >> (4 * g);
+    lw1 = key_bits[b * nwords + min(1, nwords - 1)] >> (4 * g);
+  }
+  wait_vmcnt<LPT>();  // Q
+  stage_barrier();
+  f16x8 qf[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const f16x8 q = *reinterpret_cast<const f16x8*>(qvtile + qi * 2 * HD + 16 * ((2 * kk + g) ^ swz<HD>(qi)));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[kk][e] = (f16)((float)q[e] * c2);
+  }
+  wait_vmcnt<0>();  // K
+  lds_barrier();    // every wave has its Q fragments and sees the whole K tile
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) dma_tile(qvtile, w + NW * i, vbase);
+
+  const bool active = 32 * w < S;  // waves wholly past S only take part in the transfers and barriers
+  f32x16 o[ND];
+#pragma unroll
+  for (int j = 0; j < ND; ++j) o[j] = zero16();
+  float l = 0.f;
+  f16x8 pf[8];
+  if (active) {
+    const int nkt = CAUSAL ? min((S + 31) / 32, w + 1) : (S + 31) / 32;  // key tiles with a live key
+    f32x16 sacc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      sacc[t] = zero16();
+      if (t < nkt) {
+        const int row = t * 32 + li;
+        const char* krow = ktile + row * 2 * HD;
+        const int sw = swz<HD>(row);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+          sacc[t] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + 16 * ((2 * kk + g) ^ sw)), qf[kk], sacc[t]);
+      }
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = t * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        bool dead = t >= nkt || key >= S || (CAUSAL && key > qi);
+        if constexpr (MASKED) dead = dead || !(((t < 2 ? lw0 : lw1) >> (32 * (t & 1) + 8 * (r >> 2) + (r & 3))) & 1);
+        if (dead) sacc[t][r] = kNegInf;
+        mx = fmaxf(mx, sacc[t][r]);
+      }
+    mx = max_xor32(mx);
+    // A query with no valid key (token masks) has max -inf: all-zero probabilities.
+    const float m = mx == kNegInf ? 0.f : mx;
+    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pf[2 * t + (r >> 3)][r & 7] = (f16)__builtin_amdgcn_exp2f(sacc[t][r] - m);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) l = __builtin_amdgcn_fdot2(f16x2{pf[k][2 * e], pf[k][2 * e + 1]}, ones, l, false);
+  }
+  wait_vmcnt<0>();  // V
+  lds_barrier();
+  if (active) {
+    const int vr = 4 * g + ((lane & 15) >> 2);
+    const int vc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const f16* Vc = reinterpret_cast<const f16*>(qvtile);
+    const int nks = CAUSAL ? 2 * min((S + 31) / 32, w + 1) : 2 * ((S + 31) / 32);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (ks < nks) {
+#pragma unroll
+        for (int j = 0; j < ND; ++j) {
+          const int c = j * 32 + vc;
+          const int r0 = ks * 16 + vr, r1 = r0 + 8;
+          const f16x4 lo = lds_read_tr16(Vc + r0 * HD + (((c >> 3) ^ swz<HD>(r0)) * 8) + (c & 7));
+          const f16x4 hi = lds_read_tr16(Vc + r1 * HD + (((c >> 3) ^ swz<HD>(r1)) * 8) + (c & 7));
+          const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[j] = mfma32x32x16(a, pf[ks], o[j]);
+        }
+      }
+    }
+  }
+  const float l_tot = sum_xor32(l);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  // Output through LDS (the K tile is dead): O^T quads into [128][HD] rows, then whole
+  // 16-byte chunks per lane, so the stores to ctx are row-contiguous.
+  lds_barrier();
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < ND; ++j)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = j * 32 + 8 * q4 + 4 * g;
+        f16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (f16)(o[j][q4 * 4 + e] * inv);
+        *reinterpret_cast<f16x4*>(ktile + qi * 2 * HD + 16 * ((d >> 3) ^ swz<HD>(qi)) + 8 * g) = v;
+      }
+  }
+  lds_barrier();
+  for (int idx = threadIdx.x; idx < BM * CPR; idx += NW * 64) {
+    const int row = idx / CPR, c = idx % CPR;
+    if (row < S)
+      *reinterpret_cast<f16x8*>(ctx + (b * S + row) * (int64_t)D + h * HD + 8 * c) =
+          *reinterpret_cast<const f16x8*>(ktile + row * 2 * HD + 16 * (c ^ swz<HD>(row)));
+  }
+}
+
+template <int HD, bool CAUSAL>
+static hipError_t launch_attn_short(const AttnArgs& a, float c2) {
+  const int64_t grid = (int64_t)a.heads * a.batch;
+  if (grid > 0x7fffffff) return hipErrorInvalidValue;
+  const int nwords = (int)mask_words(a.seq_len);
+  if (a.key_bits)
+    hipLaunchKernelGGL((attn_short_kernel<HD, CAUSAL, true>), dim3((unsigned)grid), dim3(256), 0, a.stream,
+                       static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads, c2, a.key_bits,
+                       nwords);
+  else
+    hipLaunchKernelGGL((attn_short_kernel<HD, CAUSAL, false>), dim3((unsigned)grid), dim3(256), 0, a.stream,
+                       static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads, c2, nullptr,
+                       nwords);
+  return hipGetLastError();
+}
+
 template <int HD, int NW, int BN, int ST, bool CAUSAL>
 static hipError_t launch_attn(const AttnArgs& a, float c2) {
   constexpr int BM = 32 * NW;
@@ -478,6 +657,9 @@ static hipError_t dispatch_waves(const AttnArgs& a, float c2) {
 template <bool CAUSAL>
 static hipError_t dispatch_hd(const AttnArgs& a, float c2) {
   const int hd = a.head_dim;
+  // Wide heads over at most 128 keys: exact softmax, one workgroup per (sequence, head).
+  if (a.seq_len <= 128 && hd == 256) return launch_attn_short<256, CAUSAL>(a, c2);
+  if (a.seq_len <= 128 && hd == 128) return launch_attn_short<128, CAUSAL>(a, c2);
   if (hd <= 16) return dispatch_waves<16, CAUSAL>(a, c2);
   if (hd <= 32) return dispatch_waves<32, CAUSAL>(a, c2);
   if (hd <= 64) return dispatch_waves<64, CAUSAL>(a, c2);

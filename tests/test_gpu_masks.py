@@ -152,7 +152,7 @@ def test_attn_op_key_mask(hd, causal):
 
     torch.manual_seed(hd + 1)
     B, H = 3, 2
-    for S in (1, 31, 64, 130, 300):
+    for S in (1, 31, 64, 128, 130, 300):
         D = H * hd
         qkv = torch.randn(B * S, 3 * D, device=DEV).half()
         m = token_mask(B, S, seed=S, left_aligned=False).to(DEV)

@@ -398,7 +398,7 @@ def test_attn_op(hd, causal):
 
     torch.manual_seed(hd)
     B, H = 2, 3
-    for S in (1, 31, 64, 130):
+    for S in (1, 31, 64, 97, 128, 130):
         D = H * hd
         qkv = torch.randn(B * S, 3 * D, device=DEV).half()
         got = ops.attn(qkv, B, S, H, hd, hd ** -0.5, causal=causal)
