@@ -342,7 +342,8 @@ def bench_long(dev, steps=2, warmup=1):
                                    "device_resident_ms_same_work": ms / 4,
                                    "note": "pageable host input and output, 4 chunks of 2 sequences, H2D/D2H and "
                                            "host staging copies overlapped with compute (PCIe-inclusive)"},
-            "roofline": roofline("attn_fwd_kernel (per sequence)", a_fl, 4 * S * D * 2, a_ms)}
+            "roofline": dict(roofline("attn_fwd_kernel (per sequence)", a_fl, 4 * S * D * 2, a_ms),
+                             traffic=committed_traffic(LONG_TRAFFIC_FILE))}
 
 
 MODEL_CASES = [  # the reference's whole-model cases (tools/sweep.py:31-47): #, B, S, D, H, F, layers (causal)
@@ -385,12 +386,13 @@ def bench_model(dev, iters=20, cases=MODEL_CASES):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_layer_split_kernel_B64_d128_H4_S128.txt")
+LONG_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_attn_fwd_kernel_B32_d1024_H16_S100000.txt")
 
 
-def committed_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed PMC summary (or None)."""
+def committed_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch of a kernel, from its committed PMC summary (or None)."""
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(path):
             if line.startswith("traffic_bytes_per_launch="):
                 return float(line.split("=", 1)[1])
     except OSError:
@@ -398,27 +400,54 @@ def committed_traffic():
     return None
 
 
-def pmc_driver(dev) -> None:
-    """Workload for `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE`: a 64 MiB device copy
-    (known bytes, the counter calibration) five times, then the dominant kernel five times."""
+PMC_CONFIGS = {  # --pmc-driver workloads: name -> (B, S, D, H)
+    "base": (64, 128, 128, 4), "gemm": (64, 128, 1024, 4), "b10000": (10000, 128, 128, 4),
+    "s1024": (64, 1024, 128, 4), "long2": (2, 100000, 1024, 16),
+}
+
+
+def pmc_driver(dev, name="base") -> None:
+    """Workload for `rocprofv3 --pmc ...`: the counter calibration, then one configuration.
+
+    Calibration, known HBM bytes: a 64 MiB device copy (ordinary loads and stores,
+    __amd_rocclr_copyBuffer) five times, and a GEMM whose operand tiles arrive by
+    LDS-DMA like every kernel on the path (gemm_dma_kernel, 65536 x 128 x 64: A, 8 MiB,
+    read once; W, 16 KiB; C, 16 MiB fp16, written once) five times.  Then three forwards
+    of the named configuration (PMC_CONFIGS; "long2" = two sequences of the long shape),
+    inputs already on the device.
+    """
+    from cobra_amd import ops
+
     src = torch.randn(16 << 20, device=dev)  # 64 MiB
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
+    a = torch.randn(65536, 64, device=dev).half()
+    w = torch.randn(128, 64, device=dev).half()
+    for _ in range(5):
+        ops.linear(a, w, None)
     torch.cuda.synchronize()
-    layer = make_layer(128, 4, dev)
-    x = synthetic_input(64, 128, 128, seed=0).half().to(dev)
+    del src, dst, a, w
+    B, S, D, H = PMC_CONFIGS[name]
+    layer = make_layer(D, H, dev)
+    if name == "long2":
+        x = torch.empty(B, S, D, device=dev, dtype=torch.float16)
+        for b in range(B):
+            x[b].copy_(synthetic_sequence(b, S, D).half())
+    else:
+        x = synthetic_input(B, S, D, seed=0).half().to(dev)
     launch = layer_launcher(layer, x, torch.empty_like(x))
     with torch.inference_mode():
-        for _ in range(5):
+        for _ in range(3):
             launch()
     torch.cuda.synchronize()
-    print("pmc driver done", flush=True)
+    print(f"pmc driver done: {name} B{B} S{S} D{D} H{H}", flush=True)
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--pmc-driver", action="store_true", help="run the PMC calibration workload and exit")
+    ap.add_argument("--pmc-driver", nargs="?", const="base", default=None, choices=sorted(PMC_CONFIGS),
+                    help="run the PMC calibration workload and one configuration, then exit")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -443,7 +472,7 @@ def main() -> int:
         print(json.dumps({"matrix": bench_model(torch.device("cuda:0"), cases=MATRIX_CASES)}), flush=True)
         return 0
     if args.pmc_driver:
-        pmc_driver(dev)
+        pmc_driver(dev, args.pmc_driver)
         return 0
     if args.only:
         names = [n for n in args.only.split(",") if n]

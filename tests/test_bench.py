@@ -92,3 +92,20 @@ def test_long_cpu_baseline_scales_a_bounded_sample():
     assert out["s_per_forward_x32_extrapolated"] == pytest.approx(32 * out["s_per_sequence"])
     assert "1 of 784 attention blocks" in out["sample"]
     assert out["cpu_model"] and out["os_cpu_count"] == os.cpu_count()
+
+
+def test_long_traffic_file_is_consistent():
+    """The long leg's committed traffic: fetch and write counters scaled as the file says,
+    per sequence, and at least the algorithmic bytes bench.py's roofline uses."""
+    fields = {}
+    with open(bench.LONG_TRAFFIC_FILE) as f:
+        for line in f:
+            if "=" in line and not line.startswith("#"):
+                k, v = line.strip().split("=", 1)
+                fields[k] = float(v)
+    S, D = 100000, 1024
+    assert fields["algorithmic_bytes_per_sequence"] == 4 * S * D * 2
+    want = (fields["kernel_fetch_kib_per_dispatch"] * fields["fetch_scale"]
+            + fields["kernel_write_kib_per_dispatch"] * fields["write_scale"]) * 1024 / fields["sequences_per_dispatch"]
+    assert abs(want - fields["traffic_bytes_per_launch"]) <= 1e-4 * want
+    assert bench.committed_traffic(bench.LONG_TRAFFIC_FILE) == fields["traffic_bytes_per_launch"]
