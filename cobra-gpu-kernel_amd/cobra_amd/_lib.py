@@ -15,12 +15,13 @@ from typing import Optional
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcobra_amd.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F16 = 0
 F32 = 1
 PLAN_FUSED = 0
 PLAN_STAGED = 1
+PLAN_PADDED = 2
 # Epilogue / row-mask flags (COBRA_EPI_* in include/cobra_amd.h).
 EPI_GELU = 1
 EPI_MASK_BRANCH = 2

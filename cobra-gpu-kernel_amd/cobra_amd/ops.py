@@ -322,6 +322,7 @@ def attn(
 
 PLAN_FUSED = _lib.PLAN_FUSED
 PLAN_STAGED = _lib.PLAN_STAGED
+PLAN_PADDED = _lib.PLAN_PADDED
 
 
 def _dt_of(dtype: torch.dtype) -> int:
@@ -333,8 +334,9 @@ def _dt_of(dtype: torch.dtype) -> int:
 
 def layer_plan(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False,
                dtype: torch.dtype = torch.float16) -> int:
-    """PLAN_FUSED (one kernel) or PLAN_STAGED for this shape and activation dtype
-    (host-only query)."""
+    """PLAN_FUSED (one kernel), PLAN_STAGED, or PLAN_PADDED (head_dim or d_model not a
+    multiple of 8: the staged plan on zero-padded copies) for this shape and activation
+    dtype (host-only query)."""
     p = _lib.lib().cobra_layer_plan(batch, seq_len, d_model, heads, 1 if masked else 0, _dt_of(dtype))
     if p < 0:
         raise ValueError(f"unsupported sublayer shape B={batch} S={seq_len} D={d_model} H={heads}")

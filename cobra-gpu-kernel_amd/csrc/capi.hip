@@ -14,6 +14,9 @@ using cobra::kF16;
 using cobra::kF32;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned_to(const void* p, int n) { return (reinterpret_cast<uintptr_t>(p) & (uintptr_t)(n - 1)) == 0; }
+int dtype_bytes(int dt) { return dt == kF32 ? 4 : 2; }
+int64_t round8(int64_t n) { return (n + 7) & ~int64_t(7); }
 bool opt_aligned16(const void* p) { return p == nullptr || aligned16(p); }
 bool is_dtype(int dt) { return dt == kF16 || dt == kF32; }
 int64_t round256(int64_t n) { return (n + 255) & ~int64_t(255); }
@@ -52,7 +55,35 @@ bool ln1_affine_ok(const float* w, const float* b) {
 bool layer_shape_ok(int64_t batch, int64_t seq_len, int64_t d, int64_t heads) {
   if (batch < 0 || seq_len < 0 || d <= 0 || heads <= 0 || d % heads != 0) return false;
   const int64_t hd = d / heads;
-  return d % 8 == 0 && hd % 8 == 0 && hd <= 256 && d <= cobra::kLnMaxD && seq_len <= 0x7fffffff;
+  return hd <= 256 && d <= cobra::kLnMaxD && seq_len <= 0x7fffffff;
+}
+
+// Shapes whose head_dim or d_model is not a multiple of 8 run the padded staged plan.
+bool layer_needs_pad(int64_t d, int64_t heads) { return d % 8 != 0 || (d / heads) % 8 != 0; }
+
+// Workspace of the padded staged plan: zero-padded weights (each head's rows / columns
+// padded from head_dim to hdp = round8(head_dim), d_model to Dp = round8(d_model)), the
+// padded activations h / ctx, qkv, the fp32 out-projection branch, the key bits.
+struct PadBuffers {
+  int64_t hdp, dp, e;  // padded head_dim, d_model, H * hdp
+  int64_t wq_off, bq_off, wo_off, bo_off, h_off, qkv_off, r_off, bits_off, total;
+};
+PadBuffers pad_buffers(int64_t batch, int64_t seq_len, int64_t d, int64_t heads, bool masked) {
+  PadBuffers p{};
+  const int64_t tokens = batch * seq_len;
+  p.hdp = round8(d / heads);
+  p.dp = round8(d);
+  p.e = heads * p.hdp;
+  p.wq_off = 0;
+  p.bq_off = p.wq_off + round256(3 * p.e * p.dp * 2);
+  p.wo_off = p.bq_off + round256(3 * p.e * 4);
+  p.bo_off = p.wo_off + round256(p.dp * p.e * 2);
+  p.h_off = p.bo_off + round256(p.dp * 4);
+  p.qkv_off = p.h_off + round256(tokens * (p.dp > p.e ? p.dp : p.e) * 2);
+  p.r_off = p.qkv_off + round256(tokens * 3 * p.e * 2);
+  p.bits_off = p.r_off + round256(tokens * p.dp * 4);
+  p.total = p.bits_off + (masked ? round256(batch * cobra::mask_words(seq_len) * 8) : 0);
+  return p;
 }
 
 }  // namespace
@@ -87,6 +118,64 @@ hipError_t scratch_of_current_device(void** out) {
   return *out ? hipSuccess : hipErrorInvalidSymbol;
 }
 
+// The padded staged plan (head_dim or d_model not a multiple of 8): the weights are
+// laid out zero-padded in the workspace, LN1 writes h padded to Dp columns, the QKV
+// GEMM produces q / k / v with every head padded to hdp dimensions, the attention
+// runs at head_dim hdp with the true scale (the zero dimensions add nothing to
+// q . k and give zero context columns), the out-projection writes its fp32 branch
+// [T, Dp] (padded rows zeroed for masked tokens), and LN2 adds x and normalises the
+// first D columns.
+int layer_fwd_padded(const void* x, int x_dtype, const uint8_t* valid_mask, const void* w_qkv, const float* b_qkv,
+                     const void* w_o, const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w,
+                     const float* ln2_b, void* y, float* resid_out, void* workspace, int64_t workspace_bytes,
+                     int64_t batch, int64_t seq_len, int64_t D, int64_t H, int causal, float eps, hipStream_t s) {
+  const bool masked = valid_mask != nullptr;
+  const PadBuffers pb = pad_buffers(batch, seq_len, D, H, masked);
+  if (!workspace || workspace_bytes < pb.total) return kBad;
+  const int64_t T = batch * seq_len;
+  if (T == 0) return 0;
+  const int64_t hd = D / H, hdp = pb.hdp, Dp = pb.dp, E = pb.e;
+  char* ws = static_cast<char*>(workspace);
+  void* wq = ws + pb.wq_off;
+  float* bq = reinterpret_cast<float*>(ws + pb.bq_off);
+  void* wo = ws + pb.wo_off;
+  float* bo = reinterpret_cast<float*>(ws + pb.bo_off);
+  void* h = ws + pb.h_off;
+  void* ctx = h;  // h is dead once the QKV projection has read it
+  void* qkv = ws + pb.qkv_off;
+  float* r = reinterpret_cast<float*>(ws + pb.r_off);
+  uint64_t* bits = masked ? reinterpret_cast<uint64_t*>(ws + pb.bits_off) : nullptr;
+  hipError_t e = hipSuccess;
+  // W_qkv [3D, D] -> [3E, Dp]: head-padded rows, tail-padded columns; b_qkv likewise.
+  cobra::PadArgs p1{w_qkv, wq, 2, D, 3 * E, Dp, hd, hdp, 3 * D, Dp, Dp, D, s};
+  cobra::PadArgs p2{b_qkv, bq, 4, 1, 3 * E, 1, hd, hdp, 3 * D, 1, 1, 1, s};
+  // W_o [D, D] -> [Dp, E]: tail-padded rows, head-padded columns; b_o tail-padded.
+  cobra::PadArgs p3{w_o, wo, 2, D, Dp, E, Dp, Dp, D, hd, hdp, D, s};
+  cobra::PadArgs p4{b_o, bo, 4, 1, Dp, 1, Dp, Dp, D, 1, 1, 1, s};
+  for (const cobra::PadArgs* pa : {&p1, &p2, &p3, &p4})
+    if ((e = cobra::run_pad(*pa)) != hipSuccess) return code(e);
+  if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
+  cobra::LnArgs ln1{x, x_dtype, nullptr, 0, ln1_w, ln1_b, nullptr, h, kF16, T, (int)D, eps, s};
+  ln1.ldy = Dp;
+  if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
+  cobra::GemmArgs proj{h, wq, bq, nullptr, kF16, qkv, kF16, T, (int)(3 * E), (int)Dp,
+                       nullptr, nullptr, nullptr, kF16, eps, s};
+  if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
+  cobra::AttnArgs at{qkv, ctx, batch, (int)seq_len, (int)H, (int)hdp, (float)(1.0 / sqrt((double)hd)),
+                     causal ? 1 : 0, s};
+  at.key_bits = bits;
+  if ((e = cobra::run_attn(at)) != hipSuccess) return code(e);
+  // Padded query rows: the attention output is zeroed before the residual add (TTB:121-122).
+  cobra::GemmArgs out{ctx, wo, bo, nullptr, kF16, r, kF32, T, (int)Dp, (int)E,
+                      nullptr, nullptr, nullptr, kF16, eps, s};
+  out.row_mask = valid_mask;
+  out.epi = masked ? cobra::kEpiMaskBranch : 0;
+  if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
+  cobra::LnArgs ln2{x, x_dtype, r, 1, ln2_w, ln2_b, resid_out, y, x_dtype, T, (int)D, eps, s};
+  ln2.ldb = Dp;
+  return code(cobra::run_ln(ln2));
+}
+
 }  // namespace
 
 extern "C" {
@@ -101,10 +190,13 @@ int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtyp
   if (!x || !y || !gamma || !beta || !is_dtype(x_dtype) || !is_dtype(y_dtype)) return kBad;
   if ((mask_flags & ~(COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT)) != 0 || (mask_flags && !row_mask)) return kBad;
   if (branch && !is_dtype(branch_dtype)) return kBad;
-  if (!aligned16(x) || !aligned16(y) || !aligned16(gamma) || !aligned16(beta) || !opt_aligned16(branch) ||
-      !opt_aligned16(resid_out))
+  // Element alignment suffices; widths that are multiples of 8 on 16-byte aligned buffers
+  // take the vector kernels.
+  if (!aligned_to(x, dtype_bytes(x_dtype)) || !aligned_to(y, dtype_bytes(y_dtype)) || !aligned_to(gamma, 4) ||
+      !aligned_to(beta, 4) || (branch && !aligned_to(branch, dtype_bytes(branch_dtype))) ||
+      (resid_out && !aligned_to(resid_out, 4)))
     return kBad;
-  if (d <= 0 || d > cobra::kLnMaxD || d % 8 != 0 || rows < 0) return kBad;
+  if (d <= 0 || d > cobra::kLnMaxD || rows < 0) return kBad;
   cobra::LnArgs a{x,        x_dtype, branch, branch_dtype == kF32 ? 1 : 0, gamma, beta, resid_out, y, y_dtype,
                   rows,     (int)d,  eps,    static_cast<hipStream_t>(stream)};
   a.row_mask = row_mask;
@@ -177,7 +269,8 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
 
 int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked, int x_dtype) {
   if (!layer_shape_ok(batch, seq_len, d_model, heads) || !is_dtype(x_dtype)) return -1;
-  (void)masked;  // both plans take a token mask
+  (void)masked;  // every plan takes a token mask
+  if (layer_needs_pad(d_model, heads)) return COBRA_PLAN_PADDED;
   return cobra::layer_fused_ok(batch, seq_len, d_model, heads, x_dtype) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
 }
 
@@ -185,6 +278,7 @@ int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_mo
                                     int x_dtype) {
   const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked, x_dtype);
   if (plan < 0) return -1;
+  if (plan == COBRA_PLAN_PADDED) return pad_buffers(batch, seq_len, d_model, heads, masked != 0).total;
   return plan == COBRA_PLAN_FUSED ? 0 : layer_buffers(batch, seq_len, d_model, masked != 0).total;
 }
 
@@ -210,6 +304,9 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     a.valid_mask = valid_mask;
     return code(cobra::run_layer_small(a));
   }
+  if (plan == COBRA_PLAN_PADDED)
+    return layer_fwd_padded(x, x_dtype, valid_mask, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, resid_out,
+                            workspace, workspace_bytes, batch, seq_len, d_model, heads, causal, eps, s);
   const LayerBuffers lb = layer_buffers(batch, seq_len, D, masked);
   if (!workspace || workspace_bytes < lb.total) return kBad;
   if (T == 0) return 0;

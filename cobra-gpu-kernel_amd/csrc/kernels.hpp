@@ -37,8 +37,26 @@ struct LnArgs {
   const uint8_t* row_mask = nullptr;  // optional [rows]; 0 = padded row
   int mask_resid = 0;      // r *= mask before the store and the statistics
   int mask_out = 0;        // y *= mask
+  // Row strides in elements (0 = d) and zero fill: with ldy > d, y columns d .. ldy-1
+  // are written as 0 (a row padded for the GEMM that consumes it).  Any stride or a
+  // width that is not a multiple of 8 takes the element-wise kernel.
+  int64_t ldx = 0, ldb = 0, ldr = 0, ldy = 0;
 };
 hipError_t run_ln(const LnArgs& a);
+
+// Weights of the padded staged plan (head_dim or d_model not a multiple of 8):
+//   out[r][c] = in[rmap(r)][cmap(c)], 0 where a map has no source;
+// a map takes i -> (i / gout) * gin + i % gout when i % gout < gin and that is < lim.
+struct PadArgs {
+  const void* in;   // [in_rows, in_cols] row-major
+  void* out;        // [out_rows, out_cols] row-major
+  int elem_bytes;   // 2 (fp16) or 4 (fp32)
+  int64_t in_cols, out_rows, out_cols;
+  int64_t r_gin, r_gout, r_lim;
+  int64_t c_gin, c_gout, c_lim;
+  hipStream_t stream;
+};
+hipError_t run_pad(const PadArgs& a);
 
 struct GemmArgs {
   const void* a;           // [M, K] fp16, row-major

@@ -154,6 +154,85 @@ __global__ __launch_bounds__(256) void ln_plain_kernel(const TX* __restrict__ x,
   }
 }
 
+// Any width, any row strides (element-wise, one wave per row, lane l holding
+// columns l, l + 64, ...): rows not a multiple of 8 wide, or rows inside wider
+// buffers, such as the padded staged plan's LN1 (x [T, D] -> h [T, Dp] with the
+// pad columns zeroed) and LN2 (x [T, D] + branch [T, Dp]).  Same arithmetic as
+// ln_rows_kernel: two-pass fp32 statistics, eps inside the square root.
+template <typename TX, typename TY, int NE>
+__global__ __launch_bounds__(256) void ln_any_kernel(const TX* __restrict__ x, int64_t ldx, const void* __restrict__ branch,
+                                                     int branch_f32, int64_t ldb, const float* __restrict__ gamma,
+                                                     const float* __restrict__ beta, float* __restrict__ resid_out,
+                                                     int64_t ldr, TY* __restrict__ y, int64_t ldy, int64_t rows, int d,
+                                                     float eps, const uint8_t* __restrict__ row_mask, int mask_resid,
+                                                     int mask_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;  // wave-uniform; no barrier follows
+  const float mv = row_mask ? (row_mask[r] != 0 ? 1.f : 0.f) : 1.f;
+  float v[NE];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int c = lane + 64 * k;
+    v[k] = 0.f;
+    if (c < d) {
+      v[k] = (float)x[r * ldx + c];
+      if (branch)
+        v[k] += branch_f32 ? static_cast<const float*>(branch)[r * ldb + c]
+                           : (float)static_cast<const f16*>(branch)[r * ldb + c];
+      if (mask_resid) v[k] *= mv;
+    }
+    s += v[k];
+  }
+  const float mean = group_sum<64>(s) / (float)d;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < NE; ++k)
+    if (lane + 64 * k < d) {
+      const float t = v[k] - mean;
+      q += t * t;
+    }
+  const float rstd = rsqrtf(group_sum<64>(q) / (float)d + eps);
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int c = lane + 64 * k;
+    if (c < d) {
+      if (resid_out) resid_out[r * ldr + c] = v[k];
+      float o = (v[k] - mean) * rstd;
+      if (gamma) o = o * gamma[c] + beta[c];
+      if (mask_out) o *= mv;
+      y[r * ldy + c] = (TY)o;
+    } else if (c < ldy) {
+      y[r * ldy + c] = (TY)0.0f;
+    }
+  }
+}
+
+template <typename TX, typename TY, int NE>
+static hipError_t launch_ln_any(const LnArgs& a) {
+  const int64_t blocks = (a.rows + 3) / 4;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((ln_any_kernel<TX, TY, NE>), dim3((unsigned)blocks), dim3(256), 0, a.stream,
+                     static_cast<const TX*>(a.x), a.ldx ? a.ldx : a.d, a.branch, a.branch_f32, a.ldb ? a.ldb : a.d,
+                     a.gamma, a.beta, a.resid_out, a.ldr ? a.ldr : a.d, static_cast<TY*>(a.y), a.ldy ? a.ldy : a.d,
+                     a.rows, a.d, a.eps, a.row_mask, a.row_mask ? a.mask_resid : 0, a.row_mask ? a.mask_out : 0);
+  return hipGetLastError();
+}
+
+template <typename TX, typename TY>
+static hipError_t dispatch_ln_any(const LnArgs& a) {
+  const int64_t ldy = a.ldy ? a.ldy : a.d;
+  const int64_t w = ldy > a.d ? ldy : a.d;  // columns to write
+  if (w <= 64) return launch_ln_any<TX, TY, 1>(a);
+  if (w <= 128) return launch_ln_any<TX, TY, 2>(a);
+  if (w <= 256) return launch_ln_any<TX, TY, 4>(a);
+  if (w <= 512) return launch_ln_any<TX, TY, 8>(a);
+  if (w <= 1024) return launch_ln_any<TX, TY, 16>(a);
+  if (w <= 2048) return launch_ln_any<TX, TY, 32>(a);
+  return launch_ln_any<TX, TY, 64>(a);
+}
+
 template <typename TX, typename TY, int NCH>
 static hipError_t launch_ln_plain(const LnArgs& a) {
   const int64_t blocks = (a.rows + 3) / 4;
@@ -190,9 +269,27 @@ static hipError_t dispatch_ln_geometry(const LnArgs& a) {
   return launch_ln<TX, TY, 64, 8>(a);
 }
 
+static bool vec_aligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 hipError_t run_ln(const LnArgs& a) {
-  if (a.rows < 0 || a.d <= 0 || a.d % 8 != 0 || a.d > kLnMaxD) return hipErrorInvalidValue;
+  if (a.rows < 0 || a.d <= 0 || a.d > kLnMaxD) return hipErrorInvalidValue;
+  const int64_t d = a.d;
+  if ((a.ldx && a.ldx < d) || (a.ldb && a.ldb < d) || (a.ldr && a.ldr < d) || (a.ldy && a.ldy < d))
+    return hipErrorInvalidValue;
   if (a.rows == 0) return hipSuccess;
+  // The vector kernels need whole 16-byte chunks: width a multiple of 8, dense rows,
+  // 16-byte aligned buffers.
+  const bool dense = (!a.ldx || a.ldx == d) && (!a.ldb || a.ldb == d) && (!a.ldr || a.ldr == d) && (!a.ldy || a.ldy == d);
+  const bool vec = d % 8 == 0 && dense && vec_aligned(a.x) && vec_aligned(a.y) && (!a.branch || vec_aligned(a.branch)) &&
+                   (!a.resid_out || vec_aligned(a.resid_out)) && (!a.gamma || vec_aligned(a.gamma)) &&
+                   (!a.beta || vec_aligned(a.beta));
+  if (!vec) {
+    if (a.x_dtype == kF16 && a.y_dtype == kF16) return dispatch_ln_any<f16, f16>(a);
+    if (a.x_dtype == kF16 && a.y_dtype == kF32) return dispatch_ln_any<f16, float>(a);
+    if (a.x_dtype == kF32 && a.y_dtype == kF16) return dispatch_ln_any<float, f16>(a);
+    if (a.x_dtype == kF32 && a.y_dtype == kF32) return dispatch_ln_any<float, float>(a);
+    return hipErrorInvalidValue;
+  }
   if (a.x_dtype == kF16 && a.y_dtype == kF16) return dispatch_ln_geometry<f16, f16>(a);
   if (a.x_dtype == kF16 && a.y_dtype == kF32) return dispatch_ln_geometry<f16, float>(a);
   if (a.x_dtype == kF32 && a.y_dtype == kF16) return dispatch_ln_geometry<float, f16>(a);

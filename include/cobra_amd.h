@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 6
+#define COBRA_ABI_VERSION 7
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
 
@@ -63,8 +63,9 @@ const char* cobra_error_string(int code);
  *     y *= m (COBRA_EPI_MASK_OUT)
  * x, branch, y: [rows, d]; gamma, beta: [d] fp32; row_mask: [rows] bytes
  * (required when mask_flags != 0; only the two flags above are accepted).
- * d % 8 == 0, d <= 4096.  Replaces _tl_add_ln / _add_ln_kernel
- * (TTB:539-569, 491-535).
+ * d <= 4096; pointers aligned to their element size (widths that are multiples of
+ * 8 on 16-byte aligned buffers take the vector kernels).  Replaces _tl_add_ln /
+ * _add_ln_kernel (TTB:539-569, 491-535).
  */
 int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtype, const float* gamma,
                  const float* beta, const uint8_t* row_mask, int mask_flags, float* resid_out, void* y, int y_dtype,
@@ -135,12 +136,16 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
 /* Execution plans of cobra_layer_fwd. */
 enum {
   COBRA_PLAN_FUSED = 0,  /* one kernel for the whole sublayer, no workspace */
-  COBRA_PLAN_STAGED = 1  /* LN1, QKV GEMM, attention, out-proj GEMM (+LN) through a workspace */
+  COBRA_PLAN_STAGED = 1, /* LN1, QKV GEMM, attention, out-proj GEMM (+LN) through a workspace */
+  COBRA_PLAN_PADDED = 2  /* the staged plan on zero-padded copies: head_dim or d_model not a multiple of 8 */
 };
 
 /*
  * Which plan cobra_layer_fwd runs for this shape and activation dtype, or -1
- * if the shape (or x_dtype) is not supported.  FUSED covers seq_len <= 128 with
+ * if the shape (or x_dtype) is not supported (d_model % heads != 0, head_dim >
+ * 256, d_model > 4096).  PADDED covers every head_dim or d_model that is not a
+ * multiple of 8 (the reference zero-pads head_dim to HD_PAD inside its attention
+ * kernel, TTB:578, 763-765, and masks its GEMM loads).  FUSED covers seq_len <= 128 with
  * d_model 128 (head_dim 32 or 64), 64 (32, 64) or 96 (32), with or without a
  * token mask; and, for fp16 activations while batch * ceil(seq_len / 32) <= 2 x
  * the device's compute units, d_model 128 at head_dim 8 or 128.  `masked` (a token

@@ -414,7 +414,7 @@ def test_invalid_shapes_raise():
     from cobra_amd import CobraError, ops
 
     with pytest.raises(ValueError):
-        ops.layer_workspace_bytes(2, 16, 120, 10)  # head_dim 12 is not a multiple of 8
+        ops.layer_workspace_bytes(2, 16, 528, 2)  # head_dim 264
     qkv = torch.zeros(16, 3 * 3 * 264, device=DEV, dtype=torch.float16)
     with pytest.raises(CobraError):
         ops.attn(qkv, 1, 16, 3, 264, 0.1)  # head_dim > 256

@@ -48,7 +48,10 @@ def test_argument_validation_rejects_before_any_launch():
     assert lib.cobra_attn_fwd(16, 16, None, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
     assert lib.cobra_attn_fwd(256, 256, 12, 1, 4, 1, 16, 0.1, 0, None) != 0  # misaligned key bits
     assert lib.cobra_mask_bits(256, 12, 1, 4, None) != 0                   # misaligned key bits
-    assert lib.cobra_layer_workspace_bytes(2, 16, 120, 10, 0, _lib.F16) == -1      # head_dim 12
+    assert lib.cobra_layer_workspace_bytes(2, 16, 528, 2, 0, _lib.F16) == -1       # head_dim 264
+    assert lib.cobra_layer_workspace_bytes(2, 16, 100, 3, 0, _lib.F16) == -1       # d_model % heads
+    assert lib.cobra_layer_plan(2, 16, 120, 10, 0, _lib.F16) == _lib.PLAN_PADDED   # head_dim 12
+    assert lib.cobra_layer_plan(2, 16, 100, 4, 0, _lib.F16) == _lib.PLAN_PADDED    # d_model 100
     assert lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0, _lib.F32) > 0     # staged plan (head_dim 8, fp32)
     assert lib.cobra_layer_workspace_bytes(2, 16, 128, 4, 0, 7) == -1           # dtype code
     assert lib.cobra_layer_plan(2, 16, 128, 4, 0, _lib.F16) == _lib.PLAN_FUSED
@@ -64,7 +67,8 @@ def test_layer_bind_validates_and_releases():
     lib = _lib.lib()
     w = [256 * (i + 1) for i in range(8)]  # aligned stand-in addresses: bind dereferences nothing
     assert not lib.cobra_layer_bind(0, 0, 12, *w[1:], None, 0, 2, 16, 128, 4, 0, 1e-5)   # misaligned w_qkv
-    assert not lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 120, 10, 0, 1e-5)          # head_dim 12
+    assert not lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 120, 10, 0, 1e-5)          # padded: needs workspace
+    assert not lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 528, 2, 0, 1e-5)           # head_dim 264
     assert not lib.cobra_layer_bind(1, 0, *w, None, 0, 2, 16, 128, 16, 0, 1e-5)          # staged: needs workspace
     assert not lib.cobra_layer_bind(5, 0, *w, None, 0, 2, 16, 128, 4, 0, 1e-5)           # dtype code
     h = lib.cobra_layer_bind(0, 0, *w, None, 0, 2, 16, 128, 4, 0, 1e-5)                  # fused: no workspace
@@ -164,7 +168,8 @@ def test_plan_selection_per_config():
     with pytest.raises(TypeError):
         ops.layer_plan(2, 16, 128, 4, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
-        ops.layer_plan(2, 16, 120, 10)
+        ops.layer_plan(2, 16, 528, 2)  # head_dim 264
+    assert ops.layer_plan(2, 16, 120, 10) == ops.PLAN_PADDED
 
 
 def test_state_dict_identical_to_reference_sublayer():
@@ -307,3 +312,25 @@ def test_noalloc_scratch_size_matches_the_header():
     # rejected on the host, before any device call: a shape beyond the scratch
     assert lib.cobra_layer_fwd_noalloc(256, _lib.F16, None, 256, 256, 256, 256, None, None, 256, 256, 256, None,
                                        200, 1024, 128, 4, 0, 1e-5, None) != 0
+
+
+def _r256(n):
+    return (n + 255) & ~255
+
+
+@pytest.mark.parametrize("B,S,D,H,masked", [(2, 16, 120, 10, False), (3, 17, 100, 4, True), (1, 5, 36, 3, True),
+                                            (2, 9, 9, 1, False), (4, 33, 260, 4, True)])
+def test_padded_plan_workspace(B, S, D, H, masked):
+    """The padded plan's workspace: padded W_qkv / b_qkv / W_o / b_o, h or ctx (the wider),
+    qkv, the fp32 branch and the key bits, each 256-byte aligned (head_dim and d_model
+    rounded up to multiples of 8)."""
+    from cobra_amd import ops
+
+    hdp = -(-(D // H) // 8) * 8
+    dp = -(-D // 8) * 8
+    e = H * hdp
+    t = B * S
+    want = (_r256(3 * e * dp * 2) + _r256(3 * e * 4) + _r256(dp * e * 2) + _r256(dp * 4) + _r256(t * max(dp, e) * 2)
+            + _r256(t * 3 * e * 2) + _r256(t * dp * 4) + (_r256(B * -(-S // 64) * 8) if masked else 0))
+    assert ops.layer_plan(B, S, D, H, masked) == ops.PLAN_PADDED
+    assert ops.layer_workspace_bytes(B, S, D, H, masked) == want
