@@ -15,7 +15,7 @@ from typing import Optional
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcobra_amd.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F16 = 0
 F32 = 1
@@ -53,6 +53,10 @@ SIGNATURES = {
     ),
     "cobra_mask_bits": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "cobra_attn_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp]),
+    "cobra_qkv_attn_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "cobra_qkv_attn_fwd": (
+        _c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp],
+    ),
     "cobra_layer_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "cobra_layer_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "cobra_layer_fwd": (

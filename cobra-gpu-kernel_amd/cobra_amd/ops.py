@@ -320,6 +320,61 @@ def attn(
     return out
 
 
+def qkv_attn(
+    h: torch.Tensor,
+    w_qkv: torch.Tensor,
+    b_qkv: Optional[torch.Tensor],
+    batch: int,
+    seq_len: int,
+    heads: int,
+    head_dim: int,
+    scale: float,
+    out_dtype: torch.dtype = torch.float16,
+    cfgs=None,
+    causal: bool = True,
+    key_mask: Optional[torch.Tensor] = None,
+    key_bits: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """QKV projection fused with attention: ``h [B*S, D]`` -> ``ctx [B*S, D]``.  Mirrors
+    ``_tl_qkvattn`` (TTB:761-785).
+
+    Differences from the reference launcher: ``w_qkv`` is the nn.Linear-layout ``[3D, D]``
+    q | k | v weight (the reference passes the transposed ``[D, 3D]``), attention may be
+    non-causal and masked (``key_mask`` / ``key_bits`` as in ``attn``), and the projected
+    q / k / v go through a workspace allocated here (``torch.empty``) between the GEMM
+    and the attention kernel.  ``cfgs`` is accepted and ignored.
+    """
+    _dev(h, "h")
+    _dev(w_qkv, "w_qkv")
+    if h.dtype != torch.float16 or w_qkv.dtype != torch.float16 or out_dtype != torch.float16:
+        raise TypeError("h, w_qkv and ctx are float16")
+    D = heads * head_dim
+    if h.shape != (batch * seq_len, D) or w_qkv.shape != (3 * D, D):
+        raise ValueError(f"h must be [{batch * seq_len}, {D}] and w_qkv [{3 * D}, {D}]")
+    bias = None if b_qkv is None else _f32_param(b_qkv, 3 * D, "b_qkv")
+    bits = key_bits
+    if key_mask is not None:
+        if key_bits is not None:
+            raise ValueError("pass key_mask or key_bits, not both")
+        if tuple(key_mask.shape) != (batch, seq_len):
+            raise ValueError(f"key_mask must be [{batch}, {seq_len}], got {tuple(key_mask.shape)}")
+        bits = mask_bits(key_mask)
+    elif bits is not None:
+        _dev(bits, "key_bits")
+        if bits.dtype != torch.int64 or tuple(bits.shape) != (batch, (seq_len + 63) // 64):
+            raise ValueError(f"key_bits must be int64 [{batch}, {(seq_len + 63) // 64}]")
+    need = _lib.lib().cobra_qkv_attn_workspace_bytes(batch, seq_len, heads, head_dim)
+    if need < 0:
+        raise ValueError(f"unsupported attention shape heads={heads} head_dim={head_dim}")
+    ws = torch.empty(max(int(need), 1), dtype=torch.uint8, device=h.device)
+    out = torch.empty((batch * seq_len, D), device=h.device, dtype=torch.float16)
+    call(
+        "cobra_qkv_attn_fwd", h.data_ptr(), w_qkv.data_ptr(), _ptr(bias), out.data_ptr(), _ptr(bits), ws.data_ptr(),
+        ws.numel(), batch, seq_len, heads, head_dim, float(scale), 1 if causal else 0, _stream(h),
+    )
+    return out
+
+
 PLAN_FUSED = _lib.PLAN_FUSED
 PLAN_STAGED = _lib.PLAN_STAGED
 PLAN_PADDED = _lib.PLAN_PADDED

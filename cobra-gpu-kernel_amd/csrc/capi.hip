@@ -267,6 +267,32 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
   return code(cobra::run_attn(a));
 }
 
+int64_t cobra_qkv_attn_workspace_bytes(int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim) {
+  if (batch < 0 || seq_len < 0 || heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256) return -1;
+  return round256(batch * seq_len * 3 * heads * head_dim * 2);
+}
+
+int cobra_qkv_attn_fwd(const void* h, const void* w_qkv, const float* b_qkv, void* ctx, const uint64_t* key_bits,
+                       void* workspace, int64_t workspace_bytes, int64_t batch, int64_t seq_len, int64_t heads,
+                       int64_t head_dim, float scale, int causal, void* stream) {
+  const int64_t need = cobra_qkv_attn_workspace_bytes(batch, seq_len, heads, head_dim);
+  if (need < 0 || seq_len > 0x7fffffff || heads > 0x7fffffff || !(scale > 0.f)) return kBad;
+  if (!h || !w_qkv || !ctx || !aligned16(h) || !aligned16(w_qkv) || !aligned16(ctx) || !opt_aligned16(b_qkv))
+    return kBad;
+  if (key_bits && (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
+  if (!workspace || !aligned16(workspace) || workspace_bytes < need) return kBad;
+  const int64_t T = batch * seq_len, D = heads * head_dim;
+  if (T == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kF16, workspace, kF16, T, (int)(3 * D), (int)D,
+                       nullptr, nullptr, nullptr, kF16, 1e-5f, s};
+  hipError_t e = cobra::run_gemm(proj);
+  if (e != hipSuccess) return code(e);
+  cobra::AttnArgs at{workspace, ctx, batch, (int)seq_len, (int)heads, (int)head_dim, scale, causal ? 1 : 0, s};
+  at.key_bits = key_bits;
+  return code(cobra::run_attn(at));
+}
+
 int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked, int x_dtype) {
   if (!layer_shape_ok(batch, seq_len, d_model, heads) || !is_dtype(x_dtype)) return -1;
   (void)masked;  // every plan takes a token mask

@@ -481,3 +481,36 @@ def test_persistent_store_variants_agree(B, S, D, H, causal, masked):
     assert torch.equal(y_full, y_gen)
     want = oracle_on(ref, x[[0, B - 1]].float().cpu(), causal, "cpu", mask=None if m is None else m[[0, B - 1]].cpu())
     assert compare_outputs(want, y_full[[0, B - 1]].float().cpu()).passed
+
+
+@pytest.mark.parametrize("hd,S,causal,masked", [(32, 128, True, False), (64, 77, False, True), (256, 40, True, True),
+                                                 (8, 300, False, False)])
+def test_qkv_attn_op(hd, S, causal, masked):
+    """ops.qkv_attn (cobra_qkv_attn_fwd, the counterpart of _tl_qkvattn) equals the
+    projection GEMM followed by the attention op bit for bit, and an fp32 torch
+    reference within tolerance."""
+    from cobra_amd import ops
+
+    torch.manual_seed(hd + S)
+    B, H = 3, 2
+    D = H * hd
+    h = torch.randn(B * S, D, device=DEV).half()
+    w = (torch.randn(3 * D, D, device=DEV) / D ** 0.5).half()
+    b = torch.randn(3 * D, device=DEV) * 0.1
+    m = None
+    if masked:
+        m = torch.rand(B, S, device=DEV) > 0.3
+        m[:, 0] = True
+    got = ops.qkv_attn(h, w, b, B, S, H, hd, hd ** -0.5, causal=causal, key_mask=m)
+    two = ops.attn(ops.linear(h, w, b), B, S, H, hd, hd ** -0.5, causal=causal, key_mask=m)
+    assert torch.equal(got, two)
+    qkv = (h.float() @ w.float().t() + b).half().float()
+    q, k, v = qkv.view(B, S, 3, H, hd).permute(2, 0, 3, 1, 4)
+    s = (q @ k.transpose(-2, -1).contiguous()) * hd ** -0.5
+    dead = torch.zeros(B, 1, S, S, dtype=torch.bool, device=DEV)
+    if causal:
+        dead = dead | torch.ones(S, S, dtype=torch.bool, device=DEV).triu(1)
+    if masked:
+        dead = dead | ~m[:, None, None, :]
+    want = (torch.softmax(s.masked_fill(dead, float("-inf")), -1) @ v).transpose(1, 2).reshape(B * S, D)
+    assert torch.allclose(got.float(), want, atol=2e-3, rtol=1e-2), (got.float() - want).abs().max()
