@@ -15,7 +15,7 @@ from typing import Optional
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcobra_amd.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 F16 = 0
 F32 = 1
@@ -71,6 +71,12 @@ SIGNATURES = {
     ),
     "cobra_layer_run": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "cobra_layer_unbind": (None, [_vp]),
+    "cobra_block_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "cobra_block_fwd": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_f32, _vp],
+    ),
     "cobra_layer_fwd_noalloc": (
         _c_int,
         [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

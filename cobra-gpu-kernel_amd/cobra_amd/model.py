@@ -206,6 +206,8 @@ class CobraTransformer(nn.Module):
         bits = None if m is None else ops.mask_bits(m.view(B, S))
         out16 = x.dtype == torch.float16
         n = len(packs)
+        if ops.block_plan(B, S, D, H, cfg.ffn_dim) == 1:
+            return self._run_blocks(x, m, packs).view(B, S, D)
 
         # Layer 0's LN1 rides in its QKV projection where the row fits one k-tile.
         fold_ln1 = ops.ln_linear_ok(D, x.dtype)
@@ -235,6 +237,31 @@ class CobraTransformer(nn.Module):
                 _, h = ops.add_ln(r, None, mrow, nw, nb, cast_fp16=norm16, eps=eps, store_resid=False,
                                   mask_out=last)
         return h.view(B, S, D)
+
+    def _run_blocks(self, x: torch.Tensor, m: Optional[torch.Tensor], packs: List[_BlockPack]) -> torch.Tensor:
+        """One launch per block (``cobra_block_fwd``) for the shapes the whole-block kernel
+        takes: layer 0's norm1 by the LayerNorm kernel (which also widens x into the fp32
+        residual), then each block reads h = norm1(r) and r, updates r in place and writes
+        the next block's h (ping-pong buffers: every workgroup of a sequence reads all of
+        its h rows) or, on the last block, final_norm's output with the row mask."""
+        cfg = self.config
+        B, S, D = x.shape
+        T = B * S
+        eps = self.final_norm.eps
+        r, h = ops.add_ln(x.view(T, D), None, None, packs[0].ln1_w, packs[0].ln1_b, cast_fp16=True, eps=eps,
+                          store_resid=True)
+        h_next = torch.empty_like(h) if len(packs) > 1 else None
+        out = None
+        for i, p in enumerate(packs):
+            last = i == len(packs) - 1
+            nw, nb = self._final if last else (packs[i + 1].ln1_w, packs[i + 1].ln1_b)
+            out = torch.empty((T, D), device=x.device, dtype=x.dtype) if last else h_next
+            ops.block_fwd(h, r, p.w_qkv, p.b_qkv, p.w_o, p.b_o, p.ln2_w, p.ln2_b, p.w1, p.b1, p.w2, p.b2, nw, nb,
+                          r, out, B, S, cfg.num_heads, cfg.causal, eps=eps,
+                          valid_mask=None if m is None else m.view(T), mask_out=last and m is not None)
+            if not last:
+                h, h_next = out, h
+        return out
 
     def _run_graphed(self, x, m, packs):
         if self._graph is None:

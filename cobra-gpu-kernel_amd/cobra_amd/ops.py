@@ -445,6 +445,64 @@ def layer_fwd_args(x, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, wor
             B, S, D, heads, 1 if causal else 0, float(eps), _stream(x)]
 
 
+def block_plan(batch: int, seq_len: int, d_model: int, heads: int, ffn_dim: int) -> int:
+    """``cobra_block_plan``: -1 the whole-block kernel does not take the shape, 0 it does
+    but composing the per-op kernels is expected to be faster, 1 it does and is preferred."""
+    return int(_lib.lib().cobra_block_plan(batch, seq_len, d_model, heads, ffn_dim))
+
+
+def block_fwd(
+    h: torch.Tensor,
+    r: torch.Tensor,
+    w_qkv: torch.Tensor,
+    b_qkv: torch.Tensor,
+    w_o: torch.Tensor,
+    b_o: torch.Tensor,
+    ln2_w: torch.Tensor,
+    ln2_b: torch.Tensor,
+    w1: torch.Tensor,
+    b1: torch.Tensor,
+    w2: torch.Tensor,
+    b2: torch.Tensor,
+    lnn_w: torch.Tensor,
+    lnn_b: torch.Tensor,
+    r_out: torch.Tensor,
+    out: torch.Tensor,
+    batch: int,
+    seq_len: int,
+    heads: int,
+    causal: bool,
+    eps: float = 1e-5,
+    valid_mask: Optional[torch.Tensor] = None,
+    mask_out: bool = False,
+) -> None:
+    """One transformer block of the fused stack in one launch (``cobra_block_fwd``; the
+    loop body of the reference's ``_run_fused``, TTB:1216-1267): ``h = norm1(r)`` fp16
+    and the fp32 residual ``r`` in; the block's residual to ``r_out`` (may be ``r``) and
+    the next norm's output (``lnn``; ``final_norm`` with ``mask_out`` on the last block)
+    to ``out`` (fp16 or fp32).  ``valid_mask``: optional [B, S] uint8, 0 = padded token.
+    """
+    T, D = h.shape
+    F = w1.shape[0]
+    if h.dtype != torch.float16 or r.dtype != torch.float32 or r_out.dtype != torch.float32:
+        raise TypeError("h is float16, r and r_out float32")
+    if T != batch * seq_len or r.shape != (T, D) or r_out.shape != (T, D) or out.shape != (T, D):
+        raise ValueError("h, r, r_out and out must be [batch * seq_len, d_model]")
+    if tuple(w1.shape) != (F, D) or tuple(w2.shape) != (D, F):
+        raise ValueError(f"w1 must be [F, {D}] and w2 [{D}, F]")
+    for name, t in (("h", h), ("r", r), ("r_out", r_out), ("out", out)):
+        _dev(t, name)
+    if valid_mask is not None:
+        _dev(valid_mask, "valid_mask")
+        if valid_mask.dtype != torch.uint8 or valid_mask.numel() != T:
+            raise ValueError("valid_mask must be uint8 with batch * seq_len elements")
+    call("cobra_block_fwd", h.data_ptr(), r.data_ptr(), _ptr(valid_mask), w_qkv.data_ptr(), b_qkv.data_ptr(),
+         w_o.data_ptr(), b_o.data_ptr(), ln2_w.data_ptr(), ln2_b.data_ptr(), w1.data_ptr(), b1.data_ptr(),
+         w2.data_ptr(), b2.data_ptr(), lnn_w.data_ptr(), lnn_b.data_ptr(), r_out.data_ptr(), out.data_ptr(),
+         _dtype_code(out, "out"), 1 if mask_out else 0, batch, seq_len, D, heads, F, 1 if causal else 0, float(eps),
+         _stream(h))
+
+
 NOALLOC_MAX_BYTES = _lib.NOALLOC_MAX_BYTES
 
 

@@ -448,4 +448,37 @@ int cobra_layer_fwd_noalloc(const void* x, int x_dtype, const uint8_t* valid_mas
                          ws, need, batch, seq_len, d_model, heads, causal, eps, stream);
 }
 
+int cobra_block_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int64_t ffn_dim) {
+  if (batch < 0 || !cobra::block_split_ok(seq_len, d_model, heads, ffn_dim)) return -1;
+  return cobra::block_split_pays(batch, seq_len) ? 1 : 0;
+}
+
+int cobra_block_fwd(const void* h, const float* r, const uint8_t* valid_mask, const void* w_qkv, const float* b_qkv,
+                    const void* w_o, const float* b_o, const float* ln2_w, const float* ln2_b, const void* w1,
+                    const float* b1, const void* w2, const float* b2, const float* lnn_w, const float* lnn_b,
+                    float* r_out, void* out, int out_dtype, int mask_out, int64_t batch, int64_t seq_len,
+                    int64_t d_model, int64_t heads, int64_t ffn_dim, int causal, float eps, void* stream) {
+  if (cobra_block_plan(batch, seq_len, d_model, heads, ffn_dim) < 0 || !is_dtype(out_dtype)) return kBad;
+  const void* must[] = {h, r, w_qkv, b_qkv, w_o, b_o, ln2_w, ln2_b, w1, b1, w2, b2, lnn_w, lnn_b, r_out, out};
+  for (const void* p : must)
+    if (!p || !aligned16(p)) return kBad;
+  if (mask_out && !valid_mask) return kBad;
+  // out must not overlap h (every workgroup of a sequence reads all of its h rows) or r.
+  const int64_t T = batch * seq_len;
+  auto overlaps = [](const void* a, int64_t na, const void* b, int64_t nb) {
+    const char* pa = static_cast<const char*>(a);
+    const char* pb = static_cast<const char*>(b);
+    return pa < pb + nb && pb < pa + na;
+  };
+  const int64_t hb = T * d_model * 2, rb = T * d_model * 4, ob = T * d_model * dtype_bytes(out_dtype);
+  if (overlaps(out, ob, h, hb) || overlaps(out, ob, r, rb) || overlaps(out, ob, r_out, rb) ||
+      overlaps(r_out, rb, h, hb) || (r_out != r && overlaps(r_out, rb, r, rb)))
+    return kBad;
+  cobra::BlockArgs a{h,     r,     valid_mask, w_qkv, b_qkv,    w_o,     b_o,   ln2_w, ln2_b,
+                     w1,    b1,    w2,         b2,    lnn_w,    lnn_b,   r_out, out,   out_dtype,
+                     mask_out ? 1 : 0, batch, seq_len, d_model, heads, ffn_dim, causal ? 1 : 0, eps,
+                     static_cast<hipStream_t>(stream)};
+  return code(cobra::run_block_split(a));
+}
+
 }  // extern "C"

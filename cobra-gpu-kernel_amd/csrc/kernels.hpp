@@ -168,4 +168,39 @@ bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads);
 bool layer_fused_ok(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int x_dtype);
 hipError_t run_layer_small(const SmallLayerArgs& a);
 
+// One transformer block of the fused stack in one launch (the query-split kernel's
+// whole-block mode): h = norm1(r) fp16 in, r fp32 in, r_out / out written.
+struct BlockArgs {
+  const void* h;           // [B*S, D] fp16
+  const float* r;          // [B*S, D] fp32 (r_out may equal r)
+  const uint8_t* valid_mask;  // optional [B, S], 0 = padded
+  const void* w_qkv;       // [3D, D] fp16
+  const float* b_qkv;
+  const void* w_o;         // [D, D] fp16
+  const float* b_o;
+  const float* ln2_w;
+  const float* ln2_b;
+  const void* w1;          // [F, D] fp16
+  const float* b1;
+  const void* w2;          // [D, F] fp16
+  const float* b2;
+  const float* lnn_w;      // next norm
+  const float* lnn_b;
+  float* r_out;            // [B*S, D] fp32
+  void* out;               // [B*S, D] out_dtype
+  int out_dtype;
+  int mask_out;
+  int64_t batch;
+  int64_t seq_len;
+  int64_t d_model;
+  int64_t heads;
+  int64_t ffn_dim;
+  int causal;
+  float eps;
+  hipStream_t stream;
+};
+bool block_split_ok(int64_t seq_len, int64_t d_model, int64_t heads, int64_t ffn_dim);
+bool block_split_pays(int64_t batch, int64_t seq_len);
+hipError_t run_block_split(const BlockArgs& a);
+
 }  // namespace cobra

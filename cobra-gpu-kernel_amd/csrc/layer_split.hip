@@ -151,14 +151,31 @@ __device__ __forceinline__ f16x8 tile_chunk(const char* tile, int r, int c) {
 
 }  // namespace
 
-template <int D, int HD, bool CAUSAL, bool MASKED>
+// The rest of a transformer block, for the whole-block mode of the kernel: the
+// input is then h = norm1(r) (fp16) and the residual r comes from `rin` (fp32).
+struct BlockTail {
+  const float* rin;   // [B*S, D] residual entering the block (may equal the kernel's resid_out)
+  const f16* w1;      // [F, D] ffn_in weight
+  const float* b1;    // [F]
+  const f16* w2;      // [D, F] ffn_out weight
+  const float* b2;    // [D]
+  const float* gn;    // the next norm (next block's norm1, or final_norm)
+  const float* bn;
+  int y_f32;          // output dtype: fp32 if set, else fp16
+  int mask_out;       // multiply the normalised output of padded rows by 0
+};
+
+template <int D, int HD, bool CAUSAL, bool MASKED, bool BLK>
 __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     const f16* __restrict__ x, const f16* __restrict__ wqkv, const float* __restrict__ bqkv,
     const f16* __restrict__ wo, const float* __restrict__ bo, const float* __restrict__ g1,
-    const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, f16* __restrict__ y,
-    float* __restrict__ resid_out, int S, int NS, float c2, float eps, const uint8_t* __restrict__ vmask) {
+    const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, void* __restrict__ yv,
+    float* resid_out, int S, int NS, float c2, float eps, const uint8_t* __restrict__ vmask, BlockTail tail) {
   using P = SplitPlan<D, HD>;
   constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH, NQT = P::NQT;
+  // Whole-block mode: the FFN's hidden width equals d_model, one 32-wide tile per wave.
+  static_assert(!BLK || NNT == kSplitWaves, "whole-block mode: d_model 128");
+  f16* const y = static_cast<f16*>(yv);
 
   __shared__ __attribute__((aligned(1024))) char smem[P::BYTES];
   char* const rA = smem;               // W_k/W_v staging, then K^T | V fragments
@@ -204,8 +221,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 
   // ---- DMA, in the order the data is needed -------------------------------------------
   const RowSpans<D> spans(lane);
-  const bool aff1 = g1 != nullptr;  // LN1 with elementwise affine
-  if (aff1) {  // [gamma1 | beta1] (later vmcnt waits count only what follows the token tile)
+  const bool aff1 = !BLK && g1 != nullptr;  // LN1 with elementwise affine
+  if constexpr (BLK) {  // b1, b2 and the next norm's parameters of tile w, after the other segments
+    const int seg = lane >> 3, off = 32 * w + 4 * (lane & 7);
+    const float* src = seg == 0 ? tail.b1 + off : seg == 1 ? tail.b2 + off : seg == 2 ? tail.gn + off
+                       : seg == 3 ? tail.bn + off : tail.b1 + off;
+    dma16(src, rP + 1024);
+  } else if (aff1) {  // [gamma1 | beta1] (later vmcnt waits count only what follows the token tile)
     const int c = 4 * lane;
     dma16(c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0), rP + 1024);
   }
@@ -253,8 +275,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   };
 
   // ---- LN1 of token 32w + li (columns 16kk + 8g + e): its tile is in. ------------------
-  wait_vmcnt<1 + NV>();
   KeyBits kbits{~0ull, ~0ull};
+  if constexpr (BLK) {
+    // The input is already normalised: the projections read the token tiles as they landed.
+#pragma unroll
+    for (int slot = 0; slot < NSLOT; ++slot) issue_late(slot);
+  } else {
+  wait_vmcnt<1 + NV>();
   if constexpr (MASKED) kbits = key_bits_of(kbytes, S, lane);
   {
     f16x8 xc[KD];
@@ -332,9 +359,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     // (The fragments overwrite the token tile in place: every read of it above
     // precedes the first write.)
   }
+  }
 
   // ---- operand fragments of this wave's weights -------------------------------------------
   wait_vmcnt<P::N_Q>();
+  if constexpr (BLK && MASKED) kbits = key_bits_of(kbytes, S, lane);  // the mask bytes are older
   f16x8 wk[KD], wv[KD];  // A operand of K^T = W_k h^T; B operand of V = h W_v^T
 #pragma unroll
   for (int kk = 0; kk < KD; ++kk) {
@@ -349,6 +378,16 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int kk = 0; kk < KD; ++kk) wq[dt][kk] = tile_chunk<D>(rWq, 32 * dt + li, 2 * kk + g);
   const float* pp = reinterpret_cast<const float*>(rP);  // the 32-float segments above
   lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
+
+  // Whole-block mode: the residual entering the block, row qtok, columns 32w + 8qd + 4g + e
+  // (the out-projection's accumulator layout), loaded before any later transfer so the
+  // wait for the W_o rows covers it.  Rows past S read row 0 of the sequence (unused).
+  f32x4 rres[4];
+  if constexpr (BLK) {
+    const float* rp = tail.rin + ((int64_t)b * S + (q_ok ? qtok : 0)) * D + 32 * w + 4 * g;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) rres[qd] = *reinterpret_cast<const f32x4*>(rp + 8 * qd);
+  }
 
   // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.  A
   // projecting wave issues them between its token tiles, where the matrix cores are
@@ -388,7 +427,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     f16x8 hf[2][KD];
     auto fetch = [&](int t, int buf) {
 #pragma unroll
-      for (int kk = 0; kk < KD; ++kk) hf[buf][kk] = Hb[(t * KD + kk) * 64 + lane];
+      for (int kk = 0; kk < KD; ++kk)
+        hf[buf][kk] = BLK ? tile_chunk<D>(rX + t * P::TILEB, li, 2 * kk + g) : Hb[(t * KD + kk) * 64 + lane];
     };
     // Tile t - 1 is converted and stored a quarter at a time between the products of
     // tile t, each quarter pinned after two products (scheduling barriers): the wave
@@ -466,6 +506,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     }
   }
   lds_barrier();  // K, V of every token tile and head are in LDS
+
+  // Whole-block mode: W1 rows 32w .. 32w+31 (FFN hidden tile w) into the token-tile area,
+  // free now that every projection has read it (the split head writes its probabilities
+  // there, so it takes W1 after the attention).
+  char* const rW1 = rX + w * P::TILEB;
+  char* const rW2 = rQ + w * P::TILEB;
+  if constexpr (BLK && !P::QSPLIT) dma_span_rows<D, P::N_O>(rW1, reinterpret_cast<const char*>(tail.w1 + (int64_t)32 * w * D), spans);
 
   // ---- attention of head w: S^T = K Q^T for all (at most 128) keys at once, one exact
   // softmax pass (no running max, no rescale), O^T = V^T P^T.
@@ -654,7 +701,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int half = 0; half < 2; ++half) Cx[(h * KSH + 2 * dt + half) * 64 + lane] = scaled_f16(ot[dt], half, inv);
   }
-  wait_vmcnt<0>();  // W_o rows (this wave's own transfers: readable without a barrier)
+  // W_o rows (this wave's own transfers: readable without a barrier); W1 may still be in flight.
+  wait_vmcnt<(BLK && !P::QSPLIT) ? P::N_O : 0>();
   // Row li of the W_o tile at the k order of the attention output: columns
   // 16ks + 4g + {0..3} (chunk 2ks) and 16ks + 8 + 4g + {0..3} (chunk 2ks + 1).
   f16x8 wof[KD];
@@ -666,6 +714,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     wof[ks] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
   lds_barrier();    // attention output of every head is in LDS
+  if constexpr (BLK) {  // W2 rows 32w .. 32w+31 (output tile w) into the W_o area, read above
+    if constexpr (P::QSPLIT)
+      dma_span_rows<D, P::N_O>(rW1, reinterpret_cast<const char*>(tail.w1 + (int64_t)32 * w * D), spans);
+    dma_span_rows<D, P::N_O>(rW2, reinterpret_cast<const char*>(tail.w2 + (int64_t)32 * w * D), spans);
+  }
 
   // ---- out^T tile w = W_o[32w..32w+31] ctx^T, + b_o + x, then LN2 ----------------------
   float v[4][4];  // query qtok, column 32w + 8qd + 4g + e
@@ -680,11 +733,19 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int qd = 0; qd < 4; ++qd) {
       const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 128 + 8 * qd + 4 * g);
       // x[qtok][32w + 8qd + 4g + e]: k-step 2w + qd/2, fragment half qd % 2, elements 4g + e.
-      const f16x4 xr = *reinterpret_cast<const f16x4*>(
-          reinterpret_cast<const char*>(Raw + (2 * w + (qd >> 1)) * 64 + li + 32 * (qd & 1)) + 8 * g);
+      float xr[4];
+      if constexpr (BLK) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[e] = rres[qd][e];
+      } else {
+        const f16x4 xh = *reinterpret_cast<const f16x4*>(
+            reinterpret_cast<const char*>(Raw + (2 * w + (qd >> 1)) * 64 + li + 32 * (qd & 1)) + 8 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[e] = (float)xh[e];
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[qd][e] = (qv ? oacc[4 * qd + e] + bb[e] : 0.f) + (float)xr[e];
+        v[qd][e] = (qv ? oacc[4 * qd + e] + bb[e] : 0.f) + xr[e];
         sum += v[qd][e];
         sq = fmaf(v[qd][e], v[qd][e], sq);
       }
@@ -708,7 +769,29 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     }
     const float mean = tot * (1.0f / D);
     const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - mean * mean, 0.f) + eps);
-    if (q_ok) {
+    if constexpr (BLK) {
+      // h2 = LN2(r1) rounded to fp16, into the attention-output area (read by every
+      // wave's out-projection before the barrier above) as the B operand of the FFN:
+      // k-step 2w + half holds columns 32w + 16 half + 4g + {0..3} and + 8.
+      float o[4][4];
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4 gg = *reinterpret_cast<const f32x4*>(pp + 160 + 8 * qd + 4 * g);
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 192 + 8 * qd + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[qd][e] = (v[qd][e] - mean) * rstd * gg[e] + bb[e];
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        f16x8 hh;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hh[e] = (f16)o[2 * half][e];
+          hh[4 + e] = (f16)o[2 * half + 1][e];
+        }
+        Cx[(2 * w + half) * 64 + lane] = hh;
+      }
+    } else if (q_ok) {
       const int64_t row = (int64_t)b * S + qtok;
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
@@ -721,6 +804,98 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         store4(y + row * D + n0, o);
         if (resid_out) store4(resid_out + row * D + n0, v[qd]);
       }
+    }
+  }
+  if constexpr (!BLK) return;
+
+  // ---- whole-block mode: FFN and the next norm (TTB:1255-1267) ----------------------------
+  // Row li of a W1 / W2 tile at the k order of the fragments the accumulators produce
+  // (the same order as the W_o rows above).
+  auto row_frags = [&](const char* tile, f16x8 (&f)[KD]) {
+#pragma unroll
+    for (int ks = 0; ks < KD; ++ks) {
+      const char* row = tile + li * 2 * D + 8 * g;
+      const f16x4 lo = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks) ^ row_swz<D>(li)));
+      const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16 * ((2 * ks + 1) ^ row_swz<D>(li)));
+      f[ks] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+  const float* pt = reinterpret_cast<const float*>(rP + 1024);  // b1 | b2 | gn | bn of tile w
+  f16x8* const Hid = Raw;  // FFN hidden fragments (the residual area is unused in this mode)
+  wait_vmcnt<P::N_O>();    // W1 rows (W2 may still be in flight)
+  f16x8 w1f[KD];
+  row_frags(rW1, w1f);
+  lds_barrier();  // h2 of every column tile is in LDS
+  {
+    // hid^T tile w = W1[32w .. 32w+31] h2^T, + b1, exact GELU, fp16 (TTB:1260)
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KD; ++ks) acc = mfma32x32x16(w1f[ks], Cx[ks * 64 + lane], acc);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      f16x8 hh;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = 8 * half + j;
+        hh[j] = (f16)gelu_erf(acc[r] + pt[8 * (r >> 2) + 4 * g + (r & 3)]);
+      }
+      Hid[(2 * w + half) * 64 + lane] = hh;
+    }
+  }
+  wait_vmcnt<0>();  // W2 rows
+  f16x8 w2f[KD];
+  row_frags(rW2, w2f);
+  lds_barrier();  // hidden activations of every tile are in LDS
+  // r2 = (r1 + hid W2^T + b2) * row_valid (TTB:144-145), then the next norm.
+  const float rv = (!MASKED || kbits.valid(qtok)) ? 1.f : 0.f;
+  sum = 0.f;
+  sq = 0.f;
+  {
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KD; ++ks) acc = mfma32x32x16(w2f[ks], Hid[ks * 64 + lane], acc);
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const f32x4 bb = *reinterpret_cast<const f32x4*>(pt + 32 + 8 * qd + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[qd][e] = (acc[4 * qd + e] + bb[e] + v[qd][e]) * rv;
+        sum += v[qd][e];
+        sq = fmaf(v[qd][e], v[qd][e], sq);
+      }
+    }
+  }
+  sum = sum_xor32(sum);
+  sq = sum_xor32(sq);
+  if (g == 0) {
+    Stat[w * 32 + li] = sum;
+    Stat[(kSplitWaves + w) * 32 + li] = sq;
+  }
+  lds_barrier();
+  float tot = 0.f, tsq = 0.f;
+#pragma unroll
+  for (int n = 0; n < NNT; ++n) {
+    tot += Stat[n * 32 + li];
+    tsq += Stat[(kSplitWaves + n) * 32 + li];
+  }
+  const float mean = tot * (1.0f / D);
+  const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - mean * mean, 0.f) + eps);
+  const float om = tail.mask_out ? rv : 1.f;
+  if (q_ok) {
+    const int64_t row = (int64_t)b * S + qtok;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int n0 = 32 * w + 8 * qd + 4 * g;
+      const f32x4 gg = *reinterpret_cast<const f32x4*>(pt + 64 + 8 * qd + 4 * g);
+      const f32x4 bb = *reinterpret_cast<const f32x4*>(pt + 96 + 8 * qd + 4 * g);
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = ((v[qd][e] - mean) * rstd * gg[e] + bb[e]) * om;
+      if (tail.y_f32)
+        store4(static_cast<float*>(yv) + row * D + n0, o);
+      else
+        store4(y + row * D + n0, o);
+      store4(resid_out + row * D + n0, v[qd]);
     }
   }
 }
@@ -746,16 +921,11 @@ static hipError_t launch_split(const SmallLayerArgs& a, float c2) {
   const int ns = (int)((a.seq_len + 31) / 32);
   const int64_t grid = a.batch * ns;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  if (a.valid_mask)
-    hipLaunchKernelGGL((layer_split_kernel<D, HD, CAUSAL, true>), dim3((unsigned)grid), dim3(64 * kSplitWaves), 0,
-                       a.stream, static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
-                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
-                       static_cast<f16*>(a.y), a.resid_out, (int)a.seq_len, ns, c2, a.eps, a.valid_mask);
-  else
-    hipLaunchKernelGGL((layer_split_kernel<D, HD, CAUSAL, false>), dim3((unsigned)grid), dim3(64 * kSplitWaves), 0,
-                       a.stream, static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv,
-                       static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w, a.ln1_b, a.ln2_w, a.ln2_b,
-                       static_cast<f16*>(a.y), a.resid_out, (int)a.seq_len, ns, c2, a.eps, nullptr);
+  auto kern = a.valid_mask ? layer_split_kernel<D, HD, CAUSAL, true, false> : layer_split_kernel<D, HD, CAUSAL, false, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, static_cast<const f16*>(a.x),
+                     static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w,
+                     a.ln1_b, a.ln2_w, a.ln2_b, a.y, a.resid_out, (int)a.seq_len, ns, c2, a.eps, a.valid_mask,
+                     BlockTail{});
   return hipGetLastError();
 }
 
@@ -774,6 +944,49 @@ static hipError_t split_shape(const SmallLayerArgs& a, float c2) {
 // Shape and dtype checks are the caller's (run_layer_small: layer_split_ok, layer_split_pays).
 hipError_t run_layer_split(const SmallLayerArgs& a, float c2) {
   return a.causal ? split_shape<true>(a, c2) : split_shape<false>(a, c2);
+}
+
+// ---- whole-block mode -------------------------------------------------------------------
+
+bool block_split_ok(int64_t seq_len, int64_t d_model, int64_t heads, int64_t ffn_dim) {
+  return d_model == 128 && ffn_dim == 128 && layer_split_ok(seq_len, d_model, heads);
+}
+
+bool block_split_pays(int64_t batch, int64_t seq_len) {
+  return batch * ((seq_len + 31) / 32) <= 2 * (int64_t)compute_units();
+}
+
+template <int HD, bool CAUSAL>
+static hipError_t launch_block(const BlockArgs& a, float c2) {
+  const int ns = (int)((a.seq_len + 31) / 32);
+  const int64_t grid = a.batch * ns;
+  if (grid > 0x7fffffff) return hipErrorInvalidValue;
+  const BlockTail tail{a.r, static_cast<const f16*>(a.w1), a.b1, static_cast<const f16*>(a.w2), a.b2, a.lnn_w,
+                       a.lnn_b, a.out_dtype == kF32, a.mask_out};
+  auto kern = a.valid_mask ? layer_split_kernel<128, HD, CAUSAL, true, true> : layer_split_kernel<128, HD, CAUSAL, false, true>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, static_cast<const f16*>(a.h),
+                     static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<const f16*>(a.w_o), a.b_o, nullptr, nullptr,
+                     a.ln2_w, a.ln2_b, a.out, a.r_out, (int)a.seq_len, ns, c2, a.eps, a.valid_mask, tail);
+  return hipGetLastError();
+}
+
+template <bool CAUSAL>
+static hipError_t block_shape(const BlockArgs& a, float c2) {
+  switch (a.d_model / a.heads) {
+    case 8: return launch_block<8, CAUSAL>(a, c2);
+    case 32: return launch_block<32, CAUSAL>(a, c2);
+    case 64: return launch_block<64, CAUSAL>(a, c2);
+    default: return launch_block<128, CAUSAL>(a, c2);
+  }
+}
+
+hipError_t run_block_split(const BlockArgs& a) {
+  if (!block_split_ok(a.seq_len, a.d_model, a.heads, a.ffn_dim) || a.batch < 0 || a.batch > 0x7fffffff)
+    return hipErrorInvalidValue;
+  if (a.batch == 0) return hipSuccess;
+  const double hd = (double)(a.d_model / a.heads);
+  const float c2 = (float)(1.0 / sqrt(hd)) * 1.4426950408889634f;  // as the sublayer mode
+  return a.causal ? block_shape<true>(a, c2) : block_shape<false>(a, c2);
 }
 
 }  // namespace cobra

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 8
+#define COBRA_ABI_VERSION 9
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
 
@@ -254,6 +254,40 @@ int cobra_layer_fwd_noalloc(const void* x, int x_dtype, const uint8_t* valid_mas
                             const float* ln1_b, const float* ln2_w, const float* ln2_b, void* y, float* resid_out,
                             int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int causal, float eps,
                             void* stream);
+
+/*
+ * One whole transformer block of the reference's fused stack in one launch
+ * (replaces the loop body of _run_fused, torch_transformer_benchmark.py:1216-1267,
+ * fuse_ln branch: _tl_attn / _tl_qkvattn, _tl_linear_ln, _tl_linear(gelu),
+ * _tl_linear_ln):
+ *   r1  = r + mask_branch(attention(h) W_o^T + b_o)      (fp32)
+ *   h2  = LN2(r1)                                        (fp16)
+ *   f   = gelu(h2 W1^T + b1)                             (fp16, exact erf GELU)
+ *   r2  = (r1 + f W2^T + b2) * row_valid                 (fp32 -> r_out)
+ *   out = LNn(r2) [* row_valid if mask_out]              (out_dtype)
+ * h = norm1(r) in fp16 (the previous block's epilogue, or a LayerNorm of the
+ * model input for block 0); r fp32.  LNn is the next block's norm1, or
+ * final_norm for the last block (then mask_out = 1 with a token mask, and
+ * out_dtype the model's).  Weights: w_qkv [3D, D] (q | k | v rows), w_o [D, D],
+ * w1 [F, D], w2 [D, F] fp16; biases and LayerNorm parameters fp32.
+ * r_out may equal r (in place); out must not overlap h, r or r_out, and r_out
+ * must not overlap h.  Shapes: cobra_block_plan() >= 0 (d_model 128,
+ * ffn_dim 128, seq_len <= 128, head_dim 8 / 32 / 64 / 128).  No workspace.
+ */
+int cobra_block_fwd(const void* h, const float* r, const uint8_t* valid_mask, const void* w_qkv, const float* b_qkv,
+                    const void* w_o, const float* b_o, const float* ln2_w, const float* ln2_b, const void* w1,
+                    const float* b1, const void* w2, const float* b2, const float* lnn_w, const float* lnn_b,
+                    float* r_out, void* out, int out_dtype, int mask_out, int64_t batch, int64_t seq_len,
+                    int64_t d_model, int64_t heads, int64_t ffn_dim, int causal, float eps, void* stream);
+
+/*
+ * Whether cobra_block_fwd takes a shape: -1 no; 0 yes, but composing the
+ * per-op entry points is expected to be faster (more than two rounds of
+ * workgroups: every workgroup recomputes its sequence's K and V); 1 yes and
+ * preferred.  (The reference gates its fused paths by shape the same way,
+ * torch_transformer_benchmark.py:1030-1071.)
+ */
+int cobra_block_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int64_t ffn_dim);
 
 #ifdef __cplusplus
 }
