@@ -25,9 +25,14 @@ and GEMM operands in fp16 (the reference's fused policy, TTB:1170-1290):
                                         the output row mask on the last block
 
 The op order and roundings are the reference's; the output is x.dtype.
-Small inputs (<= 64 MiB, TTB:1077-1079) replay a captured hipGraph of the
-whole forward with static input / mask buffers (TTB:1331-1360); inputs that
-do not fit one device pass stream in batch chunks (TTB:1364-1508).
+At d_model 128, ffn_dim 128, seq_len <= 128 (head_dim 8 / 32 / 64 / 128) and
+batches of at most two rounds of workgroups, each block is ONE launch
+(``cobra_block_fwd``: the query-split kernel's whole-block mode) fed by one
+LayerNorm launch for layer 0's norm1; the GELU there uses a branch-free erf
+(Abramowitz & Stegun 7.1.26, |error| <= 1.5e-7).  Those forwards launch directly;
+other shapes replay a captured hipGraph of the whole forward for small inputs
+(<= 64 MiB, TTB:1077-1079) with static input / mask buffers (TTB:1331-1360);
+inputs that do not fit one device pass stream in batch chunks (TTB:1364-1508).
 """
 
 from __future__ import annotations
@@ -159,7 +164,12 @@ class CobraTransformer(nn.Module):
         masked = valid_token_mask is not None
         sig = (tuple(x.shape), x.dtype, x.device, masked)
         if sig != self._sig:
-            self._graph_ok = (self.graph if self.graph is not None else True) and \
+            # Automatic: replay a hipGraph for the composed forward (five launches per
+            # block); launch the one-kernel-per-block forward directly, which measured
+            # faster than its graph replay at B >= 4 (56 vs 62 us at case 1).
+            cfg = self.config
+            blocks = ops.block_plan(x.shape[0], x.shape[1], cfg.d_model, cfg.num_heads, cfg.ffn_dim) == 1
+            self._graph_ok = (self.graph if self.graph is not None else not blocks) and \
                 x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
             self._graph = None
             self._static_x = self._static_m = self._static_out = None

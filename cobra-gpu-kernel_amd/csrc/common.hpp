@@ -146,6 +146,23 @@ __device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
 // operation order: v * 0.5 * (1 + erf(v / sqrt(2))) (TTB:326-328).
 __device__ __forceinline__ float gelu_erf(float v) { return v * 0.5f * (1.0f + erff(v * 0.7071067811865476f)); }
 
+// The same GELU without branches, for epilogues where a handful of values per lane
+// sit on the critical path: erf from Abramowitz & Stegun 7.1.26,
+//   erf(z) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),  t = 1 / (1 + p z),
+// |error| <= 1.5e-7 for z >= 0 (one reciprocal, one exp2, six fma).  1 + erf(v / sqrt 2) is
+// formed as 2 - q (v >= 0) or q (v < 0) with q = 1 - erf(|v| / sqrt 2), so the negative
+// tail keeps its small values instead of cancelling against 1.
+__device__ __forceinline__ float gelu_erf_fast(float v) {
+  const float z = fabsf(v) * 0.7071067811865476f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  const float q = poly * t * __builtin_amdgcn_exp2f(v * v * -0.7213475204444817f);  // exp(-v^2 / 2)
+  return v * 0.5f * (v >= 0.f ? 2.0f - q : q);
+}
+
 // Workgroup-id remap so that consecutive logical tiles land on the same XCD
 // (the hardware deals workgroups round-robin over 8 XCDs, each with its own
 // L2).  A bijection on [0, n) for any n.

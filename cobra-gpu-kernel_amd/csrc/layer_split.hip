@@ -724,9 +724,14 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   float v[4][4];  // query qtok, column 32w + 8qd + 4g + e
   float sum = 0.f, sq = 0.f;
   if (w < NNT) {
+    // Every attention-output fragment is requested before the first product (one wait).
+    f16x8 cf[KD];
+#pragma unroll
+    for (int ks = 0; ks < KD; ++ks) cf[ks] = Cx[ks * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 oacc = zero16();
 #pragma unroll
-    for (int ks = 0; ks < KD; ++ks) oacc = mfma32x32x16(wof[ks], Cx[ks * 64 + lane], oacc);
+    for (int ks = 0; ks < KD; ++ks) oacc = mfma32x32x16(wof[ks], cf[ks], oacc);
     // A padded query's attention output is zero (masked_fill before the residual add).
     const bool qv = !MASKED || kbits.valid(qtok);
 #pragma unroll
@@ -822,22 +827,35 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   };
   const float* pt = reinterpret_cast<const float*>(rP + 1024);  // b1 | b2 | gn | bn of tile w
   f16x8* const Hid = Raw;  // FFN hidden fragments (the residual area is unused in this mode)
+  // The bias rows of this lane's accumulator registers (4qd + e: row 8qd + 4g + e), in
+  // registers before the products rather than one LDS round trip per element after them.
+  f32x4 b1v[4], b2v[4];
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    b1v[qd] = *reinterpret_cast<const f32x4*>(pt + 8 * qd + 4 * g);
+    b2v[qd] = *reinterpret_cast<const f32x4*>(pt + 32 + 8 * qd + 4 * g);
+  }
   wait_vmcnt<P::N_O>();    // W1 rows (W2 may still be in flight)
   f16x8 w1f[KD];
   row_frags(rW1, w1f);
   lds_barrier();  // h2 of every column tile is in LDS
   {
-    // hid^T tile w = W1[32w .. 32w+31] h2^T, + b1, exact GELU, fp16 (TTB:1260)
+    // hid^T tile w = W1[32w .. 32w+31] h2^T, + b1, exact GELU, fp16 (TTB:1260).  Every
+    // operand fragment is requested before the first product, so one wait covers them.
+    f16x8 hb[KD];
+#pragma unroll
+    for (int ks = 0; ks < KD; ++ks) hb[ks] = Cx[ks * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 acc = zero16();
 #pragma unroll
-    for (int ks = 0; ks < KD; ++ks) acc = mfma32x32x16(w1f[ks], Cx[ks * 64 + lane], acc);
+    for (int ks = 0; ks < KD; ++ks) acc = mfma32x32x16(w1f[ks], hb[ks], acc);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       f16x8 hh;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int r = 8 * half + j;
-        hh[j] = (f16)gelu_erf(acc[r] + pt[8 * (r >> 2) + 4 * g + (r & 3)]);
+        hh[j] = (f16)gelu_erf_fast(acc[r] + b1v[r >> 2][r & 3]);
       }
       Hid[(2 * w + half) * 64 + lane] = hh;
     }
@@ -851,12 +869,16 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   sum = 0.f;
   sq = 0.f;
   {
+    f16x8 hf2[KD];
+#pragma unroll
+    for (int ks = 0; ks < KD; ++ks) hf2[ks] = Hid[ks * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 acc = zero16();
 #pragma unroll
-    for (int ks = 0; ks < KD; ++ks) acc = mfma32x32x16(w2f[ks], Hid[ks * 64 + lane], acc);
+    for (int ks = 0; ks < KD; ++ks) acc = mfma32x32x16(w2f[ks], hf2[ks], acc);
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(pt + 32 + 8 * qd + 4 * g);
+      const f32x4 bb = b2v[qd];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[qd][e] = (acc[4 * qd + e] + bb[e] + v[qd][e]) * rv;
