@@ -53,8 +53,8 @@ namespace {
 constexpr int kSplitWaves = 4;
 constexpr int kSplitTiles = kSmallMaxS / 32;  // token tiles of a sequence
 
-// LDS plan (bytes) and per-wave DMA counts.
-template <int D, int HD>
+// LDS plan (bytes) and per-wave DMA counts; BLK: the whole-block mode.
+template <int D, int HD, bool BLK>
 struct SplitPlan {
   static constexpr int KD = D / 16;    // k-steps over d_model
   static constexpr int NNT = D / 32;   // 32-wide tiles of d_model
@@ -77,8 +77,11 @@ struct SplitPlan {
   static constexpr int X = kSplitWaves * TILEB;        // token tiles, then LN1 output fragments
   static constexpr int Q = D * ROWB;                   // W_q rows, then W_o rows
   static constexpr int CX = KD * 1024;                 // attention output fragments
-  static constexpr int RAWB = KD * 1024;               // raw fragments of the slice's token tile (the residual)
-  static constexpr int PB = 2048;                      // parameter rows of one wave, then [gamma1 | beta1]
+  // The residual of the slice: raw fp16 fragments of its token tile, or (whole-block
+  // mode) the fp32 rows of the block's residual, 4 KB per wave.
+  static constexpr int RAWB = BLK ? kSplitWaves * 4096 : KD * 1024;
+  // Parameter rows of one wave, then [gamma1 | beta1] (or, whole-block mode, b1 | b2 | the next norm).
+  static constexpr int PB = BLK ? 1536 : 2048;
   static constexpr int OFF_X = A, OFF_Q = OFF_X + X, OFF_CX = OFF_Q + Q, OFF_R = OFF_CX + CX;
   static constexpr int OFF_P = OFF_R + RAWB, OFF_STAT = OFF_P + kSplitWaves * PB;
   static constexpr int BYTES = OFF_STAT + 2 * kSplitWaves * 32 * 4;
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     const f16* __restrict__ wo, const float* __restrict__ bo, const float* __restrict__ g1,
     const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, void* __restrict__ yv,
     float* resid_out, int S, int NS, float c2, float eps, const uint8_t* __restrict__ vmask, BlockTail tail) {
-  using P = SplitPlan<D, HD>;
+  using P = SplitPlan<D, HD, BLK>;
   constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH, NQT = P::NQT;
   // Whole-block mode: the FFN's hidden width equals d_model, one 32-wide tile per wave.
   static_assert(!BLK || NNT == kSplitWaves, "whole-block mode: d_model 128");
@@ -222,11 +225,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   // ---- DMA, in the order the data is needed -------------------------------------------
   const RowSpans<D> spans(lane);
   const bool aff1 = !BLK && g1 != nullptr;  // LN1 with elementwise affine
-  if constexpr (BLK) {  // b1, b2 and the next norm's parameters of tile w, after the other segments
+  if constexpr (BLK) {  // b1, b2 and the next norm's parameters of tile w (512 bytes: lanes 0-31)
     const int seg = lane >> 3, off = 32 * w + 4 * (lane & 7);
-    const float* src = seg == 0 ? tail.b1 + off : seg == 1 ? tail.b2 + off : seg == 2 ? tail.gn + off
-                       : seg == 3 ? tail.bn + off : tail.b1 + off;
-    dma16(src, rP + 1024);
+    const float* src = seg == 0 ? tail.b1 + off : seg == 1 ? tail.b2 + off : seg == 2 ? tail.gn + off : tail.bn + off;
+    if (lane < 32) dma16(src, rP + 1024);
   } else if (aff1) {  // [gamma1 | beta1] (later vmcnt waits count only what follows the token tile)
     const int c = 4 * lane;
     dma16(c < D ? g1 + c : be1 + (c < 2 * D ? c - D : 0), rP + 1024);
@@ -379,14 +381,21 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   const float* pp = reinterpret_cast<const float*>(rP);  // the 32-float segments above
   lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
 
-  // Whole-block mode: the residual entering the block, row qtok, columns 32w + 8qd + 4g + e
-  // (the out-projection's accumulator layout), loaded before any later transfer so the
-  // wait for the W_o rows covers it.  Rows past S read row 0 of the sequence (unused).
-  f32x4 rres[4];
+  // Whole-block mode: the residual entering the block, rows of the slice x columns
+  // 32w .. 32w+31 (fp32, 128 bytes a row), into this wave's 4 KB of the residual area,
+  // before any later transfer so the wait for the W_o rows covers it.  16-byte chunk c of
+  // row r sits at chunk c ^ (r & 7): the epilogue's reads (32 rows, one chunk) are then
+  // conflict-free.  (Held in registers instead, the rows were moved to spill registers
+  // as soon as they were requested, a wait for every transfer in flight.)  Rows past S
+  // read row 0 of the sequence (unused).
+  char* const rRes = smem + P::OFF_R + w * 4096;
   if constexpr (BLK) {
-    const float* rp = tail.rin + ((int64_t)b * S + (q_ok ? qtok : 0)) * D + 32 * w + 4 * g;
 #pragma unroll
-    for (int qd = 0; qd < 4; ++qd) rres[qd] = *reinterpret_cast<const f32x4*>(rp + 8 * qd);
+    for (int i = 0; i < 4; ++i) {
+      const int r = 8 * i + (lane >> 3), c = (lane & 7) ^ (r & 7);
+      const int tok = 32 * s + r < S ? 32 * s + r : 0;
+      dma16(tail.rin + ((int64_t)b * S + tok) * D + 32 * w + 4 * c, rRes + 1024 * i);
+    }
   }
 
   // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.  A
@@ -506,13 +515,6 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     }
   }
   lds_barrier();  // K, V of every token tile and head are in LDS
-
-  // Whole-block mode: W1 rows 32w .. 32w+31 (FFN hidden tile w) into the token-tile area,
-  // free now that every projection has read it (the split head writes its probabilities
-  // there, so it takes W1 after the attention).
-  char* const rW1 = rX + w * P::TILEB;
-  char* const rW2 = rQ + w * P::TILEB;
-  if constexpr (BLK && !P::QSPLIT) dma_span_rows<D, P::N_O>(rW1, reinterpret_cast<const char*>(tail.w1 + (int64_t)32 * w * D), spans);
 
   // ---- attention of head w: S^T = K Q^T for all (at most 128) keys at once, one exact
   // softmax pass (no running max, no rescale), O^T = V^T P^T.
@@ -701,8 +703,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int half = 0; half < 2; ++half) Cx[(h * KSH + 2 * dt + half) * 64 + lane] = scaled_f16(ot[dt], half, inv);
   }
-  // W_o rows (this wave's own transfers: readable without a barrier); W1 may still be in flight.
-  wait_vmcnt<(BLK && !P::QSPLIT) ? P::N_O : 0>();
+  wait_vmcnt<0>();  // W_o rows (this wave's own transfers: readable without a barrier)
   // Row li of the W_o tile at the k order of the attention output: columns
   // 16ks + 4g + {0..3} (chunk 2ks) and 16ks + 8 + 4g + {0..3} (chunk 2ks + 1).
   f16x8 wof[KD];
@@ -714,11 +715,13 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     wof[ks] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
   lds_barrier();    // attention output of every head is in LDS
-  if constexpr (BLK) {  // W2 rows 32w .. 32w+31 (output tile w) into the W_o area, read above
-    if constexpr (P::QSPLIT)
-      dma_span_rows<D, P::N_O>(rW1, reinterpret_cast<const char*>(tail.w1 + (int64_t)32 * w * D), spans);
-    dma_span_rows<D, P::N_O>(rW2, reinterpret_cast<const char*>(tail.w2 + (int64_t)32 * w * D), spans);
-  }
+  // Whole-block mode: W1 rows 32w .. 32w+31 (FFN hidden tile w) into the token-tile area,
+  // free now; it lands during the out-projection and LN2.  (Issued before the attention
+  // instead, it slowed the attention's LDS reads by more than the transfer saved.)  W2
+  // follows after the LN2 exchange, so the two do not queue in front of each other.
+  char* const rW1 = rX + w * P::TILEB;
+  char* const rW2 = rQ + w * P::TILEB;
+  if constexpr (BLK) dma_span_rows<D, P::N_O>(rW1, reinterpret_cast<const char*>(tail.w1 + (int64_t)32 * w * D), spans);
 
   // ---- out^T tile w = W_o[32w..32w+31] ctx^T, + b_o + x, then LN2 ----------------------
   float v[4][4];  // query qtok, column 32w + 8qd + 4g + e
@@ -740,8 +743,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       // x[qtok][32w + 8qd + 4g + e]: k-step 2w + qd/2, fragment half qd % 2, elements 4g + e.
       float xr[4];
       if constexpr (BLK) {
+        const f32x4 rr = *reinterpret_cast<const f32x4*>(rRes + li * 128 + 16 * ((2 * qd + g) ^ (li & 7)));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xr[e] = rres[qd][e];
+        for (int e = 0; e < 4; ++e) xr[e] = rr[e];
       } else {
         const f16x4 xh = *reinterpret_cast<const f16x4*>(
             reinterpret_cast<const char*>(Raw + (2 * w + (qd >> 1)) * 64 + li + 32 * (qd & 1)) + 8 * g);
@@ -765,6 +769,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     }
   }
   lds_barrier();
+  // W2 rows 32w .. 32w+31 (output tile w) into the W_o area (read into registers above).
+  if constexpr (BLK) dma_span_rows<D, P::N_O>(rW2, reinterpret_cast<const char*>(tail.w2 + (int64_t)32 * w * D), spans);
   if (w < NNT) {
     float tot = 0.f, tsq = 0.f;
 #pragma unroll
@@ -826,7 +832,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     }
   };
   const float* pt = reinterpret_cast<const float*>(rP + 1024);  // b1 | b2 | gn | bn of tile w
-  f16x8* const Hid = Raw;  // FFN hidden fragments (the residual area is unused in this mode)
+  f16x8* const Hid = Kl;  // FFN hidden fragments, in the K / V area (free after the attention)
   // The bias rows of this lane's accumulator registers (4qd + e: row 8qd + 4g + e), in
   // registers before the products rather than one LDS round trip per element after them.
   f32x4 b1v[4], b2v[4];
