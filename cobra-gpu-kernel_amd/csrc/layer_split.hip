@@ -14,9 +14,8 @@
 // sequence run side by side, and inside a workgroup the waves split every
 // phase four ways:
 //   1. wave w normalises tokens 32w .. 32w+31 (LN1, mean and variance in one
-//      pass) while the W_k / W_v rows of d-tile w and the W_q rows of head w
-//      arrive; the wave whose tile holds the slice's own queries keeps a raw
-//      copy of it, the residual;
+//      pass) while the W_k / W_v rows of d-tile w arrive; the wave whose tile
+//      holds the slice's own queries keeps a raw copy of it, the residual;
 //   2. wave w projects K^T and V of d-tile w for ALL tokens (every workgroup
 //      of the sequence recomputes them: twice the projection FLOPs of the
 //      persistent kernel, but no cross-workgroup traffic at all), and Q^T of
@@ -86,7 +85,8 @@ struct SplitPlan {
   static constexpr int OFF_P = OFF_R + RAWB, OFF_STAT = OFF_P + kSplitWaves * PB;
   static constexpr int BYTES = OFF_STAT + 2 * kSplitWaves * 32 * 4;
   // DMA instructions of one wave, in issue order: [gamma1|beta1] 1 (affine LN1 only),
-  // token tile N_X, other parameters 1, W_k/W_v N_A, W_q N_Q; W_o N_O after barrier 1.
+  // token tile N_X, other parameters 1, W_k/W_v N_A before barrier 1; W_q N_Q between
+  // the first token tiles' K / V products; W_o N_O after barrier 2.
   static constexpr int N_X = TILEB / 1024, N_A = 2 * TILEB / 1024, N_Q = NQT * TILEB / 1024;
   static constexpr int N_O = TILEB / 1024;
   static_assert(D == 64 || D == 128, "swizzle and row geometry");
@@ -168,12 +168,17 @@ struct BlockTail {
   int mask_out;       // multiply the normalised output of padded rows by 0
 };
 
-template <int D, int HD, bool CAUSAL, bool MASKED, bool BLK>
+// Argument order: everything the first transfers need (S, the grid size, x, W_qkv and
+// the parameter rows) comes first, in the first 56 bytes of the argument block, which
+// one scalar load returns; `nblk` is gridDim.x, passed explicitly so the tile mapping
+// does not wait on a second load of the dispatch's hidden arguments.
+// AFF1: LN1 with an elementwise affine (g1 / be1 non-null; never in whole-block mode).
+template <int D, int HD, bool CAUSAL, bool MASKED, bool BLK, bool AFF1>
 __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
-    const f16* __restrict__ x, const f16* __restrict__ wqkv, const float* __restrict__ bqkv,
-    const f16* __restrict__ wo, const float* __restrict__ bo, const float* __restrict__ g1,
-    const float* __restrict__ be1, const float* __restrict__ g2, const float* __restrict__ be2, void* __restrict__ yv,
-    float* resid_out, int S, int NS, float c2, float eps, const uint8_t* __restrict__ vmask, BlockTail tail) {
+    int S, int nblk, const f16* __restrict__ x, const f16* __restrict__ wqkv, const float* __restrict__ bqkv,
+    const float* __restrict__ bo, const float* __restrict__ g2, const float* __restrict__ be2,
+    const f16* __restrict__ wo, const float* __restrict__ g1, const float* __restrict__ be1, void* __restrict__ yv,
+    float* resid_out, float c2, float eps, const uint8_t* __restrict__ vmask, BlockTail tail) {
   using P = SplitPlan<D, HD, BLK>;
   constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH, NQT = P::NQT;
   // Whole-block mode: the FFN's hidden width equals d_model, one 32-wide tile per wave.
@@ -195,7 +200,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 
   // The S/32 slices of a sequence run on one XCD, so its L2 serves the token
   // tiles they all read.
-  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int NS = (S + 31) >> 5;  // query slices per sequence
+  const int item = xcd_remap(blockIdx.x, nblk);
   const int b = item / NS;
   const int s = item - b * NS;  // query slice
   const int lane = threadIdx.x & 63;
@@ -224,7 +230,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 
   // ---- DMA, in the order the data is needed -------------------------------------------
   const RowSpans<D> spans(lane);
-  const bool aff1 = !BLK && g1 != nullptr;  // LN1 with elementwise affine
+  static_assert(!(BLK && AFF1), "the whole-block input is already normalised");
+  constexpr bool aff1 = AFF1;
   if constexpr (BLK) {  // b1, b2 and the next norm's parameters of tile w (512 bytes: lanes 0-31)
     const int seg = lane >> 3, off = 32 * w + 4 * (lane & 7);
     const float* src = seg == 0 ? tail.b1 + off : seg == 1 ? tail.b2 + off : seg == 2 ? tail.gn + off : tail.bn + off;
@@ -254,25 +261,21 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   // W_k rows 32dq .. 32dq+31, in flight while the token tile is still on its way.
   const char* const wbytes = reinterpret_cast<const char*>(wqkv);
   dma_span_rows<D, P::N_A / 2>(rWkv, wbytes + (int64_t)(D + 32 * dq) * 2 * D, spans);
-  // The W_v rows and the W_q rows qrow0 .. qrow0 + 32 NQT - 1 are issued from inside
-  // LN1, a span or two between its arithmetic steps.  The CU's load path drains about
-  // one 1 KB transfer per 16 cycles; a wave that issues more than the queue holds
-  // stalls at the issue, so transfers issued in one run ahead of LN1 would hold LN1
-  // back until the load path had worked through them all.  (Issuing W_k from inside
-  // LN1 as well lets the token tile land ~300 cycles sooner but stretches LN1 more.)
-  constexpr int NV = P::N_A / 2, NLATE = NV + P::N_Q, NSLOT = 2 * KD;
-  constexpr int PER_SLOT = (NLATE + NSLOT - 1) / NSLOT;
+  // The W_v rows are issued from inside LN1, spread evenly over its arithmetic steps.
+  // The CU's load path drains about one 1 KB transfer per 20 cycles; a wave that
+  // issues more than the queue holds stalls at the issue, so transfers issued in one
+  // run ahead of LN1 would hold LN1 back until the load path had worked through them
+  // all.  Only what the K / V products need is loaded before the first barrier: the
+  // W_q rows follow between the first token tiles' products and the W_o rows during
+  // the attention, so neither is waited for before the matrix cores start.
+  constexpr int NV = P::N_A / 2, NSLOT = 2 * KD;
   const char* const wvsrc = wbytes + (int64_t)(2 * D + 32 * dq) * 2 * D;
   const char* const wqsrc = wbytes + (int64_t)qrow0 * 2 * D;
-  auto issue_late = [&](int slot) {  // slot < NSLOT; spans PER_SLOT * slot ..
+  auto issue_late = [&](int slot) {  // slot < NSLOT: spans ceil(slot NV / NSLOT) ..
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = PER_SLOT * slot; j < PER_SLOT * (slot + 1) && j < NLATE; ++j) {
-      if (j < NV)
-        dma16(wvsrc + 1024 * j + spans.off[j % RowSpans<D>::NP], rWkv + P::TILEB + 1024 * j);
-      else
-        dma16(wqsrc + 1024 * (j - NV) + spans.off[(j - NV) % RowSpans<D>::NP], rWq + 1024 * (j - NV));
-    }
+    for (int j = (slot * NV + NSLOT - 1) / NSLOT; j < ((slot + 1) * NV + NSLOT - 1) / NSLOT; ++j)
+      dma16(wvsrc + 1024 * j + spans.off[j % RowSpans<D>::NP], rWkv + P::TILEB + 1024 * j);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   }
 
   // ---- operand fragments of this wave's weights -------------------------------------------
-  wait_vmcnt<P::N_Q>();
+  wait_vmcnt<0>();
   if constexpr (BLK && MASKED) kbits = key_bits_of(kbytes, S, lane);  // the mask bytes are older
   f16x8 wk[KD], wv[KD];  // A operand of K^T = W_k h^T; B operand of V = h W_v^T
 #pragma unroll
@@ -372,12 +375,6 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     wk[kk] = tile_chunk<D>(rWkv, li, 2 * kk + g);
     wv[kk] = tile_chunk<D>(rWkv + P::TILEB, li, 2 * kk + g);
   }
-  wait_vmcnt<0>();
-  f16x8 wq[NQT][KD];  // A operand of Q^T = W_q h^T
-#pragma unroll
-  for (int dt = 0; dt < NQT; ++dt)
-#pragma unroll
-    for (int kk = 0; kk < KD; ++kk) wq[dt][kk] = tile_chunk<D>(rWq, 32 * dt + li, 2 * kk + g);
   const float* pp = reinterpret_cast<const float*>(rP);  // the 32-float segments above
   lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
 
@@ -398,17 +395,17 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     }
   }
 
-  // W_o rows 32dq .. 32dq+31 into the W_q staging area: in by the out-projection.  A
-  // projecting wave issues them between its token tiles, where the matrix cores are
-  // still busy with the previous tile, rather than stalling on the load path first.
-  const char* const wob = reinterpret_cast<const char*>(wo + (int64_t)32 * dq * D);
-  constexpr int kWoPer = (P::N_O + kSplitTiles - 2) / (kSplitTiles - 1);  // spans per tile 1 ..
-  auto issue_wo = [&](int t) {  // t >= 1
+  // W_q rows qrow0 .. qrow0 + 32 NQT - 1 of a wave that projects Q^T, issued at the
+  // start of the first token tiles' products (the matrix cores are busy with those
+  // while the wave waits at the issue) and read back at the last tile.
+  const bool doq = P::QBYTILE || w < H;
+  constexpr int kWqPer = (P::N_Q + kSplitTiles - 2) / (kSplitTiles - 1);  // spans per tile 0 ..
+  auto issue_wq = [&](int t) {  // t < kSplitTiles - 1
 #pragma unroll
-    for (int i = (t - 1) * kWoPer; i < t * kWoPer && i < P::N_O; ++i)
-      dma16(wob + 1024 * i + spans.off[i % RowSpans<D>::NP], rWo + 1024 * i);
+    for (int i = t * kWqPer; i < (t + 1) * kWqPer && i < P::N_Q; ++i)
+      dma16(wqsrc + 1024 * i + spans.off[i % RowSpans<D>::NP], rWq + 1024 * i);
   };
-  if (w >= NNT) dma_span_rows<D, P::N_O>(rWo, wob, spans);
+  f16x8 wq[NQT][KD];  // A operand of Q^T = W_q h^T
 
   // ---- K^T and V of d-tile w for every token tile; Q^T of the slice for head w ---------
   f16x8 qB[P::NARROW ? 2 : KSH];  // B operand of S^T = K Q^T (narrow heads: the two k-steps of d-tile w)
@@ -459,7 +456,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       }
     };
     auto products = [&](int t) {
-      if (t >= 1) issue_wo(t);
+      if (doq && t + 1 < kSplitTiles) issue_wq(t);
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
         const f16x8 hb = hf[t & 1][kk];
@@ -467,11 +464,19 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         va[t & 1] = mfma32x32x16(hb, wv[kk], kk == 0 ? bv : va[t & 1]);
         // The next tile's fragments (after the last tile: those of the slice, for
         // Q^T) are requested behind this tile's first two products, never ahead of
-        // them.  The first wait for LDS data after an LDS-DMA issue (issue_wo) is
+        // them.  The first wait for LDS data after an LDS-DMA issue (issue_wq) is
         // compiled as lgkmcnt(0), i.e. it would also wait for requests just made.
         if (kk == 0) {
           __builtin_amdgcn_sched_barrier(0);
           fetch(t + 1 < kSplitTiles ? t + 1 : s, (t + 1) & 1);
+          // The W_q rows (this wave's own transfers, issued two tiles ago at the latest).
+          if (doq && t + 1 == kSplitTiles) {
+            wait_vmcnt<0>();
+#pragma unroll
+            for (int dt = 0; dt < NQT; ++dt)
+#pragma unroll
+              for (int k2 = 0; k2 < KD; ++k2) wq[dt][k2] = tile_chunk<D>(rWq, 32 * dt + li, 2 * k2 + g);
+          }
         }
         if (t >= 1)
 #pragma unroll
@@ -484,7 +489,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int t = 0; t < kSplitTiles; ++t) products(t);
     // Q^T of the slice for head w (waves past the last head have none), or d-tile w
     // of the split head, with the last K / V tile stored between its products.
-    if (P::QBYTILE || w < H) {
+    if (doq) {
 #pragma unroll
       for (int dt = 0; dt < NQT; ++dt) {
         f32x16 qa;
@@ -514,7 +519,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       for (int c = 0; c < 4; ++c) store_part(kSplitTiles - 1, c);
     }
   }
-  lds_barrier();  // K, V of every token tile and head are in LDS
+  lds_barrier();  // K, V of every token tile and head are in LDS; every W_q read is done
+  // W_o rows 32dq .. 32dq+31 into the W_q staging area, free now: they land during the
+  // attention.  (Waves past the last output tile fetch tile 0 again, identical bytes
+  // to the same place.)
+  dma_span_rows<D, P::N_O>(rWo, reinterpret_cast<const char*>(wo + (int64_t)32 * dq * D), spans);
 
   // ---- attention of head w: S^T = K Q^T for all (at most 128) keys at once, one exact
   // softmax pass (no running max, no rescale), O^T = V^T P^T.
@@ -946,13 +955,15 @@ bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dty
 
 template <int D, int HD, bool CAUSAL>
 static hipError_t launch_split(const SmallLayerArgs& a, float c2) {
-  const int ns = (int)((a.seq_len + 31) / 32);
-  const int64_t grid = a.batch * ns;
+  const int64_t grid = a.batch * ((a.seq_len + 31) / 32);
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  auto kern = a.valid_mask ? layer_split_kernel<D, HD, CAUSAL, true, false> : layer_split_kernel<D, HD, CAUSAL, false, false>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, static_cast<const f16*>(a.x),
-                     static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<const f16*>(a.w_o), a.b_o, a.ln1_w,
-                     a.ln1_b, a.ln2_w, a.ln2_b, a.y, a.resid_out, (int)a.seq_len, ns, c2, a.eps, a.valid_mask,
+  auto kern = a.ln1_w ? (a.valid_mask ? layer_split_kernel<D, HD, CAUSAL, true, false, true>
+                                      : layer_split_kernel<D, HD, CAUSAL, false, false, true>)
+                      : (a.valid_mask ? layer_split_kernel<D, HD, CAUSAL, true, false, false>
+                                      : layer_split_kernel<D, HD, CAUSAL, false, false, false>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, (int)a.seq_len, (int)grid,
+                     static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv, a.b_o, a.ln2_w, a.ln2_b,
+                     static_cast<const f16*>(a.w_o), a.ln1_w, a.ln1_b, a.y, a.resid_out, c2, a.eps, a.valid_mask,
                      BlockTail{});
   return hipGetLastError();
 }
@@ -986,15 +997,15 @@ bool block_split_pays(int64_t batch, int64_t seq_len) {
 
 template <int HD, bool CAUSAL>
 static hipError_t launch_block(const BlockArgs& a, float c2) {
-  const int ns = (int)((a.seq_len + 31) / 32);
-  const int64_t grid = a.batch * ns;
+  const int64_t grid = a.batch * ((a.seq_len + 31) / 32);
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
   const BlockTail tail{a.r, static_cast<const f16*>(a.w1), a.b1, static_cast<const f16*>(a.w2), a.b2, a.lnn_w,
                        a.lnn_b, a.out_dtype == kF32, a.mask_out};
-  auto kern = a.valid_mask ? layer_split_kernel<128, HD, CAUSAL, true, true> : layer_split_kernel<128, HD, CAUSAL, false, true>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, static_cast<const f16*>(a.h),
-                     static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<const f16*>(a.w_o), a.b_o, nullptr, nullptr,
-                     a.ln2_w, a.ln2_b, a.out, a.r_out, (int)a.seq_len, ns, c2, a.eps, a.valid_mask, tail);
+  auto kern = a.valid_mask ? layer_split_kernel<128, HD, CAUSAL, true, true, false>
+                           : layer_split_kernel<128, HD, CAUSAL, false, true, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, (int)a.seq_len, (int)grid,
+                     static_cast<const f16*>(a.h), static_cast<const f16*>(a.w_qkv), a.b_qkv, a.b_o, a.ln2_w, a.ln2_b,
+                     static_cast<const f16*>(a.w_o), nullptr, nullptr, a.out, a.r_out, c2, a.eps, a.valid_mask, tail);
   return hipGetLastError();
 }
 
