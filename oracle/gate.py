@@ -18,6 +18,10 @@ import torch
 ATOL = 2e-3
 RTOL = 2e-2
 
+# Opt-in log of every comparison, for the per-test worst-error report the test
+# session writes (tests/conftest.py, COBRA_PARITY_REPORT).  None: not recording.
+RECORD: "List[Tuple[float, float, int, int, float]] | None" = None
+
 
 @dataclass
 class AccuracyResult:
@@ -69,12 +73,20 @@ def compare_outputs(
     else:
         dims = torch.nonzero(failed.any(dim=tuple(range(reference.ndim - 1)))).flatten().tolist()
 
+    max_abs = float(err.max().item()) if err.numel() else 0.0
+    max_rel = float(rel.max().item()) if rel.numel() else 0.0
+    if RECORD is not None:
+        # The gate's margin: per element min(err / atol, err / (rtol |ref|)), <= 1 passes.
+        ratio = torch.minimum(err / atol, err / (rtol * ref.abs()).clamp_min(1e-30))
+        ratio = torch.where(torch.isfinite(ref) & torch.isfinite(opt), ratio, torch.full_like(ratio, float("inf")))
+        worst_ratio = float(ratio.max().item()) if ratio.numel() else 0.0
+        RECORD.append((max_abs, max_rel, n_failed, reference.numel(), worst_ratio))
     return AccuracyResult(
         passed=n_failed == 0,
         total_elements=reference.numel(),
         failed_elements=n_failed,
-        max_abs_error=float(err.max().item()) if err.numel() else 0.0,
-        max_relative_error=float(rel.max().item()) if rel.numel() else 0.0,
+        max_abs_error=max_abs,
+        max_relative_error=max_rel,
         mean_abs_error=float(err.mean().item()) if err.numel() else 0.0,
         failed_feature_dims=dims,
         worst_index=worst_index,

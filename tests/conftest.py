@@ -29,3 +29,45 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+# ---- per-test worst-error report --------------------------------------------------------
+# With COBRA_PARITY_REPORT=<path>, every oracle.compare_outputs call made by a test is
+# logged (worst |error|, worst relative error, failing elements, elements and the worst
+# gate ratio min(abs / 2e-3, rel / 2e-2) over elements, <= 1 passes), and the session
+# writes one line per test to <path>: the reference's gate passes an element when
+# abs <= 2e-3 OR rel <= 2e-2, so the worst abs error alone does not show the margin.
+_REPORT_PATH = os.environ.get("COBRA_PARITY_REPORT")
+_report = {}
+
+
+@pytest.hookimpl(hookwrapper=True)
+def pytest_runtest_call(item):
+    if not _REPORT_PATH:
+        yield
+        return
+    from oracle import gate
+
+    gate.RECORD = []
+    try:
+        yield
+    finally:
+        if gate.RECORD:
+            _report[item.nodeid] = list(gate.RECORD)
+        gate.RECORD = None
+
+
+def pytest_sessionfinish(session, exitstatus):
+    if not _REPORT_PATH or not _report:
+        return
+    lines = ["| test | comparisons | worst abs | worst rel | worst gate ratio | failing / elements |",
+             "|---|---|---|---|---|---|"]
+    for nodeid, recs in _report.items():
+        wa = max(r[0] for r in recs)
+        wr = max(r[1] for r in recs)
+        nf = sum(r[2] for r in recs)
+        ne = sum(r[3] for r in recs)
+        wg = max(r[4] for r in recs)
+        lines.append(f"| `{nodeid}` | {len(recs)} | {wa:.3e} | {wr:.3e} | {wg:.3f} | {nf} / {ne} |")
+    with open(_REPORT_PATH, "w") as f:
+        f.write("\n".join(lines) + "\n")
