@@ -29,20 +29,19 @@ static_assert(COBRA_EPI_GELU == cobra::kEpiGelu && COBRA_EPI_MASK_BRANCH == cobr
               "ABI flag values are the kernels' own");
 
 struct LayerBuffers {
-  int64_t h_off, qkv_off, r_off, bits_off, total;
+  int64_t h_off, qkv_off, bits_off, total;
 };
 
 // Workspace layout of cobra_layer_fwd: h (fp16 [T, D], later reused for the
-// attention context), qkv (fp16 [T, 3D]), for D > 128 the fp32 residual that
-// feeds the separate LayerNorm pass, and with a token mask the packed key
-// bits ([B][ceil(S/64)] u64).
+// attention context), qkv (fp16 [T, 3D]; for D > 128 later reused for the
+// out-projection's fp16 branch), and with a token mask the packed key bits
+// ([B][ceil(S/64)] u64).
 LayerBuffers layer_buffers(int64_t batch, int64_t seq_len, int64_t d, bool masked) {
   const int64_t tokens = batch * seq_len;
   LayerBuffers b{};
   b.h_off = 0;
   b.qkv_off = round256(tokens * d * 2);
-  b.r_off = b.qkv_off + round256(tokens * 3 * d * 2);
-  b.bits_off = b.r_off + (d > 128 ? round256(tokens * d * 4) : 0);
+  b.bits_off = b.qkv_off + round256(tokens * 3 * d * 2);
   b.total = b.bits_off + (masked ? round256(batch * cobra::mask_words(seq_len) * 8) : 0);
   return b;
 }
@@ -370,18 +369,30 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     out.epi = masked ? cobra::kEpiMaskBranch : 0;
     return code(cobra::run_gemm(out));
   }
-  // r goes to memory between the projection and LayerNorm in fp32, as the reference's
-  // fused path stores it (TTB:1274-1283): rounded to fp16 it would carry an error of
-  // half an fp16 step of |r| into LN2, amplified by 1/std (visible for inputs whose
-  // mean is large against their spread).
-  const int r_dtype = kF32;
-  void* r = resid_out ? static_cast<void*>(resid_out) : static_cast<void*>(ws + lb.r_off);
-  cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, r, r_dtype, T, (int)D, (int)D,
+  if (resid_out) {
+    // r itself is an output: the out-projection adds x and stores r in fp32 (the
+    // reference's split, TTB:1274-1283), LN2 reads it back.
+    cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, resid_out, kF32, T, (int)D, (int)D,
+                        nullptr, nullptr, nullptr, kF16, eps, s};
+    out.row_mask = valid_mask;
+    out.epi = masked ? cobra::kEpiMaskBranch : 0;
+    if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
+    cobra::LnArgs ln2{resid_out, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
+    return code(cobra::run_ln(ln2));
+  }
+  // Otherwise the out-projection stores only the branch ctx W_o^T + b_o, in fp16, into
+  // the qkv area (dead since the attention), and LN2 forms r = x + branch in fp32 (the
+  // reference's _add_ln split, TTB:539): half the bytes of an fp32 r, and no residual
+  // read in the GEMM.  The large values of r sit in x, exact in the sum; the branch's
+  // rounding is 2^-11 of its own magnitude.  (r itself rounded to fp16 would put half
+  // an fp16 step of |r| into LN2, amplified by 1/std for inputs with a large mean.)
+  void* branch = qkv;
+  cobra::GemmArgs out{ctx, w_o, b_o, nullptr, kF16, branch, kF16, T, (int)D, (int)D,
                       nullptr, nullptr, nullptr, kF16, eps, s};
   out.row_mask = valid_mask;
   out.epi = masked ? cobra::kEpiMaskBranch : 0;
   if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
-  cobra::LnArgs ln2{r, r_dtype, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
+  cobra::LnArgs ln2{x, x_dtype, branch, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
   return code(cobra::run_ln(ln2));
 }
 

@@ -111,8 +111,10 @@ __global__ __launch_bounds__(256, NCH <= 2 ? 8 : 1) void ln_rows_kernel(const TX
 // 1024): no branch, mask or residual store, the width fixed at compile time, one row
 // per wave.  Without the generic kernel's option handling (branches and address
 // arithmetic around every chunk) the pass runs ~0.8 us faster at 8192 x 1024.
-template <typename TX, typename TY, int NCH>
-__global__ __launch_bounds__(256) void ln_plain_kernel(const TX* __restrict__ x, const float* __restrict__ gamma,
+// BR: r = x + branch (fp16 branch, the sum in fp32) is normalised instead of x.
+template <typename TX, typename TY, int NCH, bool BR>
+__global__ __launch_bounds__(256) void ln_plain_kernel(const TX* __restrict__ x, const f16* __restrict__ branch,
+                                                       const float* __restrict__ gamma,
                                                        const float* __restrict__ beta, TY* __restrict__ y,
                                                        int64_t rows, float eps) {
   constexpr int D = 512 * NCH;
@@ -131,6 +133,15 @@ __global__ __launch_bounds__(256) void ln_plain_kernel(const TX* __restrict__ x,
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) load8(x + r * D + 512 * c + 8 * lane, v[c]);
+  if constexpr (BR) {
+    float bb[NCH][8];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) load8(branch + r * D + 512 * c + 8 * lane, bb[c]);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] += bb[c][i];
+  }
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
 #pragma unroll
@@ -236,8 +247,10 @@ static hipError_t dispatch_ln_any(const LnArgs& a) {
 template <typename TX, typename TY, int NCH>
 static hipError_t launch_ln_plain(const LnArgs& a) {
   const int64_t blocks = (a.rows + 3) / 4;
-  hipLaunchKernelGGL((ln_plain_kernel<TX, TY, NCH>), dim3((unsigned)blocks), dim3(256), 0, a.stream,
-                     static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<TY*>(a.y), a.rows, a.eps);
+  const f16* br = static_cast<const f16*>(a.branch);
+  auto kern = br ? ln_plain_kernel<TX, TY, NCH, true> : ln_plain_kernel<TX, TY, NCH, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, a.stream, static_cast<const TX*>(a.x), br, a.gamma,
+                     a.beta, static_cast<TY*>(a.y), a.rows, a.eps);
   return hipGetLastError();
 }
 
@@ -254,7 +267,7 @@ static hipError_t launch_ln(const LnArgs& a) {
 
 template <typename TX, typename TY>
 static hipError_t dispatch_ln_geometry(const LnArgs& a) {
-  if (!a.branch && !a.row_mask && !a.resid_out && a.rows <= (int64_t)4 * 0x7fffffff) {
+  if ((!a.branch || !a.branch_f32) && !a.row_mask && !a.resid_out && a.rows <= (int64_t)4 * 0x7fffffff) {
     if (a.d == 512) return launch_ln_plain<TX, TY, 1>(a);
     if (a.d == 1024) return launch_ln_plain<TX, TY, 2>(a);
   }

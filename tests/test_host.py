@@ -129,14 +129,15 @@ def test_workspace_size_formula():
 
     # fused plan: no workspace
     assert ops.layer_workspace_bytes(64, 128, 128, 4) == 0
-    # staged: h fp16 [T, D] + qkv fp16 [T, 3D] (+ fp32 residual for D > 128), 256-B aligned
+    # staged: h fp16 [T, D] + qkv fp16 [T, 3D], 256-B aligned (for D > 128 the out-projection's
+    # fp16 branch reuses the qkv area; an fp32 residual goes only to a caller's resid_out)
     f32 = torch.float32
     assert ops.layer_workspace_bytes(64, 128, 128, 16, dtype=f32) == 8192 * 128 * 2 + 8192 * 384 * 2
     t, d = 32 * 100000, 1024
-    assert ops.layer_workspace_bytes(32, 100000, 1024, 16) == t * d * 2 + t * 3 * d * 2 + t * d * 4
+    assert ops.layer_workspace_bytes(32, 100000, 1024, 16) == t * d * 2 + t * 3 * d * 2
     # a token mask adds the packed key bits, [B][ceil(S/64)] u64, 256-B aligned
     bits = -(-(32 * 1563 * 8) // 256) * 256
-    assert ops.layer_workspace_bytes(32, 100000, 1024, 16, masked=True) == t * d * 2 + t * 3 * d * 2 + t * d * 4 + bits
+    assert ops.layer_workspace_bytes(32, 100000, 1024, 16, masked=True) == t * d * 2 + t * 3 * d * 2 + bits
     assert ops.layer_workspace_bytes(64, 128, 128, 4, masked=True) == 0  # fused: the kernel reads the mask bytes
     assert ops.layer_workspace_bytes(64, 128, 128, 16, masked=True, dtype=f32) == 8192 * 128 * 2 + 8192 * 384 * 2 + 1024
 
