@@ -175,6 +175,40 @@ int layer_fwd_padded(const void* x, int x_dtype, const uint8_t* valid_mask, cons
   return code(cobra::run_ln(ln2));
 }
 
+// Out-projection and LN2 of the staged sublayer at d_model > 128: ctx [T, D] fp16 in,
+// y out; `spare` is a dead workspace area of at least T * D fp16 that ctx does not
+// overlap.
+int out_proj_ln2(const void* ctx, void* spare, const void* x, int x_dtype, const uint8_t* valid_mask, const void* w_o,
+                 const float* b_o, const float* ln2_w, const float* ln2_b, void* y, float* resid_out, int64_t T,
+                 int64_t D, float eps, hipStream_t s) {
+  const bool masked = valid_mask != nullptr;
+  hipError_t e = hipSuccess;
+  if (resid_out) {
+    // r itself is an output: the out-projection adds x and stores r in fp32 (the
+    // reference's split, TTB:1274-1283), LN2 reads it back.
+    cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, resid_out, kF32, T, (int)D, (int)D,
+                        nullptr, nullptr, nullptr, kF16, eps, s};
+    out.row_mask = valid_mask;
+    out.epi = masked ? cobra::kEpiMaskBranch : 0;
+    if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
+    cobra::LnArgs ln2{resid_out, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
+    return code(cobra::run_ln(ln2));
+  }
+  // Otherwise the out-projection stores only the branch ctx W_o^T + b_o, in fp16, into
+  // the spare area, and LN2 forms r = x + branch in fp32 (the reference's _add_ln split,
+  // TTB:539): half the bytes of an fp32 r, and no residual read in the GEMM.  The large
+  // values of r sit in x, exact in the sum; the branch's rounding is 2^-11 of its own
+  // magnitude.  (r itself rounded to fp16 would put half an fp16 step of |r| into LN2,
+  // amplified by 1/std for inputs with a large mean.)
+  cobra::GemmArgs out{ctx, w_o, b_o, nullptr, kF16, spare, kF16, T, (int)D, (int)D,
+                      nullptr, nullptr, nullptr, kF16, eps, s};
+  out.row_mask = valid_mask;
+  out.epi = masked ? cobra::kEpiMaskBranch : 0;
+  if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
+  cobra::LnArgs ln2{x, x_dtype, spare, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
+  return code(cobra::run_ln(ln2));
+}
+
 }  // namespace
 
 extern "C" {
@@ -283,6 +317,16 @@ int cobra_qkv_attn_fwd(const void* h, const void* w_qkv, const float* b_qkv, voi
   const int64_t T = batch * seq_len, D = heads * head_dim;
   if (T == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t hbytes = T * D * 2;
+  const char* hc = static_cast<const char*>(h);
+  const char* cc = static_cast<const char*>(ctx);
+  if (cobra::qkv_attn_head_ok(seq_len, heads, head_dim) && (cc + hbytes <= hc || hc + hbytes <= cc)) {
+    // One launch: the projection inside the attention kernel (its workgroups read every
+    // h row of their sequence while others write ctx, hence the overlap condition).
+    cobra::QkvAttnArgs f{h, w_qkv, b_qkv, ctx, batch, seq_len, heads, head_dim, scale, causal ? 1 : 0,
+                         key_bits, s};
+    return code(cobra::run_qkv_attn_head(f));
+  }
   cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kF16, workspace, kF16, T, (int)(3 * D), (int)D,
                        nullptr, nullptr, nullptr, kF16, 1e-5f, s};
   hipError_t e = cobra::run_gemm(proj);
@@ -343,6 +387,18 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
 
   hipError_t e = hipSuccess;
   if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
+  const int64_t hd = D / heads;
+  if (cobra::qkv_attn_head_ok(seq_len, heads, hd)) {
+    // head_dim 256, S <= 128: LN1, then the QKV projection fused into the attention
+    // (ctx into the qkv area: the kernel reads every h row while writing ctx), then the
+    // out-projection's fp16 branch into the h area (dead by then) and LN2 with x.
+    cobra::LnArgs ln1{x, x_dtype, nullptr, 0, ln1_w, ln1_b, nullptr, h, kF16, T, (int)D, eps, s};
+    if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
+    cobra::QkvAttnArgs f{h, w_qkv, b_qkv, qkv, batch, seq_len, heads, hd, (float)(1.0 / sqrt((double)hd)),
+                         causal ? 1 : 0, bits, s};
+    if ((e = cobra::run_qkv_attn_head(f)) != hipSuccess) return code(e);
+    return out_proj_ln2(qkv, h, x, x_dtype, valid_mask, w_o, b_o, ln2_w, ln2_b, y, resid_out, T, D, eps, s);
+  }
   if (cobra::ln_gemm_ok(D, x_dtype)) {
     // LN1 in the QKV projection's prologue: h never goes to memory.
     cobra::LnGemmArgs proj{x, x_dtype, ln1_w, ln1_b, w_qkv, b_qkv, qkv, T, (int)(3 * D), D, eps, s};
@@ -369,31 +425,7 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     out.epi = masked ? cobra::kEpiMaskBranch : 0;
     return code(cobra::run_gemm(out));
   }
-  if (resid_out) {
-    // r itself is an output: the out-projection adds x and stores r in fp32 (the
-    // reference's split, TTB:1274-1283), LN2 reads it back.
-    cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, resid_out, kF32, T, (int)D, (int)D,
-                        nullptr, nullptr, nullptr, kF16, eps, s};
-    out.row_mask = valid_mask;
-    out.epi = masked ? cobra::kEpiMaskBranch : 0;
-    if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
-    cobra::LnArgs ln2{resid_out, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
-    return code(cobra::run_ln(ln2));
-  }
-  // Otherwise the out-projection stores only the branch ctx W_o^T + b_o, in fp16, into
-  // the qkv area (dead since the attention), and LN2 forms r = x + branch in fp32 (the
-  // reference's _add_ln split, TTB:539): half the bytes of an fp32 r, and no residual
-  // read in the GEMM.  The large values of r sit in x, exact in the sum; the branch's
-  // rounding is 2^-11 of its own magnitude.  (r itself rounded to fp16 would put half
-  // an fp16 step of |r| into LN2, amplified by 1/std for inputs with a large mean.)
-  void* branch = qkv;
-  cobra::GemmArgs out{ctx, w_o, b_o, nullptr, kF16, branch, kF16, T, (int)D, (int)D,
-                      nullptr, nullptr, nullptr, kF16, eps, s};
-  out.row_mask = valid_mask;
-  out.epi = masked ? cobra::kEpiMaskBranch : 0;
-  if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
-  cobra::LnArgs ln2{x, x_dtype, branch, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
-  return code(cobra::run_ln(ln2));
+  return out_proj_ln2(ctx, qkv, x, x_dtype, valid_mask, w_o, b_o, ln2_w, ln2_b, y, resid_out, T, D, eps, s);
 }
 
 

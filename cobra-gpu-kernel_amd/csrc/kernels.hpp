@@ -135,6 +135,22 @@ struct AttnArgs {
 };
 hipError_t run_attn(const AttnArgs& a);
 
+// QKV projection fused into exact attention, one workgroup per (sequence, head):
+// head_dim 256, S <= 128 (qkv_attn.hip).  ctx must not overlap h.
+struct QkvAttnArgs {
+  const void* h;           // [B*S, D] fp16 (D = heads * head_dim)
+  const void* w_qkv;       // [3D, D] fp16: q | k | v rows
+  const float* b_qkv;      // [3D] or null
+  void* ctx;               // [B*S, D] fp16
+  int64_t batch, seq_len, heads, head_dim;
+  float scale;
+  int causal;
+  const uint64_t* key_bits;  // optional [batch][ceil(S/64)]
+  hipStream_t stream;
+};
+bool qkv_attn_head_ok(int64_t seq_len, int64_t heads, int64_t head_dim);
+hipError_t run_qkv_attn_head(const QkvAttnArgs& a);
+
 // mask [batch, S] bytes (0 = padded) -> key_bits [batch][ceil(S/64)] (attn.hip).
 hipError_t run_mask_bits(const uint8_t* mask, uint64_t* bits, int64_t batch, int seq_len, hipStream_t stream);
 inline int64_t mask_words(int64_t seq_len) { return (seq_len + 63) / 64; }
