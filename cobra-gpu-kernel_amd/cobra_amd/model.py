@@ -223,15 +223,19 @@ class CobraTransformer(nn.Module):
         fold_ln1 = ops.ln_linear_ok(D, x.dtype)
         h = None if fold_ln1 else ops.add_ln(xf, None, None, packs[0].ln1_w, packs[0].ln1_b, cast_fp16=True,
                                              eps=eps, store_resid=False)[1]
+        fused_qkv = ops.qkv_attn_fused(B, S, H, hd)
         r = xf
         for i, p in enumerate(packs):
             last = i == n - 1
             nw, nb = self._final if last else (packs[i + 1].ln1_w, packs[i + 1].ln1_b)
             if i == 0 and fold_ln1:
                 qkv = ops.ln_linear(xf, p.ln1_w, p.ln1_b, p.w_qkv, p.b_qkv, eps=eps)
+                ctx = ops.attn(qkv, B, S, H, hd, scale, causal=cfg.causal, key_bits=bits)
+            elif fused_qkv:  # the projection inside the attention kernel (head_dim 256, S <= 128)
+                ctx = ops.qkv_attn(h, p.w_qkv, p.b_qkv, B, S, H, hd, scale, causal=cfg.causal, key_bits=bits)
             else:
                 qkv = ops.linear(h, p.w_qkv, p.b_qkv)
-            ctx = ops.attn(qkv, B, S, H, hd, scale, causal=cfg.causal, key_bits=bits)
+                ctx = ops.attn(qkv, B, S, H, hd, scale, causal=cfg.causal, key_bits=bits)
             if D <= 128:
                 r, h2 = ops.linear_ln(ctx, p.w_o, p.b_o, r, p.ln2_w, p.ln2_b, rmask=mrow, eps=eps, mask_branch=True)
             else:

@@ -339,10 +339,12 @@ def qkv_attn(
     ``_tl_qkvattn`` (TTB:761-785).
 
     Differences from the reference launcher: ``w_qkv`` is the nn.Linear-layout ``[3D, D]``
-    q | k | v weight (the reference passes the transposed ``[D, 3D]``), attention may be
-    non-causal and masked (``key_mask`` / ``key_bits`` as in ``attn``), and the projected
-    q / k / v go through a workspace allocated here (``torch.empty``) between the GEMM
-    and the attention kernel.  ``cfgs`` is accepted and ignored.
+    q | k | v weight (the reference passes the transposed ``[D, 3D]``), and attention may be
+    non-causal and masked (``key_mask`` / ``key_bits`` as in ``attn``).  For head_dim 256
+    and seq_len <= 128 the projection runs inside the attention kernel, one workgroup per
+    (sequence, head), as the reference's fused kernel does; otherwise the projected q / k / v
+    go through a workspace allocated here (``torch.empty``) between the GEMM and the
+    attention kernel.  ``cfgs`` is accepted and ignored.
     """
     _dev(h, "h")
     _dev(w_qkv, "w_qkv")
@@ -366,13 +368,20 @@ def qkv_attn(
     need = _lib.lib().cobra_qkv_attn_workspace_bytes(batch, seq_len, heads, head_dim)
     if need < 0:
         raise ValueError(f"unsupported attention shape heads={heads} head_dim={head_dim}")
-    ws = torch.empty(max(int(need), 1), dtype=torch.uint8, device=h.device)
+    ws = torch.empty(int(need), dtype=torch.uint8, device=h.device) if need > 0 else None
     out = torch.empty((batch * seq_len, D), device=h.device, dtype=torch.float16)
     call(
-        "cobra_qkv_attn_fwd", h.data_ptr(), w_qkv.data_ptr(), _ptr(bias), out.data_ptr(), _ptr(bits), ws.data_ptr(),
-        ws.numel(), batch, seq_len, heads, head_dim, float(scale), 1 if causal else 0, _stream(h),
+        "cobra_qkv_attn_fwd", h.data_ptr(), w_qkv.data_ptr(), _ptr(bias), out.data_ptr(), _ptr(bits), _ptr(ws),
+        0 if ws is None else ws.numel(), batch, seq_len, heads, head_dim, float(scale), 1 if causal else 0,
+        _stream(h),
     )
     return out
+
+
+def qkv_attn_fused(batch: int, seq_len: int, heads: int, head_dim: int) -> bool:
+    """Whether ``qkv_attn`` runs as one launch (the projection inside the attention kernel,
+    no q / k / v buffer) for this shape (host-only query)."""
+    return _lib.lib().cobra_qkv_attn_workspace_bytes(batch, seq_len, heads, head_dim) == 0
 
 
 PLAN_FUSED = _lib.PLAN_FUSED

@@ -302,6 +302,7 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
 
 int64_t cobra_qkv_attn_workspace_bytes(int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim) {
   if (batch < 0 || seq_len < 0 || heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256) return -1;
+  if (cobra::qkv_attn_head_ok(seq_len, heads, head_dim)) return 0;  // one fused launch, no q / k / v buffer
   return round256(batch * seq_len * 3 * heads * head_dim * 2);
 }
 
@@ -313,20 +314,22 @@ int cobra_qkv_attn_fwd(const void* h, const void* w_qkv, const float* b_qkv, voi
   if (!h || !w_qkv || !ctx || !aligned16(h) || !aligned16(w_qkv) || !aligned16(ctx) || !opt_aligned16(b_qkv))
     return kBad;
   if (key_bits && (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
-  if (!workspace || !aligned16(workspace) || workspace_bytes < need) return kBad;
   const int64_t T = batch * seq_len, D = heads * head_dim;
-  if (T == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t hbytes = T * D * 2;
-  const char* hc = static_cast<const char*>(h);
-  const char* cc = static_cast<const char*>(ctx);
-  if (cobra::qkv_attn_head_ok(seq_len, heads, head_dim) && (cc + hbytes <= hc || hc + hbytes <= cc)) {
-    // One launch: the projection inside the attention kernel (its workgroups read every
-    // h row of their sequence while others write ctx, hence the overlap condition).
+  if (need == 0) {
+    // One launch: the projection inside the attention kernel.  Its workgroups read every
+    // h row of their sequence while others write ctx, so the two must not overlap.
+    const int64_t hbytes = T * D * 2;
+    const char* hc = static_cast<const char*>(h);
+    const char* cc = static_cast<const char*>(ctx);
+    if (T > 0 && cc < hc + hbytes && hc < cc + hbytes) return kBad;
+    if (T == 0) return 0;
     cobra::QkvAttnArgs f{h, w_qkv, b_qkv, ctx, batch, seq_len, heads, head_dim, scale, causal ? 1 : 0,
                          key_bits, s};
     return code(cobra::run_qkv_attn_head(f));
   }
+  if (!workspace || !aligned16(workspace) || workspace_bytes < need) return kBad;
+  if (T == 0) return 0;
   cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kF16, workspace, kF16, T, (int)(3 * D), (int)D,
                        nullptr, nullptr, nullptr, kF16, 1e-5f, s};
   hipError_t e = cobra::run_gemm(proj);

@@ -135,17 +135,18 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
 
 /*
  * Fused QKV projection + multi-head attention on a normalised activation:
- *     qkv = h . w_qkv^T + b_qkv   (fp16, in the workspace: [batch*seq_len, 3*D])
- *     ctx = MHA(q, k, v)          (as cobra_attn_fwd: scale, causal, key_bits)
+ *     q | k | v = h . w_qkv^T + b_qkv   (rounded to fp16)
+ *     ctx = MHA(q, k, v)                (as cobra_attn_fwd: scale, causal, key_bits)
  * h: [batch*seq_len, D] fp16 (D = heads*head_dim); w_qkv: [3*D, D] fp16 (rows:
  * q_proj, k_proj, v_proj weights); b_qkv: [3*D] fp32 (optional); ctx: [batch*seq_len, D]
- * fp16.  workspace: cobra_qkv_attn_workspace_bytes() bytes.  head_dim % 8 == 0,
- * head_dim <= 256.  Two launches (the projection GEMM, then the attention).
- * Replaces _tl_qkvattn / _qkvattn_kernel (TTB:761-785, 654-741), which is causal
- * only and takes the transposed weight [D, 3D]; the reference fuses the
- * projection into the attention kernel, this library keeps q / k / v in the
- * workspace (for the whole sublayer, cobra_layer_fwd fuses further: one kernel
- * for short sequences).
+ * fp16.  head_dim % 8 == 0, head_dim <= 256.  For head_dim 256 with seq_len <= 128 it is
+ * one launch -- the projection inside the attention kernel, one workgroup per (sequence,
+ * head), q / k / v never in memory -- cobra_qkv_attn_workspace_bytes() returns 0 (the
+ * workspace may be null) and ctx must not overlap h.  Otherwise two launches (the
+ * projection GEMM into the workspace, cobra_qkv_attn_workspace_bytes() bytes, then the
+ * attention).  Replaces _tl_qkvattn / _qkvattn_kernel (TTB:761-785, 654-741), which is
+ * causal only, takes the transposed weight [D, 3D] and is used when one query block
+ * covers the sequence (TTB:1030-1071).
  */
 int64_t cobra_qkv_attn_workspace_bytes(int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim);
 int cobra_qkv_attn_fwd(const void* h, const void* w_qkv, const float* b_qkv, void* ctx, const uint64_t* key_bits,

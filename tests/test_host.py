@@ -142,6 +142,25 @@ def test_workspace_size_formula():
     assert ops.layer_workspace_bytes(64, 128, 128, 16, masked=True, dtype=f32) == 8192 * 128 * 2 + 8192 * 384 * 2 + 1024
 
 
+def test_qkv_attn_workspace_and_fused_contract():
+    """cobra_qkv_attn_fwd: head_dim 256 with seq_len <= 128 is one fused launch that needs no
+    workspace (size 0, a null workspace accepted) but refuses ctx overlapping h; every other
+    shape needs the q / k / v workspace and refuses a null one -- all decided before any launch."""
+    from cobra_amd import _lib, ops
+
+    lib = _lib.lib()
+    assert lib.cobra_qkv_attn_workspace_bytes(64, 128, 4, 256) == 0
+    assert lib.cobra_qkv_attn_workspace_bytes(2, 1, 1, 256) == 0
+    assert lib.cobra_qkv_attn_workspace_bytes(64, 129, 4, 256) == round(64 * 129 * 3 * 1024 * 2 / 256 + 0.5) * 256
+    assert lib.cobra_qkv_attn_workspace_bytes(64, 128, 8, 128) == 64 * 128 * 3 * 1024 * 2
+    assert lib.cobra_qkv_attn_workspace_bytes(1, 16, 1, 264) == -1
+    assert ops.qkv_attn_fused(64, 128, 4, 256) and not ops.qkv_attn_fused(64, 128, 16, 64)
+    # ctx overlapping h on the fused shape; a null workspace on a two-launch shape
+    assert lib.cobra_qkv_attn_fwd(1 << 20, 4096, None, (1 << 20) + 256, None, None, 0, 2, 16, 1, 256, 0.0625, 0,
+                                  None) != 0
+    assert lib.cobra_qkv_attn_fwd(1 << 20, 4096, None, 1 << 24, None, None, 0, 2, 16, 2, 64, 0.125, 0, None) != 0
+
+
 def test_plan_selection_per_config():
     """One fused kernel for S <= 128 at d_model 128 with head_dim 32 or 64, and with
     head_dim 128 for fp16 batches the query-split kernel covers in two rounds of
