@@ -258,24 +258,26 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
                                   : bo + off;
     dma16(src, rP);
   }
-  // W_k rows 32dq .. 32dq+31, in flight while the token tile is still on its way.
-  const char* const wbytes = reinterpret_cast<const char*>(wqkv);
-  dma_span_rows<D, P::N_A / 2>(rWkv, wbytes + (int64_t)(D + 32 * dq) * 2 * D, spans);
-  // The W_v rows are issued from inside LN1, spread evenly over its arithmetic steps.
+  // The W_k and then the W_v rows of d-tile dq are issued from inside LN1, spread
+  // evenly over its arithmetic steps, so that LN1 starts as soon as the token tile is in.
   // The CU's load path drains about one 1 KB transfer per 20 cycles; a wave that
   // issues more than the queue holds stalls at the issue, so transfers issued in one
   // run ahead of LN1 would hold LN1 back until the load path had worked through them
   // all.  Only what the K / V products need is loaded before the first barrier: the
   // W_q rows follow between the first token tiles' products and the W_o rows during
   // the attention, so neither is waited for before the matrix cores start.
-  constexpr int NV = P::N_A / 2, NSLOT = 2 * KD;
-  const char* const wvsrc = wbytes + (int64_t)(2 * D + 32 * dq) * 2 * D;
+  const char* const wbytes = reinterpret_cast<const char*>(wqkv);
+  constexpr int NV = P::N_A / 2, NKV = 2 * NV, NSLOT = 2 * KD;
+  const char* const wksrc = wbytes + (int64_t)(D + 32 * dq) * 2 * D;  // W_k rows, then W_v rows (D rows on)
   const char* const wqsrc = wbytes + (int64_t)qrow0 * 2 * D;
-  auto issue_late = [&](int slot) {  // slot < NSLOT: spans ceil(slot NV / NSLOT) ..
+  auto issue_late = [&](int slot) {  // slot < NSLOT: spans ceil(slot NKV / NSLOT) ..
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = (slot * NV + NSLOT - 1) / NSLOT; j < ((slot + 1) * NV + NSLOT - 1) / NSLOT; ++j)
-      dma16(wvsrc + 1024 * j + spans.off[j % RowSpans<D>::NP], rWkv + P::TILEB + 1024 * j);
+    for (int j = (slot * NKV + NSLOT - 1) / NSLOT; j < ((slot + 1) * NKV + NSLOT - 1) / NSLOT; ++j) {
+      const int jj = j < NV ? j : j - NV;
+      const char* const src = j < NV ? wksrc : wksrc + (int64_t)D * 2 * D;
+      dma16(src + 1024 * jj + spans.off[jj % RowSpans<D>::NP], rWkv + (j < NV ? 0 : P::TILEB) + 1024 * jj);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
     for (int slot = 0; slot < NSLOT; ++slot) issue_late(slot);
   } else {
-  wait_vmcnt<1 + NV>();
+  wait_vmcnt<1>();  // the token tile (the parameter segments may be in flight)
   if constexpr (MASKED) kbits = key_bits_of(kbytes, S, lane);
   {
     f16x8 xc[KD];
