@@ -203,8 +203,27 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
   load_ln1_input((int)blockIdx.x * G + grp);
   // FULL: the first sequence's input is waited for here, and each later one right after
   // the previous sequence's 2 NNT stores (below), so that on both edges into the loop it
-  // is known complete and no wait for outstanding stores lands at the loop's head.
-  if constexpr (FULL) wait_vmcnt<0>();
+  // is known complete and no wait for outstanding stores lands at the loop's head.  The
+  // empty asm statements read the loaded registers: the compiler then counts the loads
+  // as complete at these two points (an explicit s_waitcnt alone does not stop it from
+  // scheduling the loads below the wait, after which the loop head waited as if they
+  // were in flight -- on every later iteration, that drained the previous stores).
+  auto input_complete = [&]() {
+    struct Words {
+      uint32_t u[sizeof(Raw8) / 4];
+    };
+#pragma unroll
+    for (int kk = 0; kk < KD; ++kk) {
+      const Words wd = __builtin_bit_cast(Words, xpre[kk]);
+#pragma unroll
+      for (int i = 0; i < (int)(sizeof(Raw8) / 4); ++i) asm volatile("" ::"v"(wd.u[i]));
+    }
+    if constexpr (MASKED) asm volatile("" ::"v"((uint32_t)kpre.lo), "v"((uint32_t)kpre.hi));
+  };
+  if constexpr (FULL) {
+    wait_vmcnt<0>();
+    input_complete();
+  }
 
   for (int sg = blockIdx.x; sg < ngroups; sg += gridDim.x) {
     const int seq = sg * G + grp;
@@ -232,7 +251,35 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
 
     // ---- LN1: token `tok`, columns 16kk + 8g + e -------------------------------
     f16x8 hB[KD];
-    {
+    if constexpr (sizeof(TX) == 2) {
+      if (!aff1) {
+        // fp16 input, no elementwise affine (the module's case): one pass over the row,
+        // sum and sum of squares by fp16 pair dot products (exact products, fp32
+        // accumulation), variance E[x^2] - mean^2; then h = x rstd - mean rstd as one
+        // mixed-precision fma per element.  No fp32 copy of the row is formed, so LN1
+        // needs few registers of its own (with a 64-register copy, the compiler took the
+        // previous sequence's store data registers and waited for those stores).
+        const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+        float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f16x2 pr = {(f16)xpre[kk][2 * e], (f16)xpre[kk][2 * e + 1]};
+            s1[e & 1] = __builtin_amdgcn_fdot2(pr, one2, s1[e & 1], false);
+            s2[e & 1] = __builtin_amdgcn_fdot2(pr, pr, s2[e & 1], false);
+          }
+        const float mean = sum_xor32(s1[0] + s1[1]) * (1.0f / D);
+        const float ex2 = sum_xor32(s2[0] + s2[1]) * (1.0f / D);
+        const float rstd = rsqrtf(fmaxf(ex2 - mean * mean, 0.f) + eps);
+        const float nmr = -mean * rstd;
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hB[kk][e] = (f16)fmaf((float)xpre[kk][e], rstd, nmr);
+      }
+    }
+    if (sizeof(TX) != 2 || aff1) {
       float xv[KD][8];
       float s = 0.f;
 #pragma unroll
@@ -489,7 +536,10 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) store4(resid_out + row * D + 32 * nt + 8 * qd + 4 * g, v[nt][qd]);
     }
-    if constexpr (FULL) wait_vmcnt<2 * NNT>();  // the prefetch, not the stores behind it
+    if constexpr (FULL) {
+      wait_vmcnt<2 * NNT>();  // the prefetch, not the stores behind it
+      input_complete();
+    }
   }  // sequence loop
 }
 
