@@ -132,8 +132,9 @@ struct XChunks<float> {
 };
 
 // The value `v` of the partner lane (lane ^ 32), any 4-byte-multiple type, through
-// v_permlane32_swap: of the swap's two results one is this lane's own value, the
-// other the partner's (which is which depends on the half; equal bits either way).
+// The value of the partner lane (lane ^ 32), from one v_permlane32_swap per dword: of
+// the swap's two results one is this lane's own value, the other the partner's (which
+// is which depends on the half; equal bits either way).
 template <typename V>
 __device__ __forceinline__ V partner_value(const V& v) {
   constexpr int NDW = sizeof(V) / 4;
@@ -149,6 +150,29 @@ __device__ __forceinline__ V partner_value(const V& v) {
     out.u[d] = r[0] == in.u[d] ? r[1] : r[0];
   }
   return __builtin_bit_cast(V, out);
+}
+
+// Lane-pair exchange of two values in one v_permlane32_swap per dword: the swap trades
+// the upper 32 lanes of its first operand for the lower 32 lanes of its second, so
+// afterwards lanes l < 32 hold (a, a of lane l + 32) and lanes l >= 32 hold
+// (b of lane l - 32, b).  With a, b the two halves of what a lane pair must regroup
+// (lane l keeps the pieces of half 0, lane l + 32 those of half 1), no selects are needed.
+template <typename V>
+__device__ __forceinline__ void swap_halves(V& a, V& b) {
+  constexpr int NDW = sizeof(V) / 4;
+  static_assert(NDW * 4 == sizeof(V), "whole dwords");
+  struct Dw {
+    uint32_t u[NDW];
+  };
+  Dw x = __builtin_bit_cast(Dw, a), y = __builtin_bit_cast(Dw, b);
+#pragma unroll
+  for (int d = 0; d < NDW; ++d) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x.u[d], y.u[d], false, false);
+    x.u[d] = r[0];
+    y.u[d] = r[1];
+  }
+  a = __builtin_bit_cast(V, x);
+  b = __builtin_bit_cast(V, y);
 }
 
 // Query-split variant of the fused kernel (layer_split.hip): fp16

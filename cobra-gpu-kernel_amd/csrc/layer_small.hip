@@ -433,12 +433,20 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
     Raw4 xres[NNT][4];
 #pragma unroll
     for (int kk = 0; kk < KD; ++kk) {
-      const Raw4 lo = {xpre[kk][0], xpre[kk][1], xpre[kk][2], xpre[kk][3]};
-      const Raw4 hi = {xpre[kk][4], xpre[kk][5], xpre[kk][6], xpre[kk][7]};
-      const Raw4 recv = partner_value(g ? lo : hi);  // the half the partner lacks, both ways
-      const int nt = kk / 2, j = kk % 2;             // columns 16kk.. = tile nt, qd 2j and 2j + 1
-      xres[nt][2 * j] = g ? recv : lo;
-      xres[nt][2 * j + 1] = g ? hi : recv;
+      // lane g = 0 keeps columns +0..3 and takes +8..11 from its partner; g = 1 takes
+      // +4..7 and keeps +12..15
+      Raw4 lo = {xpre[kk][0], xpre[kk][1], xpre[kk][2], xpre[kk][3]};
+      Raw4 hi = {xpre[kk][4], xpre[kk][5], xpre[kk][6], xpre[kk][7]};
+      const int nt = kk / 2, j = kk % 2;  // columns 16kk.. = tile nt, qd 2j and 2j + 1
+      if constexpr (L::PARAMS) {
+        swap_halves(lo, hi);
+        xres[nt][2 * j] = lo;
+        xres[nt][2 * j + 1] = hi;
+      } else {  // (see the y exchange below)
+        const Raw4 recv = partner_value(g ? lo : hi);
+        xres[nt][2 * j] = g ? recv : lo;
+        xres[nt][2 * j + 1] = g ? hi : recv;
+      }
     }
     // ---- prefetch: the next sequence's LN1 input --------------------------------------
     load_ln1_input((sg + (int)gridDim.x) * G + grp);
@@ -510,9 +518,18 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
             h0[e] = (f16)o[nt][2 * pr][e];
             h1[e] = (f16)o[nt][2 * pr + 1][e];
           }
-          const f16x4 recv = partner_value(g ? h0 : h1);
-          const f16x4 a = g ? recv : h0, b = g ? h1 : recv;
-          yo[nt][pr] = f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+          if constexpr (L::PARAMS) {
+            swap_halves(h0, h1);  // g = 0: both lanes' quad 2pr; g = 1: both lanes' quad 2pr + 1
+          } else {
+            // Parameters read from global memory (no LDS left for them): with the
+            // select-based exchanges here and for the residual above, the compiler's
+            // schedule of the gamma2 / beta2 loads measured ~8 % faster (head_dim 64).
+            const f16x4 recv = partner_value(g ? h0 : h1);
+            const f16x4 a = g ? recv : h0, b = g ? h1 : recv;
+            h0 = a;
+            h1 = b;
+          }
+          yo[nt][pr] = f16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
         }
       if (tok_ok && live) {
         TX* yrow = y + row * D;

@@ -519,11 +519,10 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
             h0[e] = (f16)acc[t][i][8 * pr + e];
             h1[e] = (f16)acc[t][i][8 * pr + 4 + e];
           }
-          const f16x4 recv = partner_value(g ? h0 : h1);
-          const f16x4 a = g ? recv : h0, b = g ? h1 : recv;
+          swap_halves(h0, h1);  // g = 0: both lanes' quad 2pr; g = 1: both lanes' quad 2pr + 1
           if (m < M)
             *reinterpret_cast<f16x8*>(C + m * N + 32 * NT * w + 32 * t + 16 * pr + 8 * g) =
-                f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                f16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
         }
     }
   }
