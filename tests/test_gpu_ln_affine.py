@@ -36,6 +36,10 @@ CASES = [
     (8, 128, 128, 4, False, False, torch.float32, "fused", None),    # persistent, fp32 activations
     (8, 128, 128, 16, False, False, torch.float32, "staged", None),  # LN1 in the QKV GEMM's prologue
     (2, 128, 1024, 16, False, True, torch.float16, "staged", None),  # LayerNorm pass + LDS-DMA GEMMs
+    # head_dim 256: LayerNorm pass, then the QKV projection fused into the attention
+    (2, 128, 1024, 4, False, False, torch.float16, "staged", None),
+    (3, 77, 1024, 4, True, True, torch.float16, "staged", None),
+    (2, 128, 1024, 4, False, True, torch.float32, "staged", None),
 ]
 
 
