@@ -378,7 +378,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     wv[kk] = tile_chunk<D>(rWkv + P::TILEB, li, 2 * kk + g);
   }
   const float* pp = reinterpret_cast<const float*>(rP);  // the 32-float segments above
-  lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
+  // The barrier that publishes every wave's LN1 output comes after this wave's products
+  // on its own token tile (below): that tile is its own LN1 output (or its own DMA in
+  // the whole-block mode), and the other waves finish their LN1 meanwhile.
 
   // Whole-block mode: the residual entering the block, rows of the slice x columns
   // 32w .. 32w+31 (fp32, 128 bytes a row), into this wave's 4 KB of the residual area,
@@ -438,13 +440,15 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       for (int kk = 0; kk < KD; ++kk)
         hf[buf][kk] = BLK ? tile_chunk<D>(rX + t * P::TILEB, li, 2 * kk + g) : Hb[(t * KD + kk) * 64 + lane];
     };
-    // Tile t - 1 is converted and stored a quarter at a time between the products of
-    // tile t, each quarter pinned after two products (scheduling barriers): the wave
+    // Token tiles in the order w, w + 1, .. (mod 4): step i projects tile tile_of(i).
+    auto tile_of = [&](int i) { return (i + w) & (kSplitTiles - 1); };
+    // Step i - 1's tile is converted and stored a quarter at a time between the products
+    // of step i, each quarter pinned after two products (scheduling barriers): the wave
     // issues instructions in order, so conversions placed after a run of products
     // would leave the matrix cores idle while they execute.
-    auto store_part = [&](int t, int c) {  // c: K half 0, K half 1, V half 0, V half 1
-      const int half = c & 1;
-      const f16x8 o = acc_f16(c < 2 ? ka[t & 1] : va[t & 1], half);
+    auto store_part = [&](int i, int c) {  // c: K half 0, K half 1, V half 0, V half 1
+      const int half = c & 1, t = tile_of(i);
+      const f16x8 o = acc_f16(c < 2 ? ka[i & 1] : va[i & 1], half);
       if constexpr (P::NARROW) {
         if (c < 2)
           Kl[(t * KD + 2 * w + half) * 64 + lane] = o;
@@ -457,22 +461,23 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
           Vl[(((h * kSplitTiles + t) * NDT + t2) * 2 + half) * 64 + lane] = o;
       }
     };
-    auto products = [&](int t) {
-      if (doq && t + 1 < kSplitTiles) issue_wq(t);
+    auto products = [&](int i) {
+      if (doq && i + 1 < kSplitTiles) issue_wq(i);
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
-        const f16x8 hb = hf[t & 1][kk];
-        ka[t & 1] = mfma32x32x16(wk[kk], hb, kk == 0 ? bk : ka[t & 1]);
-        va[t & 1] = mfma32x32x16(hb, wv[kk], kk == 0 ? bv : va[t & 1]);
+        const f16x8 hb = hf[i & 1][kk];
+        ka[i & 1] = mfma32x32x16(wk[kk], hb, kk == 0 ? bk : ka[i & 1]);
+        va[i & 1] = mfma32x32x16(hb, wv[kk], kk == 0 ? bv : va[i & 1]);
         // The next tile's fragments (after the last tile: those of the slice, for
         // Q^T) are requested behind this tile's first two products, never ahead of
         // them.  The first wait for LDS data after an LDS-DMA issue (issue_wq) is
         // compiled as lgkmcnt(0), i.e. it would also wait for requests just made.
-        if (kk == 0) {
+        // Step 0 runs before the barrier: the next tile is another wave's.
+        if (kk == 0 && i > 0) {
           __builtin_amdgcn_sched_barrier(0);
-          fetch(t + 1 < kSplitTiles ? t + 1 : s, (t + 1) & 1);
+          fetch(i + 1 < kSplitTiles ? tile_of(i + 1) : s, (i + 1) & 1);
           // The W_q rows (this wave's own transfers, issued two tiles ago at the latest).
-          if (doq && t + 1 == kSplitTiles) {
+          if (doq && i + 1 == kSplitTiles) {
             wait_vmcnt<0>();
 #pragma unroll
             for (int dt = 0; dt < NQT; ++dt)
@@ -480,15 +485,18 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
               for (int k2 = 0; k2 < KD; ++k2) wq[dt][k2] = tile_chunk<D>(rWq, 32 * dt + li, 2 * k2 + g);
           }
         }
-        if (t >= 1)
+        if (i >= 1)
 #pragma unroll
-          for (int c = kk * 4 / KD; c < (kk + 1) * 4 / KD; ++c) store_part(t - 1, c);
+          for (int c = kk * 4 / KD; c < (kk + 1) * 4 / KD; ++c) store_part(i - 1, c);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    fetch(0, 0);
+    fetch(tile_of(0), 0);
+    products(0);
+    lds_barrier();  // LN1 output of every tile is in LDS; every wave has its weight fragments
+    fetch(tile_of(1), 1);
 #pragma unroll
-    for (int t = 0; t < kSplitTiles; ++t) products(t);
+    for (int i = 1; i < kSplitTiles; ++i) products(i);
     // Q^T of the slice for head w (waves past the last head have none), or d-tile w
     // of the split head, with the last K / V tile stored between its products.
     if (doq) {
@@ -520,6 +528,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c) store_part(kSplitTiles - 1, c);
     }
+  } else {
+    lds_barrier();  // the products' barrier above: LN1 output of every tile is in LDS
   }
   lds_barrier();  // K, V of every token tile and head are in LDS; every W_q read is done
   // W_o rows 32dq .. 32dq+31 into the W_q staging area, free now: they land during the
