@@ -531,7 +531,12 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   } else {
     lds_barrier();  // the products' barrier above: LN1 output of every tile is in LDS
   }
-  lds_barrier();  // K, V of every token tile and head are in LDS; every W_q read is done
+  // K, V of every token tile and head are in LDS; every W_q read is done.  At d_model 128
+  // and head_dim 32 (outside the whole-block mode) no wave needs another's: wave w
+  // projected exactly head w's K and V, runs head w's attention, and its W_q staging
+  // area, which the W_o rows below overwrite, is its own.
+  constexpr bool kOwnHead = D == 128 && HD == 32 && !BLK;
+  if constexpr (!kOwnHead) lds_barrier();
   // W_o rows 32dq .. 32dq+31 into the W_q staging area, free now: they land during the
   // attention.  (Waves past the last output tile fetch tile 0 again, identical bytes
   // to the same place.)
