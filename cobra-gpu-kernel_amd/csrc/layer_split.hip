@@ -584,11 +584,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     f16x8 pB[2];
     float lp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[r], c2, -m));
-      lp[r & 3] += pv;
-      pB[r >> 3][r & 7] = (f16)pv;
-    }
+    for (int r = 0; r < 16; ++r) pB[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[r], c2, -m));
+    add_probs(pB[0], lp[0], lp[1]);  // the fp16 probabilities the P.V product consumes
+    add_probs(pB[1], lp[2], lp[3]);
     const float lt = sum_xor32((lp[0] + lp[1]) + (lp[2] + lp[3]));
     if (g == 0) Stat[(kSplitWaves + w) * 32 + li] = lt;
 #pragma unroll
@@ -646,11 +644,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       for (int t = 0; t < kSplitTiles; ++t) {
         f16x8 pB[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
-          lp[r & 3] += pv;
-          pB[r >> 3][r & 7] = (f16)pv;
-        }
+        for (int r = 0; r < 16; ++r) pB[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
+        add_probs(pB[0], lp[0], lp[1]);  // the fp16 probabilities the P.V product consumes
+        add_probs(pB[1], lp[2], lp[3]);
 #pragma unroll
         for (int half = 0; half < 2; ++half)
           ot = mfma32x32x16(Vl[((t * NNT + w) * 2 + half) * 64 + lane], pB[half], ot);
@@ -712,11 +708,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int t = 0; t < kSplitTiles; ++t) {
       f16x8 pB[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
-        lp[r & 3] += pv;
-        pB[r >> 3][r & 7] = (f16)pv;
-      }
+      for (int r = 0; r < 16; ++r) pB[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[t][r], c2, -m));
+      // The row sum adds the fp16 probabilities the P.V product consumes (pair dot
+      // products against ones, fp32 accumulation: half the vector instructions).
+      add_probs(pB[0], lp[0], lp[1]);
+      add_probs(pB[1], lp[2], lp[3]);
 #pragma unroll
       for (int half = 0; half < 2; ++half)
 #pragma unroll
