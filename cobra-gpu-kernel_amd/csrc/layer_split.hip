@@ -824,18 +824,33 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
         }
         Cx[(2 * w + half) * 64 + lane] = hh;
       }
-    } else if (q_ok) {
+    } else {
+      // y of columns 32w + 8qd + 4g + {0..3}.  The lanes of a pair (g = 0, 1) hold one
+      // row; one v_permlane32_swap per dword regroups quads qd, qd + 1 so that lane g
+      // owns the 8 contiguous columns 32w + 8 (qd + g) .. + 7 and writes them with one
+      // 16-byte store (two stores per lane instead of four of 8 bytes).  Every lane of the
+      // pair takes part in the swap, stored row or not.
       const int64_t row = (int64_t)b * S + qtok;
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int n0 = 32 * w + 8 * qd + 4 * g;
-        const f32x4 gg = *reinterpret_cast<const f32x4*>(pp + 160 + 8 * qd + 4 * g);
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 192 + 8 * qd + 4 * g);
-        float o[4];
+      for (int qp = 0; qp < 4; qp += 2) {
+        f16x4 yh[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (v[qd][e] - mean) * rstd * gg[e] + bb[e];
-        store4(y + row * D + n0, o);
-        if (resid_out) store4(resid_out + row * D + n0, v[qd]);
+        for (int j = 0; j < 2; ++j) {
+          const int qd = qp + j;
+          const f32x4 gg = *reinterpret_cast<const f32x4*>(pp + 160 + 8 * qd + 4 * g);
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 192 + 8 * qd + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) yh[j][e] = (f16)((v[qd][e] - mean) * rstd * gg[e] + bb[e]);
+        }
+        swap_halves(yh[0], yh[1]);
+        if (q_ok) {
+          const f16x8 y8 = {yh[0][0], yh[0][1], yh[0][2], yh[0][3], yh[1][0], yh[1][1], yh[1][2], yh[1][3]};
+          *reinterpret_cast<f16x8*>(y + row * D + 32 * w + 8 * (qp + g)) = y8;
+        }
+      }
+      if (q_ok && resid_out) {
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) store4(resid_out + row * D + 32 * w + 8 * qd + 4 * g, v[qd]);
       }
     }
   }
