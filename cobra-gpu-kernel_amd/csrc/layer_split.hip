@@ -946,22 +946,40 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   const float mean = tot * (1.0f / D);
   const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - mean * mean, 0.f) + eps);
   const float om = tail.mask_out ? rv : 1.f;
-  if (q_ok) {
-    const int64_t row = (int64_t)b * S + qtok;
+  const int64_t row = (int64_t)b * S + qtok;
+  float o[4][4];
 #pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int n0 = 32 * w + 8 * qd + 4 * g;
-      const f32x4 gg = *reinterpret_cast<const f32x4*>(pt + 64 + 8 * qd + 4 * g);
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(pt + 96 + 8 * qd + 4 * g);
-      float o[4];
+  for (int qd = 0; qd < 4; ++qd) {
+    const f32x4 gg = *reinterpret_cast<const f32x4*>(pt + 64 + 8 * qd + 4 * g);
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(pt + 96 + 8 * qd + 4 * g);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = ((v[qd][e] - mean) * rstd * gg[e] + bb[e]) * om;
-      if (tail.y_f32)
-        store4(static_cast<float*>(yv) + row * D + n0, o);
-      else
-        store4(y + row * D + n0, o);
-      store4(resid_out + row * D + n0, v[qd]);
+    for (int e = 0; e < 4; ++e) o[qd][e] = ((v[qd][e] - mean) * rstd * gg[e] + bb[e]) * om;
+  }
+  if (tail.y_f32) {
+    if (q_ok) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) store4(static_cast<float*>(yv) + row * D + 32 * w + 8 * qd + 4 * g, o[qd]);
     }
+  } else {
+    // fp16 y 16 bytes per lane, regrouped across the lane pair as in the sublayer's
+    // epilogue above (every lane takes part in the swap).
+#pragma unroll
+    for (int qp = 0; qp < 4; qp += 2) {
+      f16x4 yh[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yh[j][e] = (f16)o[qp + j][e];
+      swap_halves(yh[0], yh[1]);
+      if (q_ok) {
+        const f16x8 y8 = {yh[0][0], yh[0][1], yh[0][2], yh[0][3], yh[1][0], yh[1][1], yh[1][2], yh[1][3]};
+        *reinterpret_cast<f16x8*>(y + row * D + 32 * w + 8 * (qp + g)) = y8;
+      }
+    }
+  }
+  if (q_ok) {
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) store4(resid_out + row * D + 32 * w + 8 * qd + 4 * g, v[qd]);
   }
 }
 
