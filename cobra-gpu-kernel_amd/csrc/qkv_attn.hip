@@ -252,7 +252,7 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
 
   // ---- O^T (d-tile w) for every query tile, / row sum, -> ctx ----------------------------
   const f16x8* Pf = reinterpret_cast<const f16x8*>(smem + kQaOffP);
-  f16* const crow0 = ctx + (int64_t)b * S * D + hh * kQaHd + 32 * w + 4 * g;
+  f16* const crow0 = ctx + (int64_t)b * S * D + hh * kQaHd + 32 * w;
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4) {
     f32x16 o = zero16();
@@ -261,14 +261,20 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
     const float l = ssum[q4 * 32 + li] + ssum[(q4 + 4) * 32 + li];
     const float inv = MASKED ? (l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f) : __builtin_amdgcn_rcpf(l);
     const int query = 32 * q4 + li;
-    if (query < S) {
-      f16* const crow = crow0 + (int64_t)query * D;
+    // Lane (li, g) holds columns 8q + 4g + {0..3} of its row; one v_permlane32_swap per
+    // dword regroups quads q, q + 1 across the lane pair so that lane g writes the 8
+    // contiguous columns 8 (q + g) .. + 7 with one 16-byte store (every lane swaps).
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        f16x4 hv;
+    for (int qp = 0; qp < 4; qp += 2) {
+      f16x4 hv[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hv[e] = (f16)(o[4 * q + e] * inv);
-        *reinterpret_cast<f16x4*>(crow + 8 * q) = hv;
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hv[j][e] = (f16)(o[4 * (qp + j) + e] * inv);
+      swap_halves(hv[0], hv[1]);
+      if (query < S) {
+        const f16x8 h8 = {hv[0][0], hv[0][1], hv[0][2], hv[0][3], hv[1][0], hv[1][1], hv[1][2], hv[1][3]};
+        *reinterpret_cast<f16x8*>(crow0 + (int64_t)query * D + 8 * (qp + g)) = h8;
       }
     }
   }
