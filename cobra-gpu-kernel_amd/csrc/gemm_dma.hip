@@ -176,15 +176,16 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __rest
 
   // Epilogue in TN slices: slice j holds, for every wave column wn, the 32
   // output columns wn*WTN + j*32 .. +31 (EPW = WN * 32 columns in all), staged
-  // as fp32 rows (+ bias), then written 16 bytes per lane with the residual
-  // added.  Lane li owns row wm*WTM + i*32 + li and, per register quad q,
-  // columns 8q + 4g .. 8q + 4g + 3 of its 32-column block.
+  // as fp32 rows (+ bias), then written 16 bytes per lane (CPL columns: 8 fp16 or 4
+  // fp32) with the residual added.  Lane li owns row wm*WTM + i*32 + li and, per
+  // register quad q, columns 8q + 4g .. 8q + 4g + 3 of its 32-column block.
   float* Cs = reinterpret_cast<float*>(smem);
-  constexpr int LPR = T::EPW / 4;  // lanes per staged row
-  constexpr int RPP = NT / LPR;    // rows per pass
-  static_assert(NT % LPR == 0 && BM % RPP == 0, "epilogue geometry");
-  const int c4 = (tid % LPR) * 4;                                 // column within the slice
-  const int ccol = (c4 / 32) * T::WTN + (c4 % 32);                // column within the tile (+ j*32)
+  constexpr int CPL = 16 / (int)sizeof(TC);  // output columns per lane and store
+  constexpr int LPR = T::EPW / CPL;          // lanes per staged row
+  constexpr int RPP = NT / LPR;              // rows per pass
+  static_assert(NT % LPR == 0 && BM % RPP == 0 && 32 % CPL == 0, "epilogue geometry");
+  const int cl = (tid % LPR) * CPL;                               // column within the slice
+  const int ccol = (cl / 32) * T::WTN + (cl % 32);                // column within the tile (+ j*32)
 #pragma unroll
   for (int j = 0; j < T::TN; ++j) {
 #pragma unroll
@@ -207,37 +208,46 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __rest
     }
     __syncthreads();
     const int n = n0 + ccol + j * 32;
-    if (n < N) {  // N % 8 == 0, so a quad is all in or all out
+    if (n < N) {  // N % 8 == 0, so a lane's CPL columns are all in or all out
       for (int r = tid / LPR; r < BM; r += RPP) {
         const int64_t m = m0 + r;
         if (m >= M) break;
-        f32x4 v = *reinterpret_cast<const f32x4*>(Cs + r * T::LDC + c4);
+        float v[CPL];
+#pragma unroll
+        for (int h = 0; h < CPL / 4; ++h) {
+          const f32x4 t = *reinterpret_cast<const f32x4*>(Cs + r * T::LDC + cl + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * h + e] = t[e];
+        }
         float mv = 1.f;
         if (epi) {
           if (epi & (kEpiMaskBranch | kEpiMaskResid)) mv = row_mask[m] != 0 ? 1.f : 0.f;
           if (epi & kEpiGelu) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+            for (int e = 0; e < CPL; ++e) v[e] = gelu_erf(v[e]);
           }
-          if ((epi & kEpiMaskBranch) && mv == 0.f) v = f32x4{0.f, 0.f, 0.f, 0.f};
+          if ((epi & kEpiMaskBranch) && mv == 0.f) {
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) v[e] = 0.f;
+          }
         }
         if (resid) {
           const TR* rp = resid + m * N + n;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += to_float(rp[e]);
+          for (int e = 0; e < CPL; ++e) v[e] += to_float(rp[e]);
         }
         if (epi & kEpiMaskResid) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] *= mv;
+          for (int e = 0; e < CPL; ++e) v[e] *= mv;
         }
         TC* cp = C + m * N + n;
         if constexpr (sizeof(TC) == 4) {
-          *reinterpret_cast<f32x4*>(cp) = v;
+          *reinterpret_cast<f32x4*>(cp) = f32x4{v[0], v[1], v[2], v[3]};
         } else {
-          f16x4 h;
+          f16x8 hv;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = (f16)v[e];
-          *reinterpret_cast<f16x4*>(cp) = h;
+          for (int e = 0; e < 8; ++e) hv[e] = (f16)v[e];
+          *reinterpret_cast<f16x8*>(cp) = hv;
         }
       }
     }
