@@ -403,6 +403,8 @@ def committed_traffic(path=TRAFFIC_FILE):
 PMC_CONFIGS = {  # --pmc-driver workloads: name -> (B, S, D, H)
     "base": (64, 128, 128, 4), "gemm": (64, 128, 1024, 4), "b10000": (10000, 128, 128, 4),
     "s1024": (64, 1024, 128, 4), "long2": (2, 100000, 1024, 16),
+    "h1": (64, 128, 128, 1), "h2": (64, 128, 128, 2), "h16": (64, 128, 128, 16), "b128": (128, 128, 128, 4),
+    "s32": (64, 32, 128, 4), "b1": (1, 128, 128, 4),
 }
 
 

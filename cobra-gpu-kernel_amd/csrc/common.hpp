@@ -82,6 +82,14 @@ __device__ __forceinline__ float max_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// One value common to both lanes of a pair (l, l ^ 32): v of one of the two
+// lanes.  The first result of the swap holds the same lane's value in both
+// halves (which lane depends only on the operand order), so the pair agrees.
+__device__ __forceinline__ f16 pair_pilot(f16 v) {
+  const uint32_t u = __builtin_bit_cast(uint16_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(f16, (uint16_t)r[0]);
+}
 __device__ __forceinline__ float sum_xor16(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);

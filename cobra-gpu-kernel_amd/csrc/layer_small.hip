@@ -254,24 +254,29 @@ __global__ __launch_bounds__(64 * kSmallWaves * G) void layer_small_kernel(const
     if constexpr (sizeof(TX) == 2) {
       if (!aff1) {
         // fp16 input, no elementwise affine (the module's case): one pass over the row,
-        // sum and sum of squares by fp16 pair dot products (exact products, fp32
-        // accumulation), variance E[x^2] - mean^2; then h = x rstd - mean rstd as one
-        // mixed-precision fma per element.  No fp32 copy of the row is formed, so LN1
-        // needs few registers of its own (with a 64-register copy, the compiler took the
-        // previous sequence's store data registers and waited for those stores).
+        // shifted by a pilot p (one element of the row, common to the lane pair): sums of
+        // d = x - p and d^2 by fp16 pair dot products (exact products, fp32
+        // accumulation), variance E[d^2] - E[d]^2, well conditioned also when the mean is
+        // large against the spread; then h = x rstd - mean rstd as one mixed-precision fma
+        // per element.  No fp32 copy of the row is formed, so LN1 needs few registers of
+        // its own (with a 64-register copy, the compiler took the previous sequence's
+        // store data registers and waited for those stores).
         const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+        const f16 pil = pair_pilot((f16)xpre[0][0]);
+        const f16x2 p2 = {pil, pil};
         float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < KD; ++kk)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const f16x2 pr = {(f16)xpre[kk][2 * e], (f16)xpre[kk][2 * e + 1]};
+            const f16x2 pr = pk_sub_f16(f16x2{(f16)xpre[kk][2 * e], (f16)xpre[kk][2 * e + 1]}, p2);
             s1[e & 1] = __builtin_amdgcn_fdot2(pr, one2, s1[e & 1], false);
             s2[e & 1] = __builtin_amdgcn_fdot2(pr, pr, s2[e & 1], false);
           }
-        const float mean = sum_xor32(s1[0] + s1[1]) * (1.0f / D);
-        const float ex2 = sum_xor32(s2[0] + s2[1]) * (1.0f / D);
-        const float rstd = rsqrtf(fmaxf(ex2 - mean * mean, 0.f) + eps);
+        const float md = sum_xor32(s1[0] + s1[1]) * (1.0f / D);
+        const float ed2 = sum_xor32(s2[0] + s2[1]) * (1.0f / D);
+        const float rstd = rsqrtf(fmaxf(ed2 - md * md, 0.f) + eps);
+        const float mean = (float)pil + md;
         const float nmr = -mean * rstd;
 #pragma unroll
         for (int kk = 0; kk < KD; ++kk)

@@ -301,24 +301,31 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     }
     const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
     if (!aff1) {
-      // One pass over the tile: row sum and sum of squares by fp16 pair dot products
-      // (exact products, fp32 accumulation, independent chains), variance
-      // E[x^2] - mean^2; then h = x rstd - mean rstd, a mixed-precision fma per element
-      // (fp16 x, fp32 arithmetic) and one rounding to fp16.
+      // One pass over the tile, shifted by a pilot value p (one element of the row, the
+      // same in both lanes of the pair): sums of d = x - p and d^2 by fp16 pair dot
+      // products (exact products, fp32 accumulation, independent chains), variance
+      // E[d^2] - E[d]^2.  The shift keeps that difference well conditioned when the
+      // row's mean is large against its spread (E[x^2] - mean^2 loses every digit at a
+      // mean of ~1000 standard deviations); d is rounded to fp16 once, relative to |d|.
+      // Then h = x rstd - mean rstd, a mixed-precision fma per element (fp16 x, fp32
+      // arithmetic) and one rounding to fp16.
+      const f16 pil = pair_pilot(xc[0][0]);
+      const f16x2 p2 = {pil, pil};
       float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const f16x2 pr = {xc[kk][2 * e], xc[kk][2 * e + 1]};
+          const f16x2 pr = pk_sub_f16(f16x2{xc[kk][2 * e], xc[kk][2 * e + 1]}, p2);
           s1[e & 1] = __builtin_amdgcn_fdot2(pr, one2, s1[e & 1], false);
           s2[e & 1] = __builtin_amdgcn_fdot2(pr, pr, s2[e & 1], false);
         }
         issue_late(kk);
       }
-      const float mean = sum_xor32(s1[0] + s1[1]) * (1.0f / D);
-      const float ex2 = sum_xor32(s2[0] + s2[1]) * (1.0f / D);
-      const float rstd = rsqrtf(fmaxf(ex2 - mean * mean, 0.f) + eps);
+      const float md = sum_xor32(s1[0] + s1[1]) * (1.0f / D);
+      const float ed2 = sum_xor32(s2[0] + s2[1]) * (1.0f / D);
+      const float rstd = rsqrtf(fmaxf(ed2 - md * md, 0.f) + eps);
+      const float mean = (float)pil + md;
       const float nmr = -mean * rstd;
 #pragma unroll
       for (int kk = 0; kk < KD; ++kk) {
@@ -747,7 +754,7 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 
   // ---- out^T tile w = W_o[32w..32w+31] ctx^T, + b_o + x, then LN2 ----------------------
   float v[4][4];  // query qtok, column 32w + 8qd + 4g + e
-  float sum = 0.f, sq = 0.f;
+  float sum = 0.f, sq = 0.f, pil2 = 0.f;
   if (w < NNT) {
     // Every attention-output fragment is requested before the first product (one wait).
     f16x8 cf[KD];
@@ -759,6 +766,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     for (int ks = 0; ks < KD; ++ks) oacc = mfma32x32x16(wof[ks], cf[ks], oacc);
     // A padded query's attention output is zero (masked_fill before the residual add).
     const bool qv = !MASKED || kbits.valid(qtok);
+    // LN2's pilot: column 0 of the row's input residual (x, or in the whole-block mode the
+    // fp32 residual entering the block, wave 0's rows), the same value in every wave.
+    pil2 = BLK ? *reinterpret_cast<const float*>(smem + P::OFF_R + li * 128 + 16 * (li & 7))
+               : (float)reinterpret_cast<const f16*>(Raw + li)[0];
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
       const f32x4 bb = *reinterpret_cast<const f32x4*>(pp + 128 + 8 * qd + 4 * g);
@@ -777,12 +788,14 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[qd][e] = (qv ? oacc[4 * qd + e] + bb[e] : 0.f) + xr[e];
-        sum += v[qd][e];
-        sq = fmaf(v[qd][e], v[qd][e], sq);
+        const float d = v[qd][e] - pil2;
+        sum += d;
+        sq = fmaf(d, d, sq);
       }
     }
-    // LN2 statistics in one exchange: each wave's row sums and sums of squares over
-    // its 32 columns; variance E[r^2] - mean^2.
+    // LN2 statistics in one exchange: each wave's row sums and sums of squares of
+    // d = r - pilot over its 32 columns; variance E[d^2] - E[d]^2 (the shift keeps it
+    // well conditioned when the row's mean is large against its spread).
     sum = sum_xor32(sum);
     sq = sum_xor32(sq);
     if (g == 0) {
@@ -800,8 +813,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
       tot += Stat[n * 32 + li];
       tsq += Stat[(kSplitWaves + n) * 32 + li];
     }
-    const float mean = tot * (1.0f / D);
-    const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - mean * mean, 0.f) + eps);
+    const float md = tot * (1.0f / D);
+    const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - md * md, 0.f) + eps);
+    const float mean = pil2 + md;
     if constexpr (BLK) {
       // h2 = LN2(r1) rounded to fp16, into the attention-output area (read by every
       // wave's out-projection before the barrier above) as the B operand of the FFN:
@@ -907,8 +921,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
   f16x8 w2f[KD];
   row_frags(rW2, w2f);
   lds_barrier();  // hidden activations of every tile are in LDS
-  // r2 = (r1 + hid W2^T + b2) * row_valid (TTB:144-145), then the next norm.
+  // r2 = (r1 + hid W2^T + b2) * row_valid (TTB:144-145), then the next norm, its
+  // statistics shifted by LN2's pilot (0 on a padded row, whose r2 is 0).
   const float rv = (!MASKED || kbits.valid(qtok)) ? 1.f : 0.f;
+  const float pil3 = pil2 * rv;
   sum = 0.f;
   sq = 0.f;
   {
@@ -925,8 +941,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[qd][e] = (acc[4 * qd + e] + bb[e] + v[qd][e]) * rv;
-        sum += v[qd][e];
-        sq = fmaf(v[qd][e], v[qd][e], sq);
+        const float d = v[qd][e] - pil3;
+        sum += d;
+        sq = fmaf(d, d, sq);
       }
     }
   }
@@ -943,8 +960,9 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
     tot += Stat[n * 32 + li];
     tsq += Stat[(kSplitWaves + n) * 32 + li];
   }
-  const float mean = tot * (1.0f / D);
-  const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - mean * mean, 0.f) + eps);
+  const float md = tot * (1.0f / D);
+  const float rstd = rsqrtf(fmaxf(tsq * (1.0f / D) - md * md, 0.f) + eps);
+  const float mean = pil3 + md;
   const float om = tail.mask_out ? rv : 1.f;
   const int64_t row = (int64_t)b * S + qtok;
   float o[4][4];

@@ -30,7 +30,7 @@ def _mask(B, S, seed):
 
 
 class Case:
-    def __init__(self, B, S, H, causal, masked, seed=0, last=False, affine_seed=None):
+    def __init__(self, B, S, H, causal, masked, seed=0, last=False, affine_seed=None, offset=0.0):
         self.B, self.S, self.H, self.causal, self.masked, self.last = B, S, H, causal, masked, last
         ref = make_model(OracleTransformerConfig(B, S, D, H, FF, 2, causal), seed=seed)
         if affine_seed is not None:  # non-trivial LayerNorm parameters
@@ -43,7 +43,7 @@ class Case:
         self.ref = ref
         blk = ref.layers[0]
         self.nxt = ref.final_norm if last else ref.layers[1].norm1
-        self.r = make_input(B, S, D, seed=seed + 1)
+        self.r = make_input(B, S, D, seed=seed + 1) + offset
         self.m = _mask(B, S, seed + 2) if masked else None
         with torch.no_grad():
             self.h = F.layer_norm(self.r, (D,), blk.norm1.weight, blk.norm1.bias, 1e-5).half()
@@ -130,6 +130,27 @@ def test_block_last_fp32_output_and_in_place(H):
     assert compare_outputs(want_r, r_b).passed
     pad = ~c.m
     assert torch.equal(out32[pad], torch.zeros_like(out32[pad]))
+
+
+@pytest.mark.parametrize("offset", [300.0, 1000.0])
+@pytest.mark.parametrize("H,causal,masked,last", [(4, False, False, False), (16, True, True, False),
+                                                  (1, True, True, True)])
+def test_block_residual_mean_hundreds_of_deviations(H, causal, masked, last, offset):
+    """r = offset + N(0, 1): LN2 and the next norm see rows whose mean is hundreds of
+    standard deviations off zero (their statistics are shifted by one element of the
+    residual row); padded rows still come out exactly zero in r."""
+    c = Case(4, 100, H, causal, masked, seed=21, last=last, affine_seed=5, offset=offset)
+    log(f"[block offset {offset:g}] H{H} causal={causal} masked={masked} last={last}")
+    r2, out = c.run(torch.float32 if last else torch.float16)
+    want_r, want_o = c.expected()
+    rr = compare_outputs(want_r, r2)
+    ro = compare_outputs(want_o, out)
+    log(f"[block offset {offset:g}] r failed={rr.failed_elements}; out max_abs={ro.max_abs_error:.3e} "
+        f"failed={ro.failed_elements}")
+    assert rr.passed, rr
+    assert ro.passed, ro
+    if masked:
+        assert torch.equal(r2[~c.m], torch.zeros_like(r2[~c.m]))
 
 
 def test_block_rejects_bad_arguments():

@@ -144,3 +144,35 @@ def test_large_mean_input(B, S, D, H, causal, masked, dtype, plan, rows):
     log(f"[large mean] plan={plan} max_abs={res.max_abs_error:.3e} max_rel={res.max_relative_error:.3e} "
         f"failed={res.failed_elements}")
     assert res.passed, res
+
+
+# Offsets of hundreds of standard deviations: a one-pass E[x^2] - mean^2 in fp32 loses
+# the variance entirely near 1000 (every element of a row fails); the kernels shift the
+# sums by one element of the row, which keeps the difference well conditioned.
+OFFSET_CASES = [c for c in CASES if c[6] == torch.float16] + [CASES[6]]
+
+
+@pytest.mark.parametrize("offset", [300.0, 1000.0])
+@pytest.mark.parametrize("B,S,D,H,causal,masked,dtype,plan,rows", OFFSET_CASES,
+                         ids=[f"B{c[0]}-S{c[1]}-D{c[2]}-H{c[3]}-{'c' if c[4] else 'n'}{'m' if c[5] else ''}-"
+                              f"{'f32' if c[6] == torch.float32 else 'f16'}" for c in OFFSET_CASES])
+def test_row_mean_hundreds_of_deviations(B, S, D, H, causal, masked, dtype, plan, rows, offset):
+    """x = offset + N(0, 1) (fp16 rounds it to steps of 0.25-0.5 there; the oracle sees the
+    same rounded x): LN1 and LN2 both see rows whose mean is hundreds of standard
+    deviations off zero, on every plan."""
+    ref, mod = _pair(D, H, dtype=dtype, seed=3)
+    x = offset + make_input(B, S, D, seed=8)
+    if dtype == torch.float16:
+        x = x.half()
+    m = _mask(B, S, 12) if masked else None
+    log(f"[offset {offset:g}] B{B} S{S} D{D} H{H} causal={causal} masked={masked} {dtype}")
+    with torch.inference_mode():
+        y = mod(x.to(DEV), valid_token_mask=None if m is None else m.to(DEV), causal=causal)
+        torch.cuda.synchronize()
+    assert mod.plan == (0 if plan == "fused" else 1)
+    sel = list(range(B)) if rows is None else rows
+    want = oracle_on(ref, x[sel].float(), causal, "cpu", mask=None if m is None else m[sel])
+    res = compare_outputs(want, y.float().cpu()[sel])
+    log(f"[offset {offset:g}] plan={plan} max_abs={res.max_abs_error:.3e} max_rel={res.max_relative_error:.3e} "
+        f"failed={res.failed_elements}")
+    assert res.passed, res
