@@ -124,6 +124,28 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_host = None
+
+
+def host():
+    """The host-side companion module (``cobra_host.so``: the sublayer's native
+    steady-state call), loaded after the C-ABI library it links; raises if missing."""
+    global _host
+    if _host is None:
+        lib()
+        path = os.path.join(os.path.dirname(LIB_PATH), "cobra_host.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build it first (__graft_entry__.build() or "
+                               "python -m cobra_amd.build)")
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("cobra_amd.cobra_host", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _host = mod
+    return _host
+
+
 def check(fn: str, code: int) -> None:
     if code != 0:
         msg = lib().cobra_error_string(code)

@@ -1,8 +1,11 @@
-"""Build recipe for libcobra_amd.so (gfx950) -- plain hipcc, no torch extension.
+"""Build recipe for libcobra_amd.so (gfx950) and its host-side companion.
 
 ``python -m cobra_amd.build`` (with ``cobra-gpu-kernel_amd`` on ``sys.path``)
 compiles every ``csrc/*.hip`` translation unit in parallel and links the
 C-ABI shared library next to this file, where ``cobra_amd._lib`` loads it.
+``csrc/fastpath.cpp`` (host C++ only: the module's steady-state call, against
+torch's C++ API and the C ABI) is compiled with the host compiler alongside and
+linked into ``cobra_host.so`` in the same directory.
 """
 
 from __future__ import annotations
@@ -22,6 +25,8 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 BUILD_DIR = os.path.join(PROJECT_DIR, "_build")
 LIB_NAME = "libcobra_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+HOST_SRC = os.path.join(CSRC, "fastpath.cpp")
+HOST_PATH = os.path.join(PKG_DIR, "cobra_host.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: hipcc -O3 would otherwise emit v_pk_{add,mul,fma}_f32 from
@@ -69,22 +74,60 @@ def _compile(src: str, cc: str) -> str:
     return obj
 
 
+def _host_flags():
+    """Compiler / linker flags of a torch C++ extension on this install (the ones
+    torch.utils.cpp_extension passes for a host-only extension on ROCm)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    inc = ["-I", INCLUDE, "-I", "/opt/rocm/include"]
+    for p in cpp_extension.include_paths():
+        inc += ["-isystem", p]
+    inc += ["-isystem", sysconfig.get_paths()["include"]]
+    cflags = ["-DTORCH_EXTENSION_NAME=cobra_host", "-DTORCH_API_INCLUDE_EXTENSION_H", "-fPIC", "-std=c++17", "-O2",
+              f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}", "-D__HIP_PLATFORM_AMD__=1",
+              "-DUSE_ROCM=1", *inc]
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    ldflags = ["-shared", "-L", PKG_DIR, "-lcobra_amd", "-L", torch_lib, "-lc10_hip", "-lc10", "-ltorch_cpu",
+               "-ltorch", "-ltorch_python", "-Wl,-rpath,$ORIGIN"]
+    return cflags, ldflags
+
+
+def _compile_host() -> str:
+    cflags, _ = _host_flags()
+    obj = os.path.join(BUILD_DIR, "fastpath.o")
+    res = subprocess.run(["c++", *cflags, "-c", HOST_SRC, "-o", obj], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"c++ failed on {HOST_SRC}:\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
 def build(jobs: Optional[int] = None, verbose: bool = False) -> str:
-    """Compile and link; returns the library path.  Always rebuilds."""
+    """Compile and link both libraries; returns the C-ABI library's path.  Always rebuilds."""
     cc = hipcc()
     os.makedirs(BUILD_DIR, exist_ok=True)
     srcs = sources()
-    jobs = jobs or min(len(srcs), os.cpu_count() or 1, 8)
+    jobs = jobs or min(len(srcs) + 1, os.cpu_count() or 1, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        host_obj = ex.submit(_compile_host)
         objs = list(ex.map(lambda s: _compile(s, cc), srcs))
+        host_obj = host_obj.result()
     tmp = LIB_PATH + ".tmp"
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{LIB_NAME}", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    _, ldflags = _host_flags()
+    tmp = HOST_PATH + ".tmp"
+    res = subprocess.run(["c++", host_obj, *ldflags, "-o", tmp], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of {HOST_PATH} failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, HOST_PATH)
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH}\nbuilt {HOST_PATH}")
     return LIB_PATH
 
 

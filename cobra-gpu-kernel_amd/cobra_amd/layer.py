@@ -100,9 +100,11 @@ class _Pack:
 
 class _Fast:
     """The steady-state launch of one input signature: ``cobra_layer_fwd`` bound
-    (``cobra_layer_bind``) with everything but x, y and the stream."""
+    (``cobra_layer_bind``) with everything but x, y and the stream, and the native
+    call around it (``cobra_host.BoundForward``: checks x's signature, the parameters'
+    versions and norm1's eps, allocates y, launches on the current stream)."""
 
-    __slots__ = ("shape", "dtype", "device", "causal", "eps", "versions", "launch", "handle", "run")
+    __slots__ = ("launch", "call")
 
 
 class CobraAttentionSublayer(nn.Module):
@@ -113,6 +115,7 @@ class CobraAttentionSublayer(nn.Module):
         self.norm1 = nn.LayerNorm(d_model, eps=eps)
         self.attention = CobraSelfAttention(d_model, num_heads)
         self.norm2 = nn.LayerNorm(d_model, eps=eps)
+        self._fast: Optional[_Fast] = None
         self.causal = causal
         # hipGraph replay: None / False = direct launches (cheaper for the one to five
         # launches of a sublayer on this runtime); True = replay a captured graph for
@@ -132,7 +135,16 @@ class CobraAttentionSublayer(nn.Module):
         self._static_y: Optional[torch.Tensor] = None
         self._static_r: Optional[torch.Tensor] = None
         self._static_m: Optional[torch.Tensor] = None
-        self._fast: Optional[_Fast] = None
+
+    @property
+    def causal(self) -> bool:
+        return self._causal
+
+    @causal.setter
+    def causal(self, value: bool) -> None:
+        # The bound steady-state launch has the mode baked in.
+        self._causal = bool(value)
+        self._fast = None
 
     # -- parameters ---------------------------------------------------------
 
@@ -170,20 +182,16 @@ class CobraAttentionSublayer(nn.Module):
         causal: Optional[bool] = None,
         return_residual: bool = False,
     ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
-        # Steady state of the common call (same input signature, no mask, weights
-        # unchanged): one allocation and the library call.  At the small shapes the
-        # kernel takes less time than the Python around it, so this path is what
-        # back-to-back forwards are bound by.
+        # Steady state of the common call (same input signature, no mask, weights and
+        # eps unchanged): the native call checks all of that, allocates y and launches;
+        # it returns None for any other call.  At the small shapes the kernel takes
+        # ~7 us, as long as the checks, the allocation and the launch took from
+        # Python, so this path is what back-to-back forwards are bound by.
         f = self._fast
-        if (f is not None and valid_token_mask is None and causal is None and not return_residual
-                and x.shape == f.shape and x.dtype == f.dtype and x.is_cuda and x.is_contiguous()
-                and x.get_device() == f.device and self.causal == f.causal and self.norm1.eps == f.eps
-                and self._versions() == f.versions):
-            y = torch.empty_like(x)
-            code = f.run(f.handle, x.data_ptr(), None, y.data_ptr(), None, ops.raw_stream(f.device))
-            if code:
-                ops.check_code("cobra_layer_fwd", code)
-            return y
+        if f is not None and valid_token_mask is None and causal is None and not return_residual:
+            y = f.call(x)
+            if y is not None:
+                return y
         fast_ok = valid_token_mask is None and causal is None and not return_residual
         causal = self.causal if causal is None else bool(causal)
         pack = self._packed()
@@ -209,14 +217,15 @@ class CobraAttentionSublayer(nn.Module):
         return out
 
     def _make_fast(self, x: torch.Tensor, pack: _Pack) -> _Fast:
+        from . import _lib
+
         f = _Fast()
-        f.shape, f.dtype, f.device = x.shape, x.dtype, x.get_device()
-        f.causal, f.eps, f.versions = self.causal, self.norm1.eps, pack.versions
         B, S, D = x.shape
         f.launch = ops.LayerLaunch(x.dtype, False, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w,
                                    pack.ln1_b, pack.ln2_w, pack.ln2_b, self._ws, B, S, D,
                                    self.attention.num_heads, self.causal, self.norm1.eps)
-        f.handle, f.run = f.launch.handle, f.launch.run_fn
+        f.call = _lib.host().BoundForward(f.launch.handle, x, self._params, list(pack.versions), self.norm1,
+                                          float(self.norm1.eps), ops.check_code).__call__
         return f
 
     # -- planning -------------------------------------------------------------

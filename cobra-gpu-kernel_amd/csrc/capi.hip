@@ -440,6 +440,11 @@ struct cobra_layer_launch {
   void* workspace;
   int64_t workspace_bytes, batch, seq_len, d_model, heads;
   float eps;
+  // The query-split kernel's launch resolved at bind time (plan, variant, grid and
+  // arguments), so a run costs one hipLaunchKernel: at the small shapes that kernel
+  // takes ~7 us and the host's launch path is most of a forward's host time.
+  bool split;
+  cobra::SplitLaunch sl;
 };
 
 cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv, const float* b_qkv, const void* w_o,
@@ -457,13 +462,22 @@ cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv,
   auto* h = new (std::nothrow) cobra_layer_launch;
   if (!h) return nullptr;
   *h = cobra_layer_launch{x_dtype, masked ? 1 : 0, causal ? 1 : 0, w_qkv, b_qkv, b_o, ln1_w, ln1_b, ln2_w, ln2_b,
-                          w_o, workspace, workspace_bytes, batch, seq_len, d_model, heads, eps};
+                          w_o, workspace, workspace_bytes, batch, seq_len, d_model, heads, eps, false, {}};
+  if (plan == COBRA_PLAN_FUSED && batch > 0) {
+    cobra::SmallLayerArgs a{nullptr, x_dtype, w_qkv,   b_qkv,   w_o,   b_o,          ln1_w, ln1_b, ln2_w, ln2_b,
+                            nullptr, nullptr, batch, seq_len, d_model, heads, causal ? 1 : 0, eps, nullptr};
+    h->split = cobra::prepare_layer_split(a, &h->sl);
+  }
   return h;
 }
 
 int cobra_layer_run(const cobra_layer_launch* h, const void* x, const uint8_t* valid_mask, void* y, float* resid_out,
                     void* stream) {
   if (!h || (valid_mask && !h->masked)) return kBad;
+  if (h->split) {
+    if (!x || !aligned16(x) || !y || !aligned16(y) || !opt_aligned16(resid_out)) return kBad;
+    return code(cobra::launch_layer_split(h->sl, x, valid_mask, y, resid_out, static_cast<hipStream_t>(stream)));
+  }
   return cobra_layer_fwd(x, h->x_dtype, valid_mask, h->w_qkv, h->b_qkv, h->w_o, h->b_o, h->ln1_w, h->ln1_b, h->ln2_w,
                          h->ln2_b, y, resid_out, h->workspace, h->workspace_bytes, h->batch, h->seq_len, h->d_model,
                          h->heads, h->causal, h->eps, stream);

@@ -184,6 +184,44 @@ bool layer_small_ok(int64_t seq_len, int64_t d_model, int64_t heads);
 bool layer_fused_ok(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int x_dtype);
 hipError_t run_layer_small(const SmallLayerArgs& a);
 
+// Arguments of the query-split fused kernel (layer_split.hip), one struct of 112 bytes
+// passed by value: the HIP runtime's host cost per launch grows with the number of
+// kernel arguments and with their size past ~128 bytes (2.9 us for this struct against
+// 3.7 us for the same bytes as 16 arguments, and 3.7 us for a 184-byte struct).  Order:
+// everything the first transfers need (S, the grid size, x, W_qkv and the parameter
+// rows) comes first, in the first 56 bytes of the argument block, which one scalar
+// load returns; `nblk` is gridDim.x, passed explicitly so the tile mapping does not
+// wait on a second load of the dispatch's hidden arguments.
+struct SplitArgs {
+  int S, nblk;
+  const _Float16* x;
+  const _Float16* wqkv;
+  const float* bqkv;
+  const float* bo;
+  const float* g2;
+  const float* be2;
+  const _Float16* wo;
+  const float* g1;    // LN1's elementwise affine (null: none)
+  const float* be1;
+  void* y;
+  float* resid_out;   // optional fp32 residual
+  float c2, eps;      // softmax scale * log2(e); LayerNorm epsilon
+  const uint8_t* vmask;  // [B, S] token mask (masked variant only)
+};
+static_assert(sizeof(SplitArgs) == 112, "kernel argument block");
+// One call of the query-split kernel resolved once (shape checks, variant, grid,
+// arguments); x, y, the token mask and the residual output are set per launch.
+struct SplitLaunch {
+  const void* fn[2];  // kernel without / with a token mask
+  unsigned grid;
+  SplitArgs args;
+};
+// Whether run_layer_small would take the query-split kernel for this call.
+bool layer_split_takes(const SmallLayerArgs& a);
+bool prepare_layer_split(const SmallLayerArgs& a, SplitLaunch* l);
+hipError_t launch_layer_split(const SplitLaunch& l, const void* x, const uint8_t* valid_mask, void* y,
+                              float* resid_out, hipStream_t stream);
+
 // One transformer block of the fused stack in one launch (the query-split kernel's
 // whole-block mode): h = norm1(r) fp16 in, r fp32 in, r_out / out written.
 struct BlockArgs {

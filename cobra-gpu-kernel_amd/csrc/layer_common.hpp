@@ -180,6 +180,6 @@ __device__ __forceinline__ void swap_halves(V& a, V& b) {
 // while batch * ceil(S/32) workgroups take at most two rounds of the chip.
 bool layer_split_ok(int64_t seq_len, int64_t d_model, int64_t heads);
 bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dtype);
-hipError_t run_layer_split(const SmallLayerArgs& a, float c2);
+hipError_t run_layer_split(const SmallLayerArgs& a);
 
 }  // namespace cobra

@@ -635,10 +635,9 @@ hipError_t run_layer_small(const SmallLayerArgs& a) {
   if (a.batch < 0 || a.batch > 0x7fffffff || !layer_fused_ok(a.batch, a.seq_len, a.d_model, a.heads, a.x_dtype))
     return hipErrorInvalidValue;
   if (a.batch == 0) return hipSuccess;
+  if (layer_split_takes(a)) return run_layer_split(a);
   const double hd = (double)(a.d_model / a.heads);
   const float c2 = (float)(1.0 / sqrt(hd)) * 1.4426950408889634f;
-  if (layer_split_ok(a.seq_len, a.d_model, a.heads) && layer_split_pays(a.batch, a.seq_len, a.d_model, a.x_dtype))
-    return run_layer_split(a, c2);
   return a.causal ? small_shape<true>(a, c2) : small_shape<false>(a, c2);
 }
 

@@ -168,17 +168,37 @@ struct BlockTail {
   int mask_out;       // multiply the normalised output of padded rows by 0
 };
 
-// Argument order: everything the first transfers need (S, the grid size, x, W_qkv and
-// the parameter rows) comes first, in the first 56 bytes of the argument block, which
-// one scalar load returns; `nblk` is gridDim.x, passed explicitly so the tile mapping
-// does not wait on a second load of the dispatch's hidden arguments.
+// The whole-block mode adds the rest of the block.
+template <bool BLK>
+struct SplitKArgs : SplitArgs {};
+template <>
+struct SplitKArgs<true> : SplitArgs {
+  BlockTail tail;
+};
+
 // AFF1: LN1 with an elementwise affine (g1 / be1 non-null; never in whole-block mode).
 template <int D, int HD, bool CAUSAL, bool MASKED, bool BLK, bool AFF1>
-__global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(
-    int S, int nblk, const f16* __restrict__ x, const f16* __restrict__ wqkv, const float* __restrict__ bqkv,
-    const float* __restrict__ bo, const float* __restrict__ g2, const float* __restrict__ be2,
-    const f16* __restrict__ wo, const float* __restrict__ g1, const float* __restrict__ be1, void* __restrict__ yv,
-    float* resid_out, float c2, float eps, const uint8_t* __restrict__ vmask, BlockTail tail) {
+__global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(const SplitKArgs<BLK> ka) {
+  const int S = ka.S, nblk = ka.nblk;
+  const f16* __restrict__ x = ka.x;
+  const f16* __restrict__ wqkv = ka.wqkv;
+  const float* __restrict__ bqkv = ka.bqkv;
+  const float* __restrict__ bo = ka.bo;
+  const float* __restrict__ g2 = ka.g2;
+  const float* __restrict__ be2 = ka.be2;
+  const f16* __restrict__ wo = ka.wo;
+  const float* __restrict__ g1 = ka.g1;
+  const float* __restrict__ be1 = ka.be1;
+  void* __restrict__ yv = ka.y;
+  float* resid_out = ka.resid_out;
+  const float c2 = ka.c2, eps = ka.eps;
+  const uint8_t* __restrict__ vmask = ka.vmask;
+  const BlockTail tail = [&] {
+    if constexpr (BLK)
+      return ka.tail;
+    else
+      return BlockTail{};
+  }();
   using P = SplitPlan<D, HD, BLK>;
   constexpr int KD = P::KD, NNT = P::NNT, H = P::H, NDT = P::NDT, KSH = P::KSH, NQT = P::NQT;
   // Whole-block mode: the FFN's hidden width equals d_model, one 32-wide tile per wave.
@@ -1017,36 +1037,68 @@ bool layer_split_pays(int64_t batch, int64_t seq_len, int64_t d_model, int x_dty
   return items <= 2 * (int64_t)compute_units();
 }
 
+// The launch of one call, resolved once: kernel variant (with and without a token mask)
+// and argument block; x, y, the mask and the residual output are filled in per launch.
 template <int D, int HD, bool CAUSAL>
-static hipError_t launch_split(const SmallLayerArgs& a, float c2) {
-  const int64_t grid = a.batch * ((a.seq_len + 31) / 32);
-  if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  auto kern = a.ln1_w ? (a.valid_mask ? layer_split_kernel<D, HD, CAUSAL, true, false, true>
-                                      : layer_split_kernel<D, HD, CAUSAL, false, false, true>)
-                      : (a.valid_mask ? layer_split_kernel<D, HD, CAUSAL, true, false, false>
-                                      : layer_split_kernel<D, HD, CAUSAL, false, false, false>);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, (int)a.seq_len, (int)grid,
-                     static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv), a.b_qkv, a.b_o, a.ln2_w, a.ln2_b,
-                     static_cast<const f16*>(a.w_o), a.ln1_w, a.ln1_b, a.y, a.resid_out, c2, a.eps, a.valid_mask,
-                     BlockTail{});
-  return hipGetLastError();
+static void prepare_split(const SmallLayerArgs& a, float c2, SplitLaunch* l) {
+  const bool aff1 = a.ln1_w != nullptr;
+  l->fn[0] = aff1 ? (const void*)layer_split_kernel<D, HD, CAUSAL, false, false, true>
+                  : (const void*)layer_split_kernel<D, HD, CAUSAL, false, false, false>;
+  l->fn[1] = aff1 ? (const void*)layer_split_kernel<D, HD, CAUSAL, true, false, true>
+                  : (const void*)layer_split_kernel<D, HD, CAUSAL, true, false, false>;
+  l->grid = (unsigned)(a.batch * ((a.seq_len + 31) / 32));
+  SplitArgs& k = l->args;
+  k = SplitArgs{(int)a.seq_len, (int)l->grid, static_cast<const f16*>(a.x), static_cast<const f16*>(a.w_qkv),
+                a.b_qkv, a.b_o, a.ln2_w, a.ln2_b, static_cast<const f16*>(a.w_o), a.ln1_w, a.ln1_b, a.y,
+                a.resid_out, c2, a.eps, a.valid_mask};
 }
 
 template <bool CAUSAL>
-static hipError_t split_shape(const SmallLayerArgs& a, float c2) {
+static void split_shape(const SmallLayerArgs& a, float c2, SplitLaunch* l) {
   const int64_t hd = a.d_model / a.heads;
   if (a.d_model == 128) {
-    if (hd == 8) return launch_split<128, 8, CAUSAL>(a, c2);
-    if (hd == 32) return launch_split<128, 32, CAUSAL>(a, c2);
-    if (hd == 64) return launch_split<128, 64, CAUSAL>(a, c2);
-    return launch_split<128, 128, CAUSAL>(a, c2);
+    if (hd == 8) return prepare_split<128, 8, CAUSAL>(a, c2, l);
+    if (hd == 32) return prepare_split<128, 32, CAUSAL>(a, c2, l);
+    if (hd == 64) return prepare_split<128, 64, CAUSAL>(a, c2, l);
+    return prepare_split<128, 128, CAUSAL>(a, c2, l);
   }
-  return hd == 32 ? launch_split<64, 32, CAUSAL>(a, c2) : launch_split<64, 64, CAUSAL>(a, c2);
+  return hd == 32 ? prepare_split<64, 32, CAUSAL>(a, c2, l) : prepare_split<64, 64, CAUSAL>(a, c2, l);
 }
 
-// Shape and dtype checks are the caller's (run_layer_small: layer_split_ok, layer_split_pays).
-hipError_t run_layer_split(const SmallLayerArgs& a, float c2) {
-  return a.causal ? split_shape<true>(a, c2) : split_shape<false>(a, c2);
+bool layer_split_takes(const SmallLayerArgs& a) {
+  return layer_split_ok(a.seq_len, a.d_model, a.heads) && layer_split_pays(a.batch, a.seq_len, a.d_model, a.x_dtype);
+}
+
+static float split_c2(const SmallLayerArgs& a) {
+  const double hd = (double)(a.d_model / a.heads);
+  return (float)(1.0 / sqrt(hd)) * 1.4426950408889634f;
+}
+
+bool prepare_layer_split(const SmallLayerArgs& a, SplitLaunch* l) {
+  if (!layer_split_takes(a) || a.batch < 1 || a.batch * ((a.seq_len + 31) / 32) > 0x7fffffff) return false;
+  const float c2 = split_c2(a);
+  if (a.causal)
+    split_shape<true>(a, c2, l);
+  else
+    split_shape<false>(a, c2, l);
+  return true;
+}
+
+hipError_t launch_layer_split(const SplitLaunch& l, const void* x, const uint8_t* valid_mask, void* y,
+                              float* resid_out, hipStream_t stream) {
+  SplitArgs k = l.args;
+  k.x = static_cast<const f16*>(x);
+  k.vmask = valid_mask;
+  k.y = y;
+  k.resid_out = resid_out;
+  void* args[] = {&k};
+  return hipLaunchKernel(l.fn[valid_mask ? 1 : 0], dim3(l.grid), dim3(64 * kSplitWaves), args, 0, stream);
+}
+
+hipError_t run_layer_split(const SmallLayerArgs& a) {
+  SplitLaunch l;
+  if (!prepare_layer_split(a, &l)) return hipErrorInvalidValue;
+  return launch_layer_split(l, a.x, a.valid_mask, a.y, a.resid_out, a.stream);
 }
 
 // ---- whole-block mode -------------------------------------------------------------------
@@ -1063,13 +1115,16 @@ template <int HD, bool CAUSAL>
 static hipError_t launch_block(const BlockArgs& a, float c2) {
   const int64_t grid = a.batch * ((a.seq_len + 31) / 32);
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
-  const BlockTail tail{a.r, static_cast<const f16*>(a.w1), a.b1, static_cast<const f16*>(a.w2), a.b2, a.lnn_w,
-                       a.lnn_b, a.out_dtype == kF32, a.mask_out};
+  SplitKArgs<true> k;
+  static_cast<SplitArgs&>(k) =
+      SplitArgs{(int)a.seq_len, (int)grid, static_cast<const f16*>(a.h), static_cast<const f16*>(a.w_qkv), a.b_qkv,
+                a.b_o, a.ln2_w, a.ln2_b, static_cast<const f16*>(a.w_o), nullptr, nullptr, a.out, a.r_out, c2, a.eps,
+                a.valid_mask};
+  k.tail = BlockTail{a.r, static_cast<const f16*>(a.w1), a.b1, static_cast<const f16*>(a.w2), a.b2, a.lnn_w,
+                     a.lnn_b, a.out_dtype == kF32, a.mask_out};
   auto kern = a.valid_mask ? layer_split_kernel<128, HD, CAUSAL, true, true, false>
                            : layer_split_kernel<128, HD, CAUSAL, false, true, false>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, (int)a.seq_len, (int)grid,
-                     static_cast<const f16*>(a.h), static_cast<const f16*>(a.w_qkv), a.b_qkv, a.b_o, a.ln2_w, a.ln2_b,
-                     static_cast<const f16*>(a.w_o), nullptr, nullptr, a.out, a.r_out, c2, a.eps, a.valid_mask, tail);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, k);
   return hipGetLastError();
 }
 

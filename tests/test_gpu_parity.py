@@ -274,6 +274,30 @@ def test_steady_state_fast_path():
         y3 = mod(x3).clone()
         torch.cuda.synchronize()
     assert compare_outputs(oracle_on(ref, x3.float().cpu(), False, "cpu"), y3.float().cpu()).passed
+    # The native steady-state call: a new output tensor per call; a changed eps, a
+    # non-contiguous input or an input on the stream of another torch stream context
+    # all give what the full path gives.
+    with torch.inference_mode():
+        a = mod(x3)
+        b = mod(x3)
+        assert mod._fast is not None and a.data_ptr() != b.data_ptr() and torch.equal(a, b)
+        mod.norm1.eps = 1e-2
+        y_e = mod(x3).clone()
+        y_e_full = mod(x3, causal=False).clone()
+        mod.norm1.eps = 1e-5
+        xt = make_input(77, 3, 128, seed=5).half().to(DEV).transpose(0, 1)
+        y_t = mod(xt).clone()
+        y_t_full = mod(xt.contiguous(), causal=False).clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            y_s = mod(x3)
+        torch.cuda.current_stream().wait_stream(side)
+        y_s = y_s.clone()
+        torch.cuda.synchronize()
+    assert torch.equal(y_e, y_e_full) and not torch.equal(y_e, y3)
+    assert torch.equal(y_t, y_t_full)
+    assert torch.equal(y_s, y3)
 
 
 # ---- op-level wrappers against fp32 references of the same op -------------

@@ -94,6 +94,22 @@ def test_layer_bind_validates_and_releases():
                                1e-5, None) != 0
 
 
+def test_host_companion_loads_and_checks_its_arguments():
+    """cobra_host.so (the module's native steady-state call, linked against the C ABI
+    and torch) loads without a GPU and rejects a null launch handle, a host input and
+    a parameter list without one snapshot value per tensor, before any launch."""
+    from cobra_amd import _lib
+
+    host = _lib.host()
+    x = torch.zeros(2, 16, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="null launch handle"):
+        host.BoundForward(0, x, [], [], None, 1e-5, None)
+    with pytest.raises(RuntimeError, match="device tensor"):
+        host.BoundForward(256, x, [], [], None, 1e-5, None)
+    with pytest.raises(RuntimeError, match="one snapshot value"):
+        host.BoundForward(256, x, [x], [], None, 1e-5, None)
+
+
 def test_ln1_fold_matches_layernorm_then_projection():
     """The module's packed QKV weights carry LN1's affine: LayerNorm without affine
     followed by the folded projection equals LayerNorm with affine followed by the
