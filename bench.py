@@ -109,6 +109,22 @@ def in_graph_ms(fn, n=50, reps=5):
     return event_ms(g.replay, reps) / n
 
 
+def host_us_per_call(fn, bursts=50, n=200):
+    """Host time of one fn() call, in us: perf_counter_ns over bursts of n calls, each
+    burst started after a synchronisation (so the launch queue never fills and blocks
+    the host), median of the bursts; 10k calls by default.  When it exceeds the kernel
+    time, back-to-back forwards are bound by the host."""
+    out = []
+    for _ in range(bursts):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter_ns()
+        for _ in range(n):
+            fn()
+        out.append((time.perf_counter_ns() - t0) / n / 1e3)
+    torch.cuda.synchronize()
+    return statistics.median(out)
+
+
 def layer_launcher(layer, x, y):
     """The module's own kernel launch for (x -> y), allocation-free (graph-capturable)."""
     from cobra_amd import ops
@@ -500,6 +516,7 @@ def main() -> int:
         t1.record(stream)
         torch.cuda.synchronize()
         ms = t0.elapsed_time(t1) / args.steps
+        host_us = host_us_per_call(lambda: layer(x))
         # the dominant (here: the only) kernel -- the query-split fused kernel at
         # this batch -- launch gaps excluded
         k_ms = in_graph_ms(layer_launcher(layer, x, torch.empty_like(x)), n=50, reps=5)
@@ -527,6 +544,7 @@ def main() -> int:
         "data": "synthetic: x ~ N(0,1) seed 0 (CPU generator), nn.Linear default init under manual_seed(0)",
         "config": {"workload": "attention sublayer fwd B64 d128 H4 S128 fp16 non-causal (one fused kernel)",
                    "batch": B, "seq_len": S, "d_model": D, "heads": H, "causal": False},
+        "host_us_per_forward": host_us,
         "mfma_frac": tflops / PEAK_FP16_TFLOPS,
         "hbm_gbs": layer_bytes(B, S, D) / (ms / 1e3) / 1e9,
         "roofline": dict(roofline("layer_split_kernel", flops, layer_bytes(B, S, D), k_ms),
@@ -535,7 +553,7 @@ def main() -> int:
                   "note": "the fused plan launches one kernel directly; replaying it as a hipGraph is slower"},
     }
     log(f"[bench] base: {ms * 1e3:.2f} us/forward, {tflops:.2f} TFLOP/s; kernel {k_ms * 1e3:.2f} us; "
-        f"graph replay {g_ms * 1e3:.2f} us")
+        f"host {host_us:.2f} us/call; graph replay {g_ms * 1e3:.2f} us")
     peaks = line["measured_peaks"] = measured_peaks(dev)
     line["measured_mfma_frac"] = tflops / peaks["fp16_gemm_8192_tflops"]
     line["measured_hbm_frac"] = line["hbm_gbs"] / peaks["device_copy_gbs"]
