@@ -213,7 +213,7 @@ static_assert(sizeof(SplitArgs) == 112, "kernel argument block");
 // arguments); x, y, the token mask and the residual output are set per launch.
 struct SplitLaunch {
   const void* fn[2];  // kernel without / with a token mask
-  unsigned grid;
+  unsigned grid, block;
   SplitArgs args;
 };
 // Whether run_layer_small would take the query-split kernel for this call.

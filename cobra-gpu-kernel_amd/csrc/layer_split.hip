@@ -1077,6 +1077,7 @@ static float split_c2(const SmallLayerArgs& a) {
 bool prepare_layer_split(const SmallLayerArgs& a, SplitLaunch* l) {
   if (!layer_split_takes(a) || a.batch < 1 || a.batch * ((a.seq_len + 31) / 32) > 0x7fffffff) return false;
   const float c2 = split_c2(a);
+  l->block = 64 * kSplitWaves;
   if (a.causal)
     split_shape<true>(a, c2, l);
   else
@@ -1092,7 +1093,7 @@ hipError_t launch_layer_split(const SplitLaunch& l, const void* x, const uint8_t
   k.y = y;
   k.resid_out = resid_out;
   void* args[] = {&k};
-  return hipLaunchKernel(l.fn[valid_mask ? 1 : 0], dim3(l.grid), dim3(64 * kSplitWaves), args, 0, stream);
+  return hipLaunchKernel(l.fn[valid_mask ? 1 : 0], dim3(l.grid), dim3(l.block), args, 0, stream);
 }
 
 hipError_t run_layer_split(const SmallLayerArgs& a) {
