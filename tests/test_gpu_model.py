@@ -101,6 +101,32 @@ def test_long_sequence_sampled():
     assert res.passed, res
 
 
+def test_case14_full_length():
+    """Case 14 of the reference's matrix (tools/sweep.py:31-47) at its full length: d_model 1024,
+    16 heads, ffn 1024, 2 layers, causal, S = 100000.  Two sequences run through the stack (the
+    reference validated the same B = 2 subset of its B = 32 case, report/measurements/02_case14.md:
+    100-113, method tools/sweep.py:93-139; sequences are independent, TTB:1446-1450) and are
+    checked against the fp32 oracle model on the GPU with queries in blocks of 4096, keys past
+    each block's last query never formed (tools/reference_chunked.py:94-121)."""
+    cfg = (2, 100000, 1024, 16, 1024, 2, True)
+    ref, mod = build(cfg)
+    x = make_input(2, 100000, 1024, seed=14).half()
+    log("[case14 full] stack forward")
+    with torch.inference_mode():
+        y = mod(x.to(DEV)).float().cpu()
+        torch.cuda.synchronize()
+    log("[case14 full] oracle forward")
+    layer = ref.to(DEV)
+    try:
+        want = model_forward(layer, x.to(DEV), block_q=4096).cpu()
+    finally:
+        ref.to("cpu")
+    res = compare_outputs(want, y)
+    log(f"[case14 full] max_abs={res.max_abs_error:.3e} max_rel={res.max_relative_error:.3e} "
+        f"failed={res.failed_elements}/{res.total_elements}")
+    assert res.passed, res
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("pad", [0.3, 0.9])
 def test_padded(causal, pad):
