@@ -15,7 +15,7 @@ from typing import Optional
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcobra_amd.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 F16 = 0
 F32 = 1
@@ -39,6 +39,11 @@ SIGNATURES = {
     "cobra_error_string": (ctypes.c_char_p, [_c_int]),
     "cobra_ln_fwd": (
         _c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _c_i64, _c_i64, _c_f32, _vp],
+    ),
+    "cobra_ln_fwd_strided": (
+        _c_int,
+        [_vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _vp, _c_int, _vp, _c_i64, _vp, _c_int, _c_i64, _c_i64,
+         _c_i64, _c_f32, _vp],
     ),
     "cobra_linear_fwd": (
         _c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp],

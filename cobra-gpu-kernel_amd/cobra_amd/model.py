@@ -82,24 +82,75 @@ class CobraTransformerBlock(nn.Module):
         self.ffn_out = nn.Linear(ffn_dim, d_model)
 
 
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
+
+
+class PadGeometry:
+    """Widths the kernels run a block at: d_model, ffn_dim and head_dim rounded up to
+    multiples of 8 (16-byte rows for the GEMMs' LDS-DMA tiles and the attention's
+    operand fragments).  The reference's stack accepts any ``d_model % heads == 0``
+    (TTB:30-57) and sends such shapes to SDPA / ``F.linear`` (TTB:1030-1071); here they
+    run on the same kernels with zero-padded weights."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+        self.d, self.heads, self.f = d_model, num_heads, ffn_dim
+        self.hd = d_model // num_heads
+        self.hdp = _round8(self.hd)
+        self.e = num_heads * self.hdp  # padded width of q, k, v and of the attention output
+        self.dp = _round8(d_model)
+        self.fp = _round8(ffn_dim)
+
+    @property
+    def needed(self) -> bool:
+        return (self.dp, self.hdp, self.fp) != (self.d, self.hd, self.f)
+
+
+def pad_block_weights(w_qkv, b_qkv, w_o, b_o, w1, b1, w2, b2, g: PadGeometry):
+    """Zero-padded copies for the padded widths of ``g``: every head of q, k, v gets
+    hdp - hd zero rows (and W_o the matching zero columns), d_model gets dp - d zero
+    columns (and zero output rows), ffn_dim fp - f zero rows / columns.  The padded
+    q . k products, attention outputs and FFN activations in those places are exactly 0,
+    and the padded residual columns stay 0, so the first d columns are the unpadded
+    block's (LayerNorms run over them alone)."""
+    H, hd, hdp, D, Dp, F, Fp = g.heads, g.hd, g.hdp, g.d, g.dp, g.f, g.fp
+    wq = w_qkv.new_zeros(3, H, hdp, Dp)
+    wq[:, :, :hd, :D] = w_qkv.view(3, H, hd, D)
+    bq = b_qkv.new_zeros(3, H, hdp)
+    bq[:, :, :hd] = b_qkv.view(3, H, hd)
+    wo = w_o.new_zeros(Dp, H, hdp)
+    wo[:D, :, :hd] = w_o.view(D, H, hd)
+    bo = b_o.new_zeros(Dp)
+    bo[:D] = b_o
+    wi = w1.new_zeros(Fp, Dp)
+    wi[:F, :D] = w1
+    bi = b1.new_zeros(Fp)
+    bi[:F] = b1
+    wu = w2.new_zeros(Dp, Fp)
+    wu[:D, :F] = w2
+    bu = b2.new_zeros(Dp)
+    bu[:D] = b2
+    return (wq.view(3 * H * hdp, Dp), bq.view(-1), wo.view(Dp, H * hdp), bo, wi, bi, wu, bu)
+
+
 class _BlockPack:
     """Kernel-ready copies of one block's parameters (plain attributes, so the
-    state_dict is unchanged; TTB:857-914)."""
+    state_dict is unchanged; TTB:857-914), zero-padded when the geometry needs it."""
 
     __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "w1", "b1", "w2", "b2", "ln1_w", "ln1_b", "ln2_w", "ln2_b")
 
-    def __init__(self, blk: CobraTransformerBlock) -> None:
+    def __init__(self, blk: CobraTransformerBlock, geom: PadGeometry) -> None:
         att = blk.attention
         with torch.no_grad():
-            self.w_qkv = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(
-                torch.float16).contiguous()
-            self.b_qkv = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).float().contiguous()
-            self.w_o = att.out_proj.weight.to(torch.float16).contiguous()
-            self.b_o = att.out_proj.bias.float().contiguous()
-            self.w1 = blk.ffn_in.weight.to(torch.float16).contiguous()
-            self.b1 = blk.ffn_in.bias.float().contiguous()
-            self.w2 = blk.ffn_out.weight.to(torch.float16).contiguous()
-            self.b2 = blk.ffn_out.bias.float().contiguous()
+            w = (torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(torch.float16),
+                 torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).float(),
+                 att.out_proj.weight.to(torch.float16), att.out_proj.bias.float(),
+                 blk.ffn_in.weight.to(torch.float16), blk.ffn_in.bias.float(),
+                 blk.ffn_out.weight.to(torch.float16), blk.ffn_out.bias.float())
+            if geom.needed:
+                w = pad_block_weights(*w, geom)
+            (self.w_qkv, self.b_qkv, self.w_o, self.b_o, self.w1, self.b1, self.w2,
+             self.b2) = (t.contiguous() for t in w)
             self.ln1_w = blk.norm1.weight.float().contiguous()
             self.ln1_b = blk.norm1.bias.float().contiguous()
             self.ln2_w = blk.norm2.weight.float().contiguous()
@@ -111,6 +162,7 @@ class CobraTransformer(nn.Module):
         super().__init__()
         config.validate()
         self.config = config
+        self._geom = PadGeometry(config.d_model, config.num_heads, config.ffn_dim)
         # Construction order = BaselineTransformer's (TTB:153-161).
         self.layers = nn.ModuleList(
             [CobraTransformerBlock(config.d_model, config.num_heads, config.ffn_dim)
@@ -146,7 +198,7 @@ class CobraTransformer(nn.Module):
         if self._packs is None or self._versions != versions:
             if not self.final_norm.weight.is_cuda:
                 raise RuntimeError("CobraTransformer runs on the GPU only: move it with .to('cuda')")
-            self._packs = [_BlockPack(blk) for blk in self.layers]
+            self._packs = [_BlockPack(blk, self._geom) for blk in self.layers]
             with torch.no_grad():
                 self._final = (self.final_norm.weight.float().contiguous(), self.final_norm.bias.float().contiguous())
             self._versions = versions
@@ -185,11 +237,10 @@ class CobraTransformer(nn.Module):
             raise ValueError(f"x must be [B, S, {self.config.d_model}], got {tuple(x.shape)}")
         if x.dtype not in (torch.float16, torch.float32):
             raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
-        d, f = self.config.d_model, self.config.ffn_dim
-        hd = d // self.config.num_heads
-        if d % 8 or f % 8 or hd % 8 or hd > 256 or d > 4096:
-            raise ValueError("the HIP kernels need d_model, ffn_dim and head_dim multiples of 8, "
-                             "head_dim <= 256 and d_model <= 4096")
+        g = self._geom
+        if g.hdp > 256 or g.dp > 4096:
+            raise ValueError("the HIP kernels take head_dim <= 256 and d_model <= 4096 (after rounding up to "
+                             "multiples of 8)")
 
     @staticmethod
     def _mask_bytes(mask: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
@@ -213,11 +264,13 @@ class CobraTransformer(nn.Module):
         eps = self.final_norm.eps
         xf = x.view(T, D)
         mrow = None if m is None else m.view(T)
-        bits = None if m is None else ops.mask_bits(m.view(B, S))
         out16 = x.dtype == torch.float16
         n = len(packs)
         if ops.block_plan(B, S, D, H, cfg.ffn_dim) == 1:
             return self._run_blocks(x, m, packs).view(B, S, D)
+        bits = None if m is None else ops.mask_bits(m.view(B, S))
+        if self._geom.needed:
+            return self._run_padded(x, m, mrow, bits, packs).view(B, S, D)
 
         # Layer 0's LN1 rides in its QKV projection where the row fits one k-tile.
         fold_ln1 = ops.ln_linear_ok(D, x.dtype)
@@ -251,6 +304,37 @@ class CobraTransformer(nn.Module):
                 _, h = ops.add_ln(r, None, mrow, nw, nb, cast_fp16=norm16, eps=eps, store_resid=False,
                                   mask_out=last)
         return h.view(B, S, D)
+
+    def _run_padded(self, x: torch.Tensor, m: Optional[torch.Tensor], mrow: Optional[torch.Tensor],
+                    bits: Optional[torch.Tensor], packs: List[_BlockPack]) -> torch.Tensor:
+        """The composed forward at the padded widths (``PadGeometry``): the fp32 residual
+        is [T, dp] with its pad columns 0, every LayerNorm normalises the d true columns
+        of its row and writes a zero-padded fp16 operand, the attention runs at head_dim
+        hdp with the true scale hd^-0.5, and the last norm writes [T, d] in x.dtype."""
+        cfg, g = self.config, self._geom
+        B, S, D = x.shape
+        T = B * S
+        eps = self.final_norm.eps
+        scale = g.hd ** -0.5
+        r = torch.zeros((T, g.dp), device=x.device, dtype=torch.float32)
+        h = ops.ln_strided(x.view(T, D), D, packs[0].ln1_w, packs[0].ln1_b, out_cols=g.dp,
+                           out_dtype=torch.float16, resid_out=r, eps=eps)
+        n = len(packs)
+        for i, p in enumerate(packs):
+            last = i == n - 1
+            nw, nb = self._final if last else (packs[i + 1].ln1_w, packs[i + 1].ln1_b)
+            qkv = ops.linear(h, p.w_qkv, p.b_qkv)
+            ctx = ops.attn(qkv, B, S, cfg.num_heads, g.hdp, scale, causal=cfg.causal, key_bits=bits)
+            r = ops.linear(ctx, p.w_o, p.b_o, out_fp32=True, resid=r, rmask=mrow, mask_branch=True)
+            h2 = ops.ln_strided(r, D, p.ln2_w, p.ln2_b, out_cols=g.dp, out_dtype=torch.float16, eps=eps)
+            hid = ops.linear(h2, p.w1, p.b1, gelu=True)
+            r = ops.linear(hid, p.w2, p.b2, out_fp32=True, resid=r, rmask=mrow)
+            if last:
+                h = ops.ln_strided(r, D, nw, nb, out_cols=D, out_dtype=x.dtype, mask_row=mrow,
+                                   mask_resid=mrow is not None, mask_out=mrow is not None, eps=eps)
+            else:
+                h = ops.ln_strided(r, D, nw, nb, out_cols=g.dp, out_dtype=torch.float16, eps=eps)
+        return h
 
     def _run_blocks(self, x: torch.Tensor, m: Optional[torch.Tensor], packs: List[_BlockPack]) -> torch.Tensor:
         """One launch per block (``cobra_block_fwd``) for the shapes the whole-block kernel
@@ -300,7 +384,7 @@ class CobraTransformer(nn.Module):
     def _per_seq_bytes(self, x: torch.Tensor) -> int:
         """Device bytes one sequence holds at the peak of a block (this build's model):
         fp32 residual, fp16 h / qkv / ctx / h2 / FFN hidden, the input and the output."""
-        S, D, F = x.shape[1], self.config.d_model, self.config.ffn_dim
+        S, D, F = x.shape[1], self._geom.dp, self._geom.fp
         per_tok = 4 * D + 2 * D + 6 * D + 2 * D + 2 * D + 2 * F + 2 * D * x.element_size() + 4 * D
         return S * per_tok
 

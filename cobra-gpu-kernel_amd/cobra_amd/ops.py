@@ -132,6 +132,60 @@ def add_ln(
     return out_r, out_n
 
 
+def ln_strided(
+    x: torch.Tensor,
+    d: int,
+    w: torch.Tensor,
+    b: torch.Tensor,
+    out_cols: Optional[int] = None,
+    out_dtype: Optional[torch.dtype] = None,
+    branch: Optional[torch.Tensor] = None,
+    mask_row: Optional[torch.Tensor] = None,
+    resid_out: Optional[torch.Tensor] = None,
+    mask_resid: bool = False,
+    mask_out: bool = False,
+    eps: float = 1e-5,
+) -> torch.Tensor:
+    """LayerNorm over the first ``d`` columns of each row of ``x`` [M, ldx] (+ ``branch``
+    [M, ldb] in its first d columns) -> ``y`` [M, out_cols] with columns d .. out_cols-1
+    zero (a zero-padded GEMM operand).  The counterpart of ``_tl_add_ln`` (TTB:539-569)
+    for rows padded past their true width; ``resid_out`` [M, ldr] fp32 receives the first
+    d columns of x (+ branch) (after the row mask with ``mask_resid``), its other
+    columns are left as they are.  ``mask_out`` zeroes padded rows' output."""
+    _dev(x, "x")
+    if x.dim() != 2 or x.shape[1] < d or d <= 0:
+        raise ValueError(f"x must be [M, >= {d}]")
+    M = x.shape[0]
+    out_cols = d if out_cols is None else int(out_cols)
+    if out_cols < d:
+        raise ValueError("out_cols must be >= d")
+    w32, b32 = _f32_param(w, d, "w"), _f32_param(b, d, "b")
+    flags = 0
+    mrow = _row_mask(mask_row, M, "mask_row")
+    if mrow is not None:
+        flags |= (_lib.EPI_MASK_RESID if mask_resid else 0) | (_lib.EPI_MASK_OUT if mask_out else 0)
+    elif mask_resid or mask_out:
+        raise ValueError("mask_resid / mask_out need mask_row")
+    if branch is not None:
+        _dev(branch, "branch")
+        if branch.dim() != 2 or branch.shape[0] != M or branch.shape[1] < d:
+            raise ValueError("branch must be [M, >= d]")
+    if resid_out is not None:
+        _dev(resid_out, "resid_out")
+        if resid_out.dtype != torch.float32 or resid_out.dim() != 2 or resid_out.shape[0] != M or \
+                resid_out.shape[1] < d:
+            raise ValueError("resid_out must be fp32 [M, >= d]")
+    y = torch.empty((M, out_cols), device=x.device, dtype=out_dtype or x.dtype)
+    call(
+        "cobra_ln_fwd_strided", x.data_ptr(), _dtype_code(x, "x"), x.shape[1], _ptr(branch),
+        _dtype_code(branch, "branch") if branch is not None else 0, branch.shape[1] if branch is not None else 0,
+        w32.data_ptr(), b32.data_ptr(), _ptr(mrow), flags, _ptr(resid_out),
+        resid_out.shape[1] if resid_out is not None else 0, y.data_ptr(), _dtype_code(y, "y"), out_cols, M, d,
+        float(eps), _stream(x),
+    )
+    return y
+
+
 def linear(
     a: torch.Tensor,
     w: torch.Tensor,

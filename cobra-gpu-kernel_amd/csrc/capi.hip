@@ -238,6 +238,32 @@ int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtyp
   return code(cobra::run_ln(a));
 }
 
+int cobra_ln_fwd_strided(const void* x, int x_dtype, int64_t ldx, const void* branch, int branch_dtype, int64_t ldb,
+                         const float* gamma, const float* beta, const uint8_t* row_mask, int mask_flags,
+                         float* resid_out, int64_t ldr, void* y, int y_dtype, int64_t ldy, int64_t rows, int64_t d,
+                         float eps, void* stream) {
+  if (!x || !y || !gamma || !beta || !is_dtype(x_dtype) || !is_dtype(y_dtype)) return kBad;
+  if ((mask_flags & ~(COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT)) != 0 || (mask_flags && !row_mask)) return kBad;
+  if (branch && !is_dtype(branch_dtype)) return kBad;
+  if (!aligned_to(x, dtype_bytes(x_dtype)) || !aligned_to(y, dtype_bytes(y_dtype)) || !aligned_to(gamma, 4) ||
+      !aligned_to(beta, 4) || (branch && !aligned_to(branch, dtype_bytes(branch_dtype))) ||
+      (resid_out && !aligned_to(resid_out, 4)))
+    return kBad;
+  if (d <= 0 || d > cobra::kLnMaxD || rows < 0) return kBad;
+  const int64_t lx = ldx ? ldx : d, lb = ldb ? ldb : d, lr = ldr ? ldr : d, ly = ldy ? ldy : d;
+  if (lx < d || lb < d || lr < d || ly < d || ly > cobra::kLnMaxD) return kBad;
+  cobra::LnArgs a{x,        x_dtype, branch, branch_dtype == kF32 ? 1 : 0, gamma, beta, resid_out, y, y_dtype,
+                  rows,     (int)d,  eps,    static_cast<hipStream_t>(stream)};
+  a.row_mask = row_mask;
+  a.mask_resid = (mask_flags & COBRA_EPI_MASK_RESID) != 0;
+  a.mask_out = (mask_flags & COBRA_EPI_MASK_OUT) != 0;
+  a.ldx = lx;
+  a.ldb = lb;
+  a.ldr = lr;
+  a.ldy = ly;
+  return code(cobra::run_ln(a));
+}
+
 int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
                      const uint8_t* row_mask, int epi, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                      void* stream) {

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 9
+#define COBRA_ABI_VERSION 10
 
 enum { COBRA_F16 = 0, COBRA_F32 = 1 };
 
@@ -70,6 +70,21 @@ const char* cobra_error_string(int code);
 int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtype, const float* gamma,
                  const float* beta, const uint8_t* row_mask, int mask_flags, float* resid_out, void* y, int y_dtype,
                  int64_t rows, int64_t d, float eps, void* stream);
+
+/*
+ * cobra_ln_fwd over the first d columns of row-strided buffers: row i of x, branch,
+ * resid_out and y starts ldx, ldb, ldr, ldy elements after row i - 1 (each >= d; 0
+ * means d).  With ldy > d, columns d .. ldy-1 of y are written as 0, so y is a
+ * zero-padded operand for a GEMM whose K is a multiple of 8.  The statistics and the
+ * output cover exactly the d true columns: the counterpart of _add_ln_kernel's masked
+ * BLOCK_N columns (TTB:491-535), which normalises rows of any width; this build's
+ * stack uses it for d_model / ffn_dim / head_dim that are not multiples of 8.
+ * Element alignment suffices.
+ */
+int cobra_ln_fwd_strided(const void* x, int x_dtype, int64_t ldx, const void* branch, int branch_dtype, int64_t ldb,
+                         const float* gamma, const float* beta, const uint8_t* row_mask, int mask_flags,
+                         float* resid_out, int64_t ldr, void* y, int y_dtype, int64_t ldy, int64_t rows, int64_t d,
+                         float eps, void* stream);
 
 /*
  * Projection GEMM with fused epilogue:

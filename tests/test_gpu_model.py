@@ -148,6 +148,42 @@ def test_padded_wide_model():
     assert res.passed, res
 
 
+# d_model / ffn_dim / head_dim not multiples of 8 (the reference's stack takes any
+# d_model % heads == 0, TTB:30-57): zero-padded weights, LayerNorms over the true width.
+ODD = [(4, 77, 96, 8, 100, 2, True), (3, 64, 100, 4, 100, 2, True), (2, 50, 36, 3, 50, 3, False),
+       (2, 130, 210, 6, 90, 2, False)]
+
+
+@pytest.mark.parametrize("cfg", ODD, ids=[f"D{c[2]}-H{c[3]}-F{c[4]}-{'c' if c[6] else 'n'}" for c in ODD])
+@pytest.mark.parametrize("masked", [False, True])
+def test_shapes_not_multiples_of_8(cfg, masked):
+    B, S = cfg[0], cfg[1]
+    mask = None
+    if masked:
+        mask = torch.rand(B, S, generator=torch.Generator().manual_seed(B + S)) < 0.75
+        mask[:, 0] = True
+    res = run_case(cfg, mask=mask, seed=3)
+    assert res.passed, res
+
+
+def test_shapes_not_multiples_of_8_fp32_and_graph():
+    """fp32 activations against the unrounded oracle, and the padded forward replayed
+    from a hipGraph equal to its eager run."""
+    cfg = (3, 40, 100, 4, 60, 2, True)
+    res = run_case(cfg, dtype=torch.float32)
+    assert res.passed, res
+    _, mod = build(cfg, graph=True)
+    _, eager = build(cfg, graph=False)
+    x = make_input(3, 40, 100, seed=9).half().to(DEV)
+    with torch.inference_mode():
+        a = mod(x).clone()
+        a2 = mod(x).clone()
+        b = eager(x)
+        torch.cuda.synchronize()
+    assert mod._graph is not None
+    assert torch.equal(a, b) and torch.equal(a2, b)
+
+
 def test_fp32_io_against_unrounded_oracle():
     """The reference's scored setting: fp32 model and input, fp16 operands inside (TTB:960-1004)."""
     res = run_case((16, 128, 128, 4, 128, 4, False), dtype=torch.float32)

@@ -110,6 +110,51 @@ def test_host_companion_loads_and_checks_its_arguments():
         host.BoundForward(256, x, [x], [], None, 1e-5, None)
 
 
+def test_padded_block_weights_reproduce_the_block():
+    """The stack's zero-padded weights (d_model 100 -> 104, head_dim 25 -> 32, ffn 50 -> 56)
+    give, in fp64 on the CPU, each head's q / k / v and scores, the attention output, the
+    out-projection and the FFN of the unpadded block in the true columns and exact zeros
+    in every padded one: a head mapped to the wrong rows, a transposed W_o block or a
+    shifted FFN column fails one of these."""
+    import torch.nn.functional as F
+
+    from cobra_amd.model import PadGeometry, pad_block_weights
+
+    D, H, FF, T = 100, 4, 50, 7
+    g = PadGeometry(D, H, FF)
+    assert (g.dp, g.hdp, g.fp, g.e) == (104, 32, 56, 128) and g.needed
+    assert not PadGeometry(128, 4, 256).needed
+    gen = torch.Generator().manual_seed(0)
+    rnd = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64)  # noqa: E731
+    w_qkv, b_qkv, w_o, b_o = rnd(3 * D, D), rnd(3 * D), rnd(D, D), rnd(D)
+    w1, b1, w2, b2 = rnd(FF, D), rnd(FF), rnd(D, FF), rnd(D)
+    wq, bq, wo, bo, wi, bi, wu, bu = pad_block_weights(w_qkv, b_qkv, w_o, b_o, w1, b1, w2, b2, g)
+    assert wq.shape == (3 * g.e, g.dp) and wo.shape == (g.dp, g.e) and wi.shape == (g.fp, g.dp)
+    h = rnd(T, D)
+    hp = torch.zeros(T, g.dp, dtype=torch.float64)
+    hp[:, :D] = h
+    qkv = (h @ w_qkv.T + b_qkv).view(T, 3, H, g.hd)
+    qkvp = (hp @ wq.T + bq).view(T, 3, H, g.hdp)
+    assert torch.allclose(qkvp[..., : g.hd], qkv, atol=1e-12)
+    assert torch.equal(qkvp[..., g.hd:], torch.zeros_like(qkvp[..., g.hd:]))
+    q, k, v = (qkv[:, i].transpose(0, 1) for i in range(3))      # [H, T, hd]
+    qp, kp, vp = (qkvp[:, i].transpose(0, 1) for i in range(3))  # [H, T, hdp]
+    s_true = (q @ k.transpose(1, 2)) * g.hd ** -0.5
+    s_pad = (qp @ kp.transpose(1, 2)) * g.hd ** -0.5
+    assert torch.allclose(s_pad, s_true, atol=1e-12)
+    ctx = (torch.softmax(s_true, -1) @ v).transpose(0, 1).reshape(T, D)
+    ctxp = (torch.softmax(s_pad, -1) @ vp).transpose(0, 1).reshape(T, g.e)
+    out, outp = ctx @ w_o.T + b_o, ctxp @ wo.T + bo
+    assert torch.allclose(outp[:, :D], out, atol=1e-10)
+    assert torch.equal(outp[:, D:], torch.zeros_like(outp[:, D:]))
+    hid, hidp = F.gelu(h @ w1.T + b1), F.gelu(hp @ wi.T + bi)
+    assert torch.allclose(hidp[:, :FF], hid, atol=1e-12)
+    assert torch.equal(hidp[:, FF:], torch.zeros_like(hidp[:, FF:]))
+    y, yp = hid @ w2.T + b2, hidp @ wu.T + bu
+    assert torch.allclose(yp[:, :D], y, atol=1e-10)
+    assert torch.equal(yp[:, D:], torch.zeros_like(yp[:, D:]))
+
+
 def test_ln1_fold_matches_layernorm_then_projection():
     """The module's packed QKV weights carry LN1's affine: LayerNorm without affine
     followed by the folded projection equals LayerNorm with affine followed by the
