@@ -43,6 +43,7 @@ import torch
 import torch.nn as nn
 
 from . import ops, streaming
+from .padding import PadGeometry, pad_attention_weights
 
 GRAPH_MAX_INPUT_BYTES = 64 * 1024 * 1024
 
@@ -79,7 +80,8 @@ class _Pack:
     as W itself is; the bias term is formed in fp64 and stored in fp32.
     """
 
-    __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "versions")
+    __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "versions", "pad", "geom",
+                 "one", "zero")
 
     def __init__(self, m: "CobraAttentionSublayer", versions) -> None:
         att = m.attention
@@ -95,6 +97,17 @@ class _Pack:
             self.b_o = att.out_proj.bias.float().contiguous()
             self.ln2_w = m.norm2.weight.float().contiguous()
             self.ln2_b = m.norm2.bias.float().contiguous()
+            # d_model or head_dim not a multiple of 8: zero-padded copies made here, once
+            # per parameter version (the C ABI's padded plan, which takes the unpadded
+            # weights, lays them out again on every call).
+            att_ = m.attention
+            self.geom = PadGeometry(att_.d_model, att_.num_heads, att_.d_model)
+            self.pad = None
+            if self.geom.needed:
+                self.pad = tuple(t.contiguous() for t in pad_attention_weights(self.w_qkv, self.b_qkv, self.w_o,
+                                                                               self.b_o, self.geom))
+                self.one = torch.ones(att_.d_model, device=self.w_o.device)
+                self.zero = torch.zeros(att_.d_model, device=self.w_o.device)
         self.versions = versions
 
 
@@ -212,7 +225,7 @@ class CobraAttentionSublayer(nn.Module):
         if self._graph_ok:
             return self._run_graphed(x, m, pack, causal, return_residual)
         out = self._run_eager(x, m, pack, causal, return_residual)
-        if fast_ok and x.is_cuda and x.numel() * x.element_size() < streaming.STREAM_MIN_BYTES:
+        if fast_ok and pack.pad is None and x.is_cuda and x.numel() * x.element_size() < streaming.STREAM_MIN_BYTES:
             self._fast = self._make_fast(x, pack)
         return out
 
@@ -259,8 +272,9 @@ class CobraAttentionSublayer(nn.Module):
         B, S, D = x.shape
         H = self.attention.num_heads
         self.plan = ops.layer_plan(B, S, D, H, masked, x.dtype)
-        self._ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H, masked, x.dtype), dtype=torch.uint8,
-                               device=x.device)
+        # The padded plan runs on the pack's padded weights with tensors of its own.
+        nbytes = 0 if self.plan == ops.PLAN_PADDED else ops.layer_workspace_bytes(B, S, D, H, masked, x.dtype)
+        self._ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
         small = x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
         self._graph_ok = bool(self.graph) and small
         self._graph = None
@@ -269,9 +283,33 @@ class CobraAttentionSublayer(nn.Module):
         self._sig = sig
 
     def _launch(self, x, m, y, r, pack: _Pack, ws: torch.Tensor, causal: bool) -> None:
+        if pack.pad is not None:
+            self._launch_padded(x, m, y, r, pack, causal)
+            return
         ops.layer_fwd(x, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w, pack.ln1_b, pack.ln2_w,
                       pack.ln2_b, y, ws, self.attention.num_heads, causal, self.norm1.eps, resid_out=r,
                       valid_mask=m)
+
+    def _launch_padded(self, x, m, y, r, pack: _Pack, causal: bool) -> None:
+        """The sublayer at the padded widths (d_model or head_dim not a multiple of 8) on
+        the pack's padded weights: LN1 over the true width into a zero-padded operand, the
+        QKV projection, attention at head_dim hdp with the true scale hd^-0.5, the fp32
+        out-projection branch (padded rows' branch zeroed, TTB:121-122), and LN2 of
+        x + branch over the true width into y (and r)."""
+        wq, bq, wo, bo = pack.pad
+        g = pack.geom
+        B, S, D = x.shape
+        T = B * S
+        eps = self.norm1.eps
+        xf = x.view(T, D)
+        mrow = None if m is None else m.view(T)
+        bits = None if m is None else ops.mask_bits(m.view(B, S))
+        h = ops.ln_strided(xf, D, pack.one, pack.zero, out_cols=g.dp, out_dtype=torch.float16, eps=eps)
+        qkv = ops.linear(h, wq, bq)
+        ctx = ops.attn(qkv, B, S, g.heads, g.hdp, g.hd ** -0.5, causal=causal, key_bits=bits)
+        branch = ops.linear(ctx, wo, bo, out_fp32=True, rmask=mrow, mask_branch=True)
+        ops.ln_strided(xf, D, pack.ln2_w, pack.ln2_b, branch=branch, resid_out=None if r is None else r.view(T, D),
+                       eps=self.norm2.eps, out=y.view(T, D))
 
     def _run_eager(self, x, m, pack, causal, return_residual, ws=None):
         y = torch.empty_like(x)

@@ -145,13 +145,15 @@ def ln_strided(
     mask_resid: bool = False,
     mask_out: bool = False,
     eps: float = 1e-5,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """LayerNorm over the first ``d`` columns of each row of ``x`` [M, ldx] (+ ``branch``
     [M, ldb] in its first d columns) -> ``y`` [M, out_cols] with columns d .. out_cols-1
     zero (a zero-padded GEMM operand).  The counterpart of ``_tl_add_ln`` (TTB:539-569)
     for rows padded past their true width; ``resid_out`` [M, ldr] fp32 receives the first
     d columns of x (+ branch) (after the row mask with ``mask_resid``), its other
-    columns are left as they are.  ``mask_out`` zeroes padded rows' output."""
+    columns are left as they are.  ``mask_out`` zeroes padded rows' output.  ``out``:
+    a caller-provided y (contiguous [M, out_cols]) instead of a new tensor."""
     _dev(x, "x")
     if x.dim() != 2 or x.shape[1] < d or d <= 0:
         raise ValueError(f"x must be [M, >= {d}]")
@@ -175,7 +177,12 @@ def ln_strided(
         if resid_out.dtype != torch.float32 or resid_out.dim() != 2 or resid_out.shape[0] != M or \
                 resid_out.shape[1] < d:
             raise ValueError("resid_out must be fp32 [M, >= d]")
-    y = torch.empty((M, out_cols), device=x.device, dtype=out_dtype or x.dtype)
+    if out is None:
+        y = torch.empty((M, out_cols), device=x.device, dtype=out_dtype or x.dtype)
+    else:
+        y = _dev(out, "out")
+        if tuple(y.shape) != (M, out_cols) or (out_dtype is not None and y.dtype != out_dtype):
+            raise ValueError(f"out must be [{M}, {out_cols}]" + (f" {out_dtype}" if out_dtype else ""))
     call(
         "cobra_ln_fwd_strided", x.data_ptr(), _dtype_code(x, "x"), x.shape[1], _ptr(branch),
         _dtype_code(branch, "branch") if branch is not None else 0, branch.shape[1] if branch is not None else 0,

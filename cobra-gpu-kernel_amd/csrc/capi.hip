@@ -2,6 +2,7 @@
 // orchestration of the whole attention sublayer.
 #include "cobra_amd.h"
 
+#include <atomic>
 #include <mutex>
 #include <new>
 
@@ -96,25 +97,29 @@ static __device__ __align__(256) unsigned char scratch[COBRA_NOALLOC_MAX_BYTES];
 namespace {
 
 constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
-hipError_t g_scratch_err[kMaxDevices];
+std::mutex g_scratch_mutex;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
-// Device address of `scratch` on the current device, looked up once per
-// device with that device current (each device holds its own copy).
+// Device address of `scratch` on the current device, looked up with that device
+// current (each device holds its own copy) and kept once the lookup succeeds; a failed
+// lookup is returned and tried again on the next call.
 hipError_t scratch_of_current_device(void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  std::call_once(g_scratch_once[dev], [dev] {
-    void* p = nullptr;
-    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    g_scratch_ptr[dev] = p;
-  });
-  if (g_scratch_err[dev] != hipSuccess) return g_scratch_err[dev];
-  *out = g_scratch_ptr[dev];
-  return *out ? hipSuccess : hipErrorInvalidSymbol;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+      if (!p) return hipErrorInvalidSymbol;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return hipSuccess;
 }
 
 // The padded staged plan (head_dim or d_model not a multiple of 8): the weights are
@@ -176,30 +181,33 @@ int layer_fwd_padded(const void* x, int x_dtype, const uint8_t* valid_mask, cons
 }
 
 // Out-projection and LN2 of the staged sublayer at d_model > 128: ctx [T, D] fp16 in,
-// y out; `spare` is a dead workspace area of at least T * D fp16 that ctx does not
-// overlap.
-int out_proj_ln2(const void* ctx, void* spare, const void* x, int x_dtype, const uint8_t* valid_mask, const void* w_o,
-                 const float* b_o, const float* ln2_w, const float* ln2_b, void* y, float* resid_out, int64_t T,
-                 int64_t D, float eps, hipStream_t s) {
+// y out; `spare` is a dead workspace area of at least T * D fp16 and `spare32` one of at
+// least T * D fp32, neither overlapping ctx.
+int out_proj_ln2(const void* ctx, void* spare, float* spare32, const void* x, int x_dtype,
+                 const uint8_t* valid_mask, const void* w_o, const float* b_o, const float* ln2_w,
+                 const float* ln2_b, void* y, float* resid_out, int64_t T, int64_t D, float eps, hipStream_t s) {
   const bool masked = valid_mask != nullptr;
   hipError_t e = hipSuccess;
-  if (resid_out) {
-    // r itself is an output: the out-projection adds x and stores r in fp32 (the
-    // reference's split, TTB:1274-1283), LN2 reads it back.
-    cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, resid_out, kF32, T, (int)D, (int)D,
+  if (resid_out || x_dtype == kF32) {
+    // The out-projection adds x and stores r in fp32 (the reference's split,
+    // TTB:1274-1283), LN2 reads it back: into the caller's resid_out when r is an
+    // output, and always for fp32 activations, whose branch keeps its fp32 accumulation.
+    float* r = resid_out ? resid_out : spare32;
+    cobra::GemmArgs out{ctx, w_o, b_o, x, x_dtype, r, kF32, T, (int)D, (int)D,
                         nullptr, nullptr, nullptr, kF16, eps, s};
     out.row_mask = valid_mask;
     out.epi = masked ? cobra::kEpiMaskBranch : 0;
     if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
-    cobra::LnArgs ln2{resid_out, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
+    cobra::LnArgs ln2{r, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, x_dtype, T, (int)D, eps, s};
     return code(cobra::run_ln(ln2));
   }
-  // Otherwise the out-projection stores only the branch ctx W_o^T + b_o, in fp16, into
-  // the spare area, and LN2 forms r = x + branch in fp32 (the reference's _add_ln split,
-  // TTB:539): half the bytes of an fp32 r, and no residual read in the GEMM.  The large
-  // values of r sit in x, exact in the sum; the branch's rounding is 2^-11 of its own
-  // magnitude.  (r itself rounded to fp16 would put half an fp16 step of |r| into LN2,
-  // amplified by 1/std for inputs with a large mean.)
+  // fp16 activations, r not requested: the out-projection stores only the branch
+  // ctx W_o^T + b_o, in fp16, into the spare area, and LN2 forms r = x + branch in fp32
+  // (the reference's _add_ln split, TTB:539): half the bytes of an fp32 r, and no
+  // residual read in the GEMM.  The large values of r sit in x, exact in the sum; the
+  // branch's rounding is 2^-11 of its own magnitude, so y differs from the resid_out
+  // form's by at most that rounding's effect.  (r itself rounded to fp16 would put half
+  // an fp16 step of |r| into LN2, amplified by 1/std for inputs with a large mean.)
   cobra::GemmArgs out{ctx, w_o, b_o, nullptr, kF16, spare, kF16, T, (int)D, (int)D,
                       nullptr, nullptr, nullptr, kF16, eps, s};
   out.row_mask = valid_mask;
@@ -426,7 +434,9 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     cobra::QkvAttnArgs f{h, w_qkv, b_qkv, qkv, batch, seq_len, heads, hd, (float)(1.0 / sqrt((double)hd)),
                          causal ? 1 : 0, bits, s};
     if ((e = cobra::run_qkv_attn_head(f)) != hipSuccess) return code(e);
-    return out_proj_ln2(qkv, h, x, x_dtype, valid_mask, w_o, b_o, ln2_w, ln2_b, y, resid_out, T, D, eps, s);
+    // fp32 r (fp32 x): the qkv area past ctx, 4 T D bytes.
+    float* r32 = reinterpret_cast<float*>(static_cast<char*>(qkv) + T * D * 2);
+    return out_proj_ln2(qkv, h, r32, x, x_dtype, valid_mask, w_o, b_o, ln2_w, ln2_b, y, resid_out, T, D, eps, s);
   }
   if (cobra::ln_gemm_ok(D, x_dtype)) {
     // LN1 in the QKV projection's prologue: h never goes to memory.
@@ -454,7 +464,8 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     out.epi = masked ? cobra::kEpiMaskBranch : 0;
     return code(cobra::run_gemm(out));
   }
-  return out_proj_ln2(ctx, qkv, x, x_dtype, valid_mask, w_o, b_o, ln2_w, ln2_b, y, resid_out, T, D, eps, s);
+  return out_proj_ln2(ctx, qkv, static_cast<float*>(qkv), x, x_dtype, valid_mask, w_o, b_o, ln2_w, ln2_b, y,
+                      resid_out, T, D, eps, s);
 }
 
 

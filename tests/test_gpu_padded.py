@@ -89,3 +89,27 @@ def test_add_ln_any_width(d, branch):
     want = torch.nn.functional.layer_norm(rr, (d,), w, b, 1e-5)
     assert torch.allclose(r, rr, atol=1e-6, rtol=0)
     assert torch.allclose(y.float(), want, atol=2e-3, rtol=1e-3), (d, (y.float() - want).abs().max())
+
+
+@pytest.mark.parametrize("B,S,D,H,masked", [(3, 50, 96, 8, True), (2, 130, 260, 4, False)])
+def test_module_padding_once_equals_the_abi_padded_plan(B, S, D, H, masked):
+    """The module pads its weights once per parameter version and runs the chain of op
+    calls; cobra_layer_fwd's padded plan (the C ABI, which takes the unpadded weights)
+    lays them out on every call and runs the same kernels: y and r equal bit for bit."""
+    from cobra_amd import ops
+
+    _, mod = build_pair(D, H, seed=4)
+    x = make_input(B, S, D, seed=5).half().to(DEV)
+    m = _mask(B, S, 6).to(DEV) if masked else None
+    with torch.inference_mode():
+        r1, y1 = mod(x, valid_token_mask=m, return_residual=True)
+        p = mod._packed()
+        assert p.pad is not None
+        mb = None if m is None else m.view(torch.uint8)
+        ws = torch.empty(ops.layer_workspace_bytes(B, S, D, H, masked, x.dtype), dtype=torch.uint8, device=DEV)
+        y2 = torch.empty_like(x)
+        r2 = torch.empty(B, S, D, dtype=torch.float32, device=DEV)
+        ops.layer_fwd(x, p.w_qkv, p.b_qkv, p.w_o, p.b_o, p.ln1_w, p.ln1_b, p.ln2_w, p.ln2_b, y2, ws, H, False,
+                      resid_out=r2, valid_mask=mb)
+        torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(r1, r2)

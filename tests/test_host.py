@@ -118,7 +118,7 @@ def test_padded_block_weights_reproduce_the_block():
     shifted FFN column fails one of these."""
     import torch.nn.functional as F
 
-    from cobra_amd.model import PadGeometry, pad_block_weights
+    from cobra_amd.padding import PadGeometry, pad_block_weights
 
     D, H, FF, T = 100, 4, 50, 7
     g = PadGeometry(D, H, FF)

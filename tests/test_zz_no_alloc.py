@@ -54,6 +54,9 @@ def _run_both(mod, B, S, causal, masked, seed, resid):
         ((8, 1024, 128, 4), (3, 300, 128, 4)),    # ln_gemm + flash attention + GEMM/LN epilogue
         ((4, 128, 1024, 4), (2, 77, 256, 2)),     # d_model > 128: residual through the scratch, LN pass
         ((2, 128, 128, 4), (1, 50, 128, 4)),      # FUSED plan: no scratch used at all
+        # PADDED plan (head_dim 12): the padded weight copies live in the scratch too, and
+        # LN1 must zero the pad columns that the larger first call left behind
+        ((4, 200, 120, 4), (3, 50, 96, 8)),
     ],
 )
 @pytest.mark.parametrize("causal,masked", [(False, False), (True, True)])
