@@ -479,7 +479,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sublayer shards by batch with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(sequences are independent, so the sublayer would shard by batch with no exchange "
+              "between GPUs; one GPU's figure is one shard's)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
