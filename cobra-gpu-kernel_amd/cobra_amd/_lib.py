@@ -15,10 +15,11 @@ from typing import Optional
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcobra_amd.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 F16 = 0
 F32 = 1
+BF16 = 2
 PLAN_FUSED = 0
 PLAN_STAGED = 1
 PLAN_PADDED = 2
@@ -46,7 +47,7 @@ SIGNATURES = {
          _c_i64, _c_f32, _vp],
     ),
     "cobra_linear_fwd": (
-        _c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp],
+        _c_int, [_vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp],
     ),
     "cobra_linear_ln_fwd": (
         _c_int,
@@ -57,7 +58,7 @@ SIGNATURES = {
         _c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_f32, _vp],
     ),
     "cobra_mask_bits": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
-    "cobra_attn_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp]),
+    "cobra_attn_fwd": (_c_int, [_vp, _vp, _c_int, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp]),
     "cobra_qkv_attn_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "cobra_qkv_attn_fwd": (
         _c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f32, _c_int, _vp],

@@ -14,7 +14,8 @@ mirrors the reference's orchestration (TTB:857-1541):
 * weights are packed lazily on the first forward, as plain attributes so
   ``state_dict`` is unchanged (TTB:857-864): one fp16 ``[3D, D]`` q|k|v
   matrix in that order (TTB:876-883), fp16 ``W_o``, fp32 biases and LayerNorm
-  parameters.  The pack is rebuilt whenever a parameter changes (in-place
+  parameters; for bf16 activations the two matrices are bf16 and the sublayer runs
+  the staged kernels with bf16 MFMA operands.  The pack is rebuilt whenever a parameter changes (in-place
   updates bump its version), which the reference did only on shape changes;
 * the library picks the plan: one fused kernel for the whole sublayer
   (S <= 128, d_model <= 128) or a staged pipeline of four kernels.  Either is
@@ -76,24 +77,26 @@ class _Pack:
     nothing else of LN1's output:
         (n * g1 + b1) W^T + b = n (W diag(g1))^T + (b + W b1),   n = (x - mean) * rstd,
     so the kernels normalise without reading g1 / b1 (``ln1_w = ln1_b = None``
-    selects that form of ``cobra_layer_fwd``).  W diag(g1) is rounded to fp16 once,
-    as W itself is; the bias term is formed in fp64 and stored in fp32.
+    selects that form of ``cobra_layer_fwd``).  W diag(g1) is rounded to the operand
+    type (fp16, or bf16 for bf16 activations) once, as W itself is; the bias term is
+    formed in fp64 and stored in fp32.
     """
 
     __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "versions", "pad", "geom",
-                 "one", "zero")
+                 "one", "zero", "op")
 
-    def __init__(self, m: "CobraAttentionSublayer", versions) -> None:
+    def __init__(self, m: "CobraAttentionSublayer", versions, op: torch.dtype = torch.float16) -> None:
         att = m.attention
+        self.op = op
         with torch.no_grad():
             w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).float()
             b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).double()
             g1 = m.norm1.weight.float()
-            self.w_qkv = (w * g1).to(torch.float16).contiguous()
+            self.w_qkv = (w * g1).to(op).contiguous()
             self.b_qkv = (b + w.double() @ m.norm1.bias.double()).float().contiguous()
             self.ln1_w = None
             self.ln1_b = None
-            self.w_o = att.out_proj.weight.to(torch.float16).contiguous()
+            self.w_o = att.out_proj.weight.to(op).contiguous()
             self.b_o = att.out_proj.bias.float().contiguous()
             self.ln2_w = m.norm2.weight.float().contiguous()
             self.ln2_b = m.norm2.bias.float().contiguous()
@@ -177,13 +180,16 @@ class CobraAttentionSublayer(nn.Module):
         # counter; for those only a storage change is detected.
         return tuple([p._version if v else p.data_ptr() for p, v in zip(self._params, self._versioned)])
 
-    def _packed(self) -> _Pack:
+    def _packed(self, x_dtype: torch.dtype = torch.float16) -> _Pack:
+        # MFMA operand type of the packed weights: bf16 for bf16 activations, else fp16.
+        op = torch.bfloat16 if x_dtype == torch.bfloat16 else torch.float16
         versions = self._versions()
-        if self._pack is None or self._pack.versions != versions:
+        if self._pack is None or self._pack.versions != versions or self._pack.op != op:
             if not self.norm1.weight.is_cuda:
                 raise RuntimeError("CobraAttentionSublayer runs on the GPU only: move it with .to('cuda')")
-            self._pack = _Pack(self, versions)
+            self._pack = _Pack(self, versions, op)
             self._graph = None  # the graph baked in the old buffers' addresses
+            self._fast = None
         return self._pack
 
     # -- entry point ----------------------------------------------------------
@@ -207,7 +213,7 @@ class CobraAttentionSublayer(nn.Module):
                 return y
         fast_ok = valid_token_mask is None and causal is None and not return_residual
         causal = self.causal if causal is None else bool(causal)
-        pack = self._packed()
+        pack = self._packed(x.dtype)
         # Free memory moves between calls, so big or host-resident inputs are
         # re-checked every time (TTB:1402-1406); small ones never pay for it.
         if not x.is_cuda or x.numel() * x.element_size() >= streaming.STREAM_MIN_BYTES:
@@ -246,8 +252,8 @@ class CobraAttentionSublayer(nn.Module):
     def _validate(self, x: torch.Tensor) -> None:
         if x.dim() != 3 or x.shape[-1] != self.attention.d_model:
             raise ValueError(f"x must be [B, S, {self.attention.d_model}], got {tuple(x.shape)}")
-        if x.dtype not in (torch.float16, torch.float32):
-            raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
+        if x.dtype not in (torch.float16, torch.float32, torch.bfloat16):
+            raise TypeError(f"x dtype {x.dtype} not supported (float16, bfloat16 or float32)")
 
     @staticmethod
     def _mask_bytes(mask: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
@@ -304,7 +310,7 @@ class CobraAttentionSublayer(nn.Module):
         xf = x.view(T, D)
         mrow = None if m is None else m.view(T)
         bits = None if m is None else ops.mask_bits(m.view(B, S))
-        h = ops.ln_strided(xf, D, pack.one, pack.zero, out_cols=g.dp, out_dtype=torch.float16, eps=eps)
+        h = ops.ln_strided(xf, D, pack.one, pack.zero, out_cols=g.dp, out_dtype=pack.op, eps=eps)
         qkv = ops.linear(h, wq, bq)
         ctx = ops.attn(qkv, B, S, g.heads, g.hdp, g.hd ** -0.5, causal=causal, key_bits=bits)
         branch = ops.linear(ctx, wo, bo, out_fp32=True, rmask=mrow, mask_branch=True)
@@ -363,7 +369,7 @@ class CobraAttentionSublayer(nn.Module):
 
     def _run_streamed(self, x, valid_token_mask, causal, return_residual):
         dev = self.norm1.weight.device
-        pack = self._packed()
+        pack = self._packed(x.dtype)
         B, S, D = x.shape
         host = not x.is_cuda
         masked = valid_token_mask is not None

@@ -24,7 +24,9 @@ and GEMM operands in fp16 (the reference's fused policy, TTB:1170-1290):
     h    = LN1'(r)                      the NEXT block's norm1, or final_norm with
                                         the output row mask on the last block
 
-The op order and roundings are the reference's; the output is x.dtype.
+The op order and roundings are the reference's; the output is x.dtype.  bf16
+activations run the same per-op composition with bf16 weights and bf16 GEMM /
+attention operands (the residual stream stays fp32).
 At d_model 128, ffn_dim 128, seq_len <= 128 (head_dim 8 / 32 / 64 / 128) and
 batches of at most two rounds of workgroups, each block is ONE launch
 (``cobra_block_fwd``: the query-split kernel's whole-block mode) fed by one
@@ -85,18 +87,20 @@ class CobraTransformerBlock(nn.Module):
 
 class _BlockPack:
     """Kernel-ready copies of one block's parameters (plain attributes, so the
-    state_dict is unchanged; TTB:857-914), zero-padded when the geometry needs it."""
+    state_dict is unchanged; TTB:857-914), zero-padded when the geometry needs it.  The
+    weight matrices are in the MFMA operand type ``op``: fp16, or bf16 for bf16
+    activations."""
 
     __slots__ = ("w_qkv", "b_qkv", "w_o", "b_o", "w1", "b1", "w2", "b2", "ln1_w", "ln1_b", "ln2_w", "ln2_b")
 
-    def __init__(self, blk: CobraTransformerBlock, geom: PadGeometry) -> None:
+    def __init__(self, blk: CobraTransformerBlock, geom: PadGeometry, op: torch.dtype = torch.float16) -> None:
         att = blk.attention
         with torch.no_grad():
-            w = (torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(torch.float16),
+            w = (torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).to(op),
                  torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).float(),
-                 att.out_proj.weight.to(torch.float16), att.out_proj.bias.float(),
-                 blk.ffn_in.weight.to(torch.float16), blk.ffn_in.bias.float(),
-                 blk.ffn_out.weight.to(torch.float16), blk.ffn_out.bias.float())
+                 att.out_proj.weight.to(op), att.out_proj.bias.float(),
+                 blk.ffn_in.weight.to(op), blk.ffn_in.bias.float(),
+                 blk.ffn_out.weight.to(op), blk.ffn_out.bias.float())
             if geom.needed:
                 w = pad_block_weights(*w, geom)
             (self.w_qkv, self.b_qkv, self.w_o, self.b_o, self.w1, self.b1, self.w2,
@@ -126,6 +130,7 @@ class CobraTransformer(nn.Module):
         self._params = list(self.parameters())
         self._versioned = [not p.is_inference() for p in self._params]
         self._packs: Optional[List[_BlockPack]] = None
+        self._op = torch.float16  # operand type of the packs
         self._final = None
         self._versions = None
         self._sig = None
@@ -143,12 +148,14 @@ class CobraTransformer(nn.Module):
         self._sig = None
         return out
 
-    def _packed(self) -> List[_BlockPack]:
+    def _packed(self, x_dtype: torch.dtype = torch.float16) -> List[_BlockPack]:
+        op = torch.bfloat16 if x_dtype == torch.bfloat16 else torch.float16
         versions = tuple([p._version if v else p.data_ptr() for p, v in zip(self._params, self._versioned)])
-        if self._packs is None or self._versions != versions:
+        if self._packs is None or self._versions != versions or self._op != op:
             if not self.final_norm.weight.is_cuda:
                 raise RuntimeError("CobraTransformer runs on the GPU only: move it with .to('cuda')")
-            self._packs = [_BlockPack(blk, self._geom) for blk in self.layers]
+            self._packs = [_BlockPack(blk, self._geom, op) for blk in self.layers]
+            self._op = op
             with torch.no_grad():
                 self._final = (self.final_norm.weight.float().contiguous(), self.final_norm.bias.float().contiguous())
             self._versions = versions
@@ -159,7 +166,7 @@ class CobraTransformer(nn.Module):
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         self._validate(x)
-        packs = self._packed()
+        packs = self._packed(x.dtype)
         if not x.is_cuda or x.numel() * x.element_size() >= streaming.STREAM_MIN_BYTES:
             if self._stream_needed(x):
                 return self._run_streamed(x, valid_token_mask)
@@ -170,7 +177,8 @@ class CobraTransformer(nn.Module):
             # block); launch the one-kernel-per-block forward directly, which measured
             # faster than its graph replay at B >= 4 (56 vs 62 us at case 1).
             cfg = self.config
-            blocks = ops.block_plan(x.shape[0], x.shape[1], cfg.d_model, cfg.num_heads, cfg.ffn_dim) == 1
+            blocks = x.dtype != torch.bfloat16 and \
+                ops.block_plan(x.shape[0], x.shape[1], cfg.d_model, cfg.num_heads, cfg.ffn_dim) == 1
             self._graph_ok = (self.graph if self.graph is not None else not blocks) and \
                 x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
             self._graph = None
@@ -185,8 +193,8 @@ class CobraTransformer(nn.Module):
     def _validate(self, x: torch.Tensor) -> None:
         if x.dim() != 3 or x.shape[-1] != self.config.d_model:
             raise ValueError(f"x must be [B, S, {self.config.d_model}], got {tuple(x.shape)}")
-        if x.dtype not in (torch.float16, torch.float32):
-            raise TypeError(f"x dtype {x.dtype} not supported (float16 or float32)")
+        if x.dtype not in (torch.float16, torch.float32, torch.bfloat16):
+            raise TypeError(f"x dtype {x.dtype} not supported (float16, bfloat16 or float32)")
         g = self._geom
         if g.hdp > 256 or g.dp > 4096:
             raise ValueError("the HIP kernels take head_dim <= 256 and d_model <= 4096 (after rounding up to "
@@ -216,10 +224,13 @@ class CobraTransformer(nn.Module):
         mrow = None if m is None else m.view(T)
         out16 = x.dtype == torch.float16
         n = len(packs)
-        if ops.block_plan(B, S, D, H, cfg.ffn_dim) == 1:
+        bf16 = x.dtype == torch.bfloat16
+        if not bf16 and ops.block_plan(B, S, D, H, cfg.ffn_dim) == 1:
             return self._run_blocks(x, m, packs).view(B, S, D)
         bits = None if m is None else ops.mask_bits(m.view(B, S))
-        if self._geom.needed:
+        if self._geom.needed or bf16:
+            # bf16: the same per-op composition with bf16 operands (the LayerNorm-epilogue
+            # GEMMs, LN1-in-prologue projection and fused kernels are fp16-operand)
             return self._run_padded(x, m, mrow, bits, packs).view(B, S, D)
 
         # Layer 0's LN1 rides in its QKV projection where the row fits one k-tile.
@@ -257,18 +268,20 @@ class CobraTransformer(nn.Module):
 
     def _run_padded(self, x: torch.Tensor, m: Optional[torch.Tensor], mrow: Optional[torch.Tensor],
                     bits: Optional[torch.Tensor], packs: List[_BlockPack]) -> torch.Tensor:
-        """The composed forward at the padded widths (``PadGeometry``): the fp32 residual
-        is [T, dp] with its pad columns 0, every LayerNorm normalises the d true columns
-        of its row and writes a zero-padded fp16 operand, the attention runs at head_dim
-        hdp with the true scale hd^-0.5, and the last norm writes [T, d] in x.dtype."""
+        """The composed forward at the padded widths (``PadGeometry``; equal to the true
+        ones when nothing needs padding): the fp32 residual is [T, dp] with its pad columns
+        0, every LayerNorm normalises the d true columns of its row and writes a
+        zero-padded operand (fp16, or bf16 for bf16 activations), the attention runs at
+        head_dim hdp with the true scale hd^-0.5, and the last norm writes [T, d] in x.dtype."""
         cfg, g = self.config, self._geom
+        op = self._op
         B, S, D = x.shape
         T = B * S
         eps = self.final_norm.eps
         scale = g.hd ** -0.5
         r = torch.zeros((T, g.dp), device=x.device, dtype=torch.float32)
         h = ops.ln_strided(x.view(T, D), D, packs[0].ln1_w, packs[0].ln1_b, out_cols=g.dp,
-                           out_dtype=torch.float16, resid_out=r, eps=eps)
+                           out_dtype=op, resid_out=r, eps=eps)
         n = len(packs)
         for i, p in enumerate(packs):
             last = i == n - 1
@@ -276,14 +289,14 @@ class CobraTransformer(nn.Module):
             qkv = ops.linear(h, p.w_qkv, p.b_qkv)
             ctx = ops.attn(qkv, B, S, cfg.num_heads, g.hdp, scale, causal=cfg.causal, key_bits=bits)
             r = ops.linear(ctx, p.w_o, p.b_o, out_fp32=True, resid=r, rmask=mrow, mask_branch=True)
-            h2 = ops.ln_strided(r, D, p.ln2_w, p.ln2_b, out_cols=g.dp, out_dtype=torch.float16, eps=eps)
+            h2 = ops.ln_strided(r, D, p.ln2_w, p.ln2_b, out_cols=g.dp, out_dtype=op, eps=eps)
             hid = ops.linear(h2, p.w1, p.b1, gelu=True)
             r = ops.linear(hid, p.w2, p.b2, out_fp32=True, resid=r, rmask=mrow)
             if last:
                 h = ops.ln_strided(r, D, nw, nb, out_cols=D, out_dtype=x.dtype, mask_row=mrow,
                                    mask_resid=mrow is not None, mask_out=mrow is not None, eps=eps)
             else:
-                h = ops.ln_strided(r, D, nw, nb, out_cols=g.dp, out_dtype=torch.float16, eps=eps)
+                h = ops.ln_strided(r, D, nw, nb, out_cols=g.dp, out_dtype=op, eps=eps)
         return h
 
     def _run_blocks(self, x: torch.Tensor, m: Optional[torch.Tensor], packs: List[_BlockPack]) -> torch.Tensor:
@@ -347,7 +360,7 @@ class CobraTransformer(nn.Module):
 
     def _run_streamed(self, x, valid_token_mask):
         dev = self.final_norm.weight.device
-        packs = self._packed()
+        packs = self._packed(x.dtype)
         B = x.shape[0]
         free, _ = torch.cuda.mem_get_info(dev)
         step = streaming.plan_chunk(B, self._per_seq_bytes(x), free)

@@ -26,16 +26,16 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from ._lib import F16, F32, call
+from ._lib import BF16, F16, F32, call
 
-_DT = {torch.float16: F16, torch.float32: F32}
+_DT = {torch.float16: F16, torch.float32: F32, torch.bfloat16: BF16}
 
 
 def _dtype_code(t: torch.Tensor, what: str) -> int:
     try:
         return _DT[t.dtype]
     except KeyError:
-        raise TypeError(f"{what}: dtype {t.dtype} not supported (float16 or float32)") from None
+        raise TypeError(f"{what}: dtype {t.dtype} not supported (float16, bfloat16 or float32)") from None
 
 
 def _dev(t: torch.Tensor, what: str) -> torch.Tensor:
@@ -205,7 +205,8 @@ def linear(
 ) -> torch.Tensor:
     """``a @ w.T + bias`` (GELU) ``(+ resid)`` with fp32 accumulate.  Mirrors ``_tl_linear`` (TTB:355-381).
 
-    a: [M, K] fp16; w: [N, K] fp16; bias: [N]; resid: [M, N] fp16/fp32.
+    a: [M, K] and w: [N, K] both fp16 or both bf16 (bf16 MFMA operands); bias: [N];
+    resid: [M, N] in a's dtype or fp32.  The output is fp32 with ``out_fp32``, else a's dtype.
     ``gelu`` is the exact erf GELU after the bias (TTB:326-328).  ``rmask``
     multiplies ``(product + resid)`` of padded rows by 0 when there is a
     residual (the reference kernel applies it only then, TTB:343-348); with
@@ -214,8 +215,8 @@ def linear(
     """
     _dev(a, "a")
     _dev(w, "w")
-    if a.dtype != torch.float16 or w.dtype != torch.float16:
-        raise TypeError("a and w must be float16 (fp16 operands, fp32 accumulate)")
+    if a.dtype not in (torch.float16, torch.bfloat16) or w.dtype != a.dtype:
+        raise TypeError("a and w must be both float16 or both bfloat16 (fp32 accumulate)")
     M, K = a.shape
     N, K2 = w.shape
     if K2 != K:
@@ -225,6 +226,8 @@ def linear(
         _dev(resid, "resid")
         if resid.shape != (M, N):
             raise ValueError("resid must be [M, N]")
+        if resid.dtype not in (a.dtype, torch.float32):
+            raise TypeError(f"resid must be {a.dtype} or float32, got {resid.dtype}")
     mrow = _row_mask(rmask, M, "rmask")
     epi = _lib.EPI_GELU if gelu else 0
     if mrow is not None:
@@ -234,9 +237,9 @@ def linear(
             epi |= _lib.EPI_MASK_RESID
         else:
             mrow = None
-    out = torch.empty((M, N), device=a.device, dtype=torch.float32 if out_fp32 else torch.float16)
+    out = torch.empty((M, N), device=a.device, dtype=torch.float32 if out_fp32 else a.dtype)
     call(
-        "cobra_linear_fwd", a.data_ptr(), w.data_ptr(), _ptr(b32), _ptr(resid),
+        "cobra_linear_fwd", a.data_ptr(), w.data_ptr(), _dtype_code(a, "a"), _ptr(b32), _ptr(resid),
         _dtype_code(resid, "resid") if resid is not None else 0, _ptr(mrow), epi, out.data_ptr(),
         _dtype_code(out, "out"), M, N, K, _stream(a),
     )
@@ -342,13 +345,16 @@ def attn(
     heads: int,
     head_dim: int,
     scale: float,
-    out_dtype: torch.dtype = torch.float16,
+    out_dtype: Optional[torch.dtype] = None,
     cfgs=None,
     causal: bool = True,
     key_mask: Optional[torch.Tensor] = None,
     key_bits: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention on packed ``qkv [B*S, 3*H*hd]`` -> ``ctx [B*S, H*hd]``.  Mirrors ``_tl_attn`` (TTB:828-854).
+
+    qkv and ctx are fp16, or both bf16 (bf16 MFMA operands, the probabilities rounded to
+    bf16 for the P.V product); ``out_dtype`` None means qkv's dtype.
 
     ``cfgs`` (the reference's tile ladder) is accepted and ignored: tiles are
     chosen inside the library from (seq_len, head_dim).  ``key_mask`` ([B, S]
@@ -357,8 +363,8 @@ def attn(
     instead, so a caller with several attention calls per mask packs it once.
     """
     _dev(qkv, "qkv")
-    if qkv.dtype != torch.float16 or out_dtype != torch.float16:
-        raise TypeError("attention operands and output are float16")
+    if qkv.dtype not in (torch.float16, torch.bfloat16) or (out_dtype is not None and out_dtype != qkv.dtype):
+        raise TypeError("attention operands and output are float16, or both bfloat16")
     D = heads * head_dim
     if qkv.shape != (batch * seq_len, 3 * D):
         raise ValueError(f"qkv must be [{batch * seq_len}, {3 * D}], got {tuple(qkv.shape)}")
@@ -373,9 +379,10 @@ def attn(
         _dev(bits, "key_bits")
         if bits.dtype != torch.int64 or tuple(bits.shape) != (batch, (seq_len + 63) // 64):
             raise ValueError(f"key_bits must be int64 [{batch}, {(seq_len + 63) // 64}]")
-    out = torch.empty((batch * seq_len, D), device=qkv.device, dtype=torch.float16)
+    out = torch.empty((batch * seq_len, D), device=qkv.device, dtype=qkv.dtype)
     call(
-        "cobra_attn_fwd", qkv.data_ptr(), out.data_ptr(), _ptr(bits), batch, seq_len, heads, head_dim,
+        "cobra_attn_fwd", qkv.data_ptr(), out.data_ptr(), _dtype_code(qkv, "qkv"), _ptr(bits), batch, seq_len, heads,
+        head_dim,
         float(scale), 1 if causal else 0, _stream(qkv),
     )
     return out
@@ -454,7 +461,7 @@ def _dt_of(dtype: torch.dtype) -> int:
     try:
         return _DT[dtype]
     except KeyError:
-        raise TypeError(f"dtype {dtype} not supported (float16 or float32)") from None
+        raise TypeError(f"dtype {dtype} not supported (float16, bfloat16 or float32)") from None
 
 
 def layer_plan(batch: int, seq_len: int, d_model: int, heads: int, masked: bool = False,

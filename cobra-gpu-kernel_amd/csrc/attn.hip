@@ -45,6 +45,9 @@
 //     lgkmcnt, never behind the K/V transfers in vmcnt); a block without a
 //     valid key is skipped by the whole workgroup, a fully valid one costs a
 //     compare, and only partly valid blocks mask per key.
+// q, k, v and ctx are fp16 or bf16 (a template type): the bf16 form uses
+// v_mfma_f32_32x32x16_bf16 and v_dot2_f32_bf16 and rounds the probabilities to
+// bf16, everything else is the same code.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "lds_dma.hpp"
@@ -55,9 +58,10 @@ namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ f16x4 lds_read_tr16(const f16* p) {
+template <typename T>
+__device__ __forceinline__ typename Op16<T>::V4 lds_read_tr16(const T* p) {
   const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
-  return __builtin_bit_cast(f16x4, r);
+  return __builtin_bit_cast(typename Op16<T>::V4, r);
 }
 
 // Chunk swizzle of a [rows][HD] fp16 tile: 16-byte chunk c of row r lives at
@@ -90,10 +94,13 @@ __device__ __forceinline__ f32x16 splat16(float v) {
 
 }  // namespace
 
-template <int HD, int NW, int BN, int ST, bool CAUSAL, bool MASKED>
-__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict__ qkv, f16* __restrict__ ctx,
+template <int HD, int NW, int BN, int ST, bool CAUSAL, bool MASKED, typename TQ>
+__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const TQ* __restrict__ qkv, TQ* __restrict__ ctx,
                                                            int S, int H, int hd, float c2, int nqb,
                                                            const uint64_t* __restrict__ key_bits, int nwords) {
+  using V8 = typename Op16<TQ>::V8;
+  using V4 = typename Op16<TQ>::V4;
+  using V2 = typename Op16<TQ>::V2;
   constexpr int BM = 32 * NW;          // queries per workgroup
   constexpr int KS = HD / 16;          // k-steps of the QK^T product
   constexpr int ND = (HD + 31) / 32;   // 32-row blocks of d in O^T
@@ -128,9 +135,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   const int64_t b = bh / H;
   const int D = H * hd;
   const int64_t ld = 3 * (int64_t)D;
-  const f16* qbase = qkv + b * S * ld + h * hd;
-  const f16* kbase = qbase + D;
-  const f16* vbase = qbase + 2 * D;
+  const TQ* qbase = qkv + b * S * ld + h * hd;
+  const TQ* kbase = qbase + D;
+  const TQ* vbase = qbase + 2 * D;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   // coalesced LDS-DMA: 1 KB span `sp` of a tile holds rows sp*1024/(2HD) ..; each lane
   // fetches the global chunk that belongs in its slot.  Rows past S fetch row S-1 and
   // chunks past hd fetch chunk 0 (finite values; masked, zero-weighted or not stored).
-  auto dma_tile = [&](char* tile, int sp, const f16* base, int row0) {
+  auto dma_tile = [&](char* tile, int sp, const TQ* base, int row0) {
     const int o = sp * 1024 + 16 * lane;
     const int row = o / (2 * HD), pos = (o % (2 * HD)) / 16;
     const int r = min(row0 + row, S - 1);
@@ -161,7 +168,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   // pointers (row and chunk within the tile, K or V) plus the block's wave-uniform
   // offset: no per-block 64-bit address arithmetic on the vector ALU.  The block
   // reaching past S takes the clamped path.
-  const f16* kv_src[LPT];
+  const TQ* kv_src[LPT];
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
     const int span = w + NW * i;
@@ -198,7 +205,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
   float l_run = 0.f;  // this lane's share of the running sum
   bool started = false;  // key masks: the running max is set by the first block with a valid key
   const uint64_t* krow = MASKED ? key_bits + b * nwords : nullptr;
-  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+  const V2 ones = {(TQ)1.0f, (TQ)1.0f};
 
   // Per-lane V^T read geometry (see the header): row within a 16-key step,
   // column within a 32-wide d tile.
@@ -232,13 +239,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     wait_vmcnt<0>();
   }
   stage_barrier();
-  f16x8 qf[KS];
+  V8 qf[KS];
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
     const int row = w * 32 + li, d0 = kk * 16 + g * 8;
-    const f16x8 q = *reinterpret_cast<const f16x8*>(qtile + row * 2 * HD + 16 * ((2 * kk + g) ^ swz<HD>(row)));
+    const V8 q = *reinterpret_cast<const V8*>(qtile + row * 2 * HD + 16 * ((2 * kk + g) ^ swz<HD>(row)));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[kk][e] = d0 < hd ? (f16)((float)q[e] * c2) : (f16)0.0f;
+    for (int e = 0; e < 8; ++e) qf[kk][e] = d0 < hd ? (TQ)((float)q[e] * c2) : (TQ)0.0f;
   }
   if constexpr (!QSEP) {
     lds_barrier();  // every wave has its Q fragments before the stages are refilled
@@ -296,8 +303,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
       if (any == 0) continue;  // no valid key: the block adds nothing (uniform over the workgroup)
       kpart = all != kFull;
     }
-    const f16* Kc = reinterpret_cast<const f16*>(smem + (n % ST) * SB);
-    const f16* Vc = reinterpret_cast<const f16*>(smem + (n % ST) * SB + TB);
+    const TQ* Kc = reinterpret_cast<const TQ*>(smem + (n % ST) * SB);
+    const TQ* Vc = reinterpret_cast<const TQ*>(smem + (n % ST) * SB + TB);
     // s = scores in the exp2 domain minus the running max: the accumulator
     // starts at -m_run (every register of a lane belongs to the lane's query).
     f32x16 s[BN / 32];
@@ -305,11 +312,11 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     for (int t = 0; t < BN / 32; ++t) {
       s[t] = splat16(-m_run);
       const int row = t * 32 + li;
-      const f16* krow = Kc + row * HD;
+      const TQ* krow = Kc + row * HD;
       const int sw = swz<HD>(row);
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(krow + (((2 * kk + g) ^ sw) * 8));
+        const V8 a = *reinterpret_cast<const V8*>(krow + (((2 * kk + g) ^ sw) * 8));
         s[t] = mfma32x32x16(a, qf[kk], s[t]);
       }
     }
@@ -374,34 +381,34 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
       m_run += inc;
     }
 
-    f16x8 pf[BN / 16];
+    V8 pf[BN / 16];
 #pragma unroll
     for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pf[t * 2 + (r >> 3)][r & 7] = (f16)__builtin_amdgcn_exp2f(s[t][r]);
+      for (int r = 0; r < 16; ++r) pf[t * 2 + (r >> 3)][r & 7] = (TQ)__builtin_amdgcn_exp2f(s[t][r]);
     // Row sum of the fp16 probabilities (the values the P.V product uses), fp32 accumulation.
 #pragma unroll
     for (int k = 0; k < BN / 16; ++k)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const f16x2 pr = {pf[k][2 * e], pf[k][2 * e + 1]};
-        l_run = __builtin_amdgcn_fdot2(pr, ones, l_run, false);
+        const V2 pr = {pf[k][2 * e], pf[k][2 * e + 1]};
+        l_run = dot2(pr, ones, l_run);
       }
 
 #pragma unroll
     for (int ks = 0; ks < BN / 16; ++ks)
 #pragma unroll
       for (int j = 0; j < ND; ++j) {
-        f16x4 lo, hi;
+        V4 lo, hi;
         if (HD >= 32 || vc < HD) {
           const int c = j * 32 + vc;
           const int r0 = ks * 16 + vr, r1 = r0 + 8;
           lo = lds_read_tr16(Vc + r0 * HD + (((c >> 3) ^ swz<HD>(r0)) * 8) + (c & 7));
           hi = lds_read_tr16(Vc + r1 * HD + (((c >> 3) ^ swz<HD>(r1)) * 8) + (c & 7));
         } else {
-          lo = hi = f16x4{(f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f};  // d beyond a 16-wide head
+          lo = hi = V4{(TQ)0.0f, (TQ)0.0f, (TQ)0.0f, (TQ)0.0f};  // d beyond a 16-wide head
         }
-        const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[j] = mfma32x32x16(a, pf[ks], o[j]);
       }
 
@@ -419,10 +426,10 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
       const int d = j * 32 + 8 * q4 + 4 * g;
       if (HD >= 32 || d < HD) {
         const int row = w * 32 + li;
-        f16x4 v;
+        V4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (f16)(o[j][q4 * 4 + e] * inv);
-        *reinterpret_cast<f16x4*>(smem + row * 2 * HD + 16 * ((d >> 3) ^ swz<HD>(row)) + 8 * g) = v;
+        for (int e = 0; e < 4; ++e) v[e] = (TQ)(o[j][q4 * 4 + e] * inv);
+        *reinterpret_cast<V4*>(smem + row * 2 * HD + 16 * ((d >> 3) ^ swz<HD>(row)) + 8 * g) = v;
       }
     }
   lds_barrier();
@@ -430,8 +437,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
     const int row = idx / CPR, c = idx % CPR;
     const int q = qb * BM + row, d0 = 8 * c;
     if (q < S && d0 < hd)
-      *reinterpret_cast<f16x8*>(ctx + (b * S + q) * (int64_t)D + h * hd + d0) =
-          *reinterpret_cast<const f16x8*>(smem + row * 2 * HD + 16 * (c ^ swz<HD>(row)));
+      *reinterpret_cast<V8*>(ctx + (b * S + q) * (int64_t)D + h * hd + d0) =
+          *reinterpret_cast<const V8*>(smem + row * 2 * HD + 16 * (c ^ swz<HD>(row)));
   }
 }
 
@@ -444,10 +451,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const f16* __restrict
 // pre-scaled by scale * log2(e), O^T = V^T . P^T with V^T read by
 // ds_read_b64_tr_b16.  Rows past S fetch row S-1 (finite; their keys are masked
 // and their queries never stored).
-template <int HD, bool CAUSAL, bool MASKED>
-__global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__ qkv, f16* __restrict__ ctx, int S,
+template <int HD, bool CAUSAL, bool MASKED, typename TQ>
+__global__ __launch_bounds__(256) void attn_short_kernel(const TQ* __restrict__ qkv, TQ* __restrict__ ctx, int S,
                                                          int H, float c2, const uint64_t* __restrict__ key_bits,
                                                          int nwords) {
+  using V8 = typename Op16<TQ>::V8;
+  using V4 = typename Op16<TQ>::V4;
+  using V2 = typename Op16<TQ>::V2;
   constexpr int NW = 4, BM = 128;
   constexpr int KS = HD / 16, ND = HD / 32, CPR = HD / 8;
   constexpr int TB = BM * HD * 2;   // one [128][HD] tile
@@ -464,15 +474,15 @@ __global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__
   const int64_t b = bh / H;
   const int D = H * HD;
   const int64_t ld = 3 * (int64_t)D;
-  const f16* qbase = qkv + b * S * ld + h * HD;
-  const f16* kbase = qbase + D;
-  const f16* vbase = qbase + 2 * D;
+  const TQ* qbase = qkv + b * S * ld + h * HD;
+  const TQ* kbase = qbase + D;
+  const TQ* vbase = qbase + 2 * D;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5, li = lane & 31;
   const int qi = w * 32 + li;  // this lane's query
 
-  auto dma_tile = [&](char* tile, int sp, const f16* base) {
+  auto dma_tile = [&](char* tile, int sp, const TQ* base) {
     const int o = sp * 1024 + 16 * lane;
     const int row = o / (2 * HD), pos = (o % (2 * HD)) / 16;
     const int r = min(row, S - 1);
@@ -493,12 +503,12 @@ __global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__
   }
   wait_vmcnt<LPT>();  // Q
   stage_barrier();
-  f16x8 qf[KS];
+  V8 qf[KS];
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
-    const f16x8 q = *reinterpret_cast<const f16x8*>(qvtile + qi * 2 * HD + 16 * ((2 * kk + g) ^ swz<HD>(qi)));
+    const V8 q = *reinterpret_cast<const V8*>(qvtile + qi * 2 * HD + 16 * ((2 * kk + g) ^ swz<HD>(qi)));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[kk][e] = (f16)((float)q[e] * c2);
+    for (int e = 0; e < 8; ++e) qf[kk][e] = (TQ)((float)q[e] * c2);
   }
   wait_vmcnt<0>();  // K
   lds_barrier();    // every wave has its Q fragments and sees the whole K tile
@@ -510,7 +520,7 @@ __global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__
 #pragma unroll
   for (int j = 0; j < ND; ++j) o[j] = zero16();
   float l = 0.f;
-  f16x8 pf[8];
+  V8 pf[8];
   if (active) {
     const int nkt = CAUSAL ? min((S + 31) / 32, w + 1) : (S + 31) / 32;  // key tiles with a live key
     f32x16 sacc[4];
@@ -523,7 +533,7 @@ __global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__
         const int sw = swz<HD>(row);
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk)
-          sacc[t] = mfma32x32x16(*reinterpret_cast<const f16x8*>(krow + 16 * ((2 * kk + g) ^ sw)), qf[kk], sacc[t]);
+          sacc[t] = mfma32x32x16(*reinterpret_cast<const V8*>(krow + 16 * ((2 * kk + g) ^ sw)), qf[kk], sacc[t]);
       }
     }
     float mx = kNegInf;
@@ -540,22 +550,22 @@ __global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__
     mx = max_xor32(mx);
     // A query with no valid key (token masks) has max -inf: all-zero probabilities.
     const float m = mx == kNegInf ? 0.f : mx;
-    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+    const V2 ones = {(TQ)1.0f, (TQ)1.0f};
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pf[2 * t + (r >> 3)][r & 7] = (f16)__builtin_amdgcn_exp2f(sacc[t][r] - m);
+      for (int r = 0; r < 16; ++r) pf[2 * t + (r >> 3)][r & 7] = (TQ)__builtin_amdgcn_exp2f(sacc[t][r] - m);
 #pragma unroll
     for (int k = 0; k < 8; ++k)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) l = __builtin_amdgcn_fdot2(f16x2{pf[k][2 * e], pf[k][2 * e + 1]}, ones, l, false);
+      for (int e = 0; e < 4; ++e) l = dot2(V2{pf[k][2 * e], pf[k][2 * e + 1]}, ones, l);
   }
   wait_vmcnt<0>();  // V
   lds_barrier();
   if (active) {
     const int vr = 4 * g + ((lane & 15) >> 2);
     const int vc = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    const f16* Vc = reinterpret_cast<const f16*>(qvtile);
+    const TQ* Vc = reinterpret_cast<const TQ*>(qvtile);
     const int nks = CAUSAL ? 2 * min((S + 31) / 32, w + 1) : 2 * ((S + 31) / 32);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -564,9 +574,9 @@ __global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__
         for (int j = 0; j < ND; ++j) {
           const int c = j * 32 + vc;
           const int r0 = ks * 16 + vr, r1 = r0 + 8;
-          const f16x4 lo = lds_read_tr16(Vc + r0 * HD + (((c >> 3) ^ swz<HD>(r0)) * 8) + (c & 7));
-          const f16x4 hi = lds_read_tr16(Vc + r1 * HD + (((c >> 3) ^ swz<HD>(r1)) * 8) + (c & 7));
-          const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const V4 lo = lds_read_tr16(Vc + r0 * HD + (((c >> 3) ^ swz<HD>(r0)) * 8) + (c & 7));
+          const V4 hi = lds_read_tr16(Vc + r1 * HD + (((c >> 3) ^ swz<HD>(r1)) * 8) + (c & 7));
+          const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[j] = mfma32x32x16(a, pf[ks], o[j]);
         }
       }
@@ -583,38 +593,38 @@ __global__ __launch_bounds__(256) void attn_short_kernel(const f16* __restrict__
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int d = j * 32 + 8 * q4 + 4 * g;
-        f16x4 v;
+        V4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (f16)(o[j][q4 * 4 + e] * inv);
-        *reinterpret_cast<f16x4*>(ktile + qi * 2 * HD + 16 * ((d >> 3) ^ swz<HD>(qi)) + 8 * g) = v;
+        for (int e = 0; e < 4; ++e) v[e] = (TQ)(o[j][q4 * 4 + e] * inv);
+        *reinterpret_cast<V4*>(ktile + qi * 2 * HD + 16 * ((d >> 3) ^ swz<HD>(qi)) + 8 * g) = v;
       }
   }
   lds_barrier();
   for (int idx = threadIdx.x; idx < BM * CPR; idx += NW * 64) {
     const int row = idx / CPR, c = idx % CPR;
     if (row < S)
-      *reinterpret_cast<f16x8*>(ctx + (b * S + row) * (int64_t)D + h * HD + 8 * c) =
-          *reinterpret_cast<const f16x8*>(ktile + row * 2 * HD + 16 * (c ^ swz<HD>(row)));
+      *reinterpret_cast<V8*>(ctx + (b * S + row) * (int64_t)D + h * HD + 8 * c) =
+          *reinterpret_cast<const V8*>(ktile + row * 2 * HD + 16 * (c ^ swz<HD>(row)));
   }
 }
 
-template <int HD, bool CAUSAL>
+template <int HD, bool CAUSAL, typename TQ>
 static hipError_t launch_attn_short(const AttnArgs& a, float c2) {
   const int64_t grid = (int64_t)a.heads * a.batch;
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
   const int nwords = (int)mask_words(a.seq_len);
   if (a.key_bits)
-    hipLaunchKernelGGL((attn_short_kernel<HD, CAUSAL, true>), dim3((unsigned)grid), dim3(256), 0, a.stream,
-                       static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads, c2, a.key_bits,
+    hipLaunchKernelGGL((attn_short_kernel<HD, CAUSAL, true, TQ>), dim3((unsigned)grid), dim3(256), 0, a.stream,
+                       static_cast<const TQ*>(a.qkv), static_cast<TQ*>(a.ctx), a.seq_len, a.heads, c2, a.key_bits,
                        nwords);
   else
-    hipLaunchKernelGGL((attn_short_kernel<HD, CAUSAL, false>), dim3((unsigned)grid), dim3(256), 0, a.stream,
-                       static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads, c2, nullptr,
+    hipLaunchKernelGGL((attn_short_kernel<HD, CAUSAL, false, TQ>), dim3((unsigned)grid), dim3(256), 0, a.stream,
+                       static_cast<const TQ*>(a.qkv), static_cast<TQ*>(a.ctx), a.seq_len, a.heads, c2, nullptr,
                        nwords);
   return hipGetLastError();
 }
 
-template <int HD, int NW, int BN, int ST, bool CAUSAL>
+template <int HD, int NW, int BN, int ST, bool CAUSAL, typename TQ>
 static hipError_t launch_attn(const AttnArgs& a, float c2) {
   constexpr int BM = 32 * NW;
   const int nqb = (a.seq_len + BM - 1) / BM;
@@ -622,17 +632,17 @@ static hipError_t launch_attn(const AttnArgs& a, float c2) {
   if (grid > 0x7fffffff) return hipErrorInvalidValue;
   const int nwords = (int)mask_words(a.seq_len);
   if (a.key_bits)
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL, true>), dim3((unsigned)grid), dim3(NW * 64), 0,
-                       a.stream, static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads,
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL, true, TQ>), dim3((unsigned)grid), dim3(NW * 64), 0,
+                       a.stream, static_cast<const TQ*>(a.qkv), static_cast<TQ*>(a.ctx), a.seq_len, a.heads,
                        a.head_dim, c2, nqb, a.key_bits, nwords);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL, false>), dim3((unsigned)grid), dim3(NW * 64), 0,
-                       a.stream, static_cast<const f16*>(a.qkv), static_cast<f16*>(a.ctx), a.seq_len, a.heads,
+    hipLaunchKernelGGL((attn_fwd_kernel<HD, NW, BN, ST, CAUSAL, false, TQ>), dim3((unsigned)grid), dim3(NW * 64), 0,
+                       a.stream, static_cast<const TQ*>(a.qkv), static_cast<TQ*>(a.ctx), a.seq_len, a.heads,
                        a.head_dim, c2, nqb, nullptr, nwords);
   return hipGetLastError();
 }
 
-template <int HD, bool CAUSAL>
+template <int HD, bool CAUSAL, typename TQ>
 static hipError_t dispatch_waves(const AttnArgs& a, float c2) {
   // Waves per workgroup follow the sequence length: every K/V tile a
   // workgroup stages is shared by all of its waves, so long sequences take 8
@@ -645,26 +655,26 @@ static hipError_t dispatch_waves(const AttnArgs& a, float c2) {
   constexpr int BN8 = HD <= 32 ? 128 : BN;
   constexpr int ST = HD >= 128 ? 3 : 4;
   if constexpr (HD <= 64) {
-    if (a.seq_len <= 32) return launch_attn<HD, 1, BN, ST, CAUSAL>(a, c2);
-    if (a.seq_len <= 64) return launch_attn<HD, 2, BN, ST, CAUSAL>(a, c2);
+    if (a.seq_len <= 32) return launch_attn<HD, 1, BN, ST, CAUSAL, TQ>(a, c2);
+    if (a.seq_len <= 64) return launch_attn<HD, 2, BN, ST, CAUSAL, TQ>(a, c2);
   }
   if constexpr (HD <= 128) {
-    if (a.seq_len > 128) return launch_attn<HD, 8, BN8, ST, CAUSAL>(a, c2);
+    if (a.seq_len > 128) return launch_attn<HD, 8, BN8, ST, CAUSAL, TQ>(a, c2);
   }
-  return launch_attn<HD, 4, BN, ST, CAUSAL>(a, c2);
+  return launch_attn<HD, 4, BN, ST, CAUSAL, TQ>(a, c2);
 }
 
-template <bool CAUSAL>
+template <bool CAUSAL, typename TQ>
 static hipError_t dispatch_hd(const AttnArgs& a, float c2) {
   const int hd = a.head_dim;
   // Wide heads over at most 128 keys: exact softmax, one workgroup per (sequence, head).
-  if (a.seq_len <= 128 && hd == 256) return launch_attn_short<256, CAUSAL>(a, c2);
-  if (a.seq_len <= 128 && hd == 128) return launch_attn_short<128, CAUSAL>(a, c2);
-  if (hd <= 16) return dispatch_waves<16, CAUSAL>(a, c2);
-  if (hd <= 32) return dispatch_waves<32, CAUSAL>(a, c2);
-  if (hd <= 64) return dispatch_waves<64, CAUSAL>(a, c2);
-  if (hd <= 128) return dispatch_waves<128, CAUSAL>(a, c2);
-  return dispatch_waves<256, CAUSAL>(a, c2);
+  if (a.seq_len <= 128 && hd == 256) return launch_attn_short<256, CAUSAL, TQ>(a, c2);
+  if (a.seq_len <= 128 && hd == 128) return launch_attn_short<128, CAUSAL, TQ>(a, c2);
+  if (hd <= 16) return dispatch_waves<16, CAUSAL, TQ>(a, c2);
+  if (hd <= 32) return dispatch_waves<32, CAUSAL, TQ>(a, c2);
+  if (hd <= 64) return dispatch_waves<64, CAUSAL, TQ>(a, c2);
+  if (hd <= 128) return dispatch_waves<128, CAUSAL, TQ>(a, c2);
+  return dispatch_waves<256, CAUSAL, TQ>(a, c2);
 }
 
 // One wave per 64-bit word: lane j reads the byte of key 64w + j (coalesced)
@@ -697,7 +707,9 @@ hipError_t run_attn(const AttnArgs& a) {
   if (a.head_dim <= 0 || a.head_dim % 8 != 0 || a.head_dim > 256) return hipErrorInvalidValue;
   if (a.batch == 0 || a.seq_len == 0) return hipSuccess;
   const float c2 = a.scale * 1.4426950408889634f;  // scale * log2(e): softmax in the exp2 domain
-  return a.causal ? dispatch_hd<true>(a, c2) : dispatch_hd<false>(a, c2);
+  if (a.dtype == kBF16) return a.causal ? dispatch_hd<true, bf16>(a, c2) : dispatch_hd<false, bf16>(a, c2);
+  if (a.dtype != kF16) return hipErrorInvalidValue;
+  return a.causal ? dispatch_hd<true, f16>(a, c2) : dispatch_hd<false, f16>(a, c2);
 }
 
 }  // namespace cobra

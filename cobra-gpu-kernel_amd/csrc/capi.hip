@@ -11,6 +11,7 @@
 
 namespace {
 
+using cobra::kBF16;
 using cobra::kF16;
 using cobra::kF32;
 
@@ -20,6 +21,8 @@ int dtype_bytes(int dt) { return dt == kF32 ? 4 : 2; }
 int64_t round8(int64_t n) { return (n + 7) & ~int64_t(7); }
 bool opt_aligned16(const void* p) { return p == nullptr || aligned16(p); }
 bool is_dtype(int dt) { return dt == kF16 || dt == kF32; }
+bool is_act_dtype(int dt) { return is_dtype(dt) || dt == kBF16; }  // activations that may be bf16
+bool is_op_dtype(int dt) { return dt == kF16 || dt == kBF16; }     // 16-bit MFMA operands
 int64_t round256(int64_t n) { return (n + 255) & ~int64_t(255); }
 int code(hipError_t e) { return static_cast<int>(e); }
 constexpr int kBad = static_cast<int>(hipErrorInvalidValue);
@@ -139,6 +142,7 @@ int layer_fwd_padded(const void* x, int x_dtype, const uint8_t* valid_mask, cons
   const int64_t T = batch * seq_len;
   if (T == 0) return 0;
   const int64_t hd = D / H, hdp = pb.hdp, Dp = pb.dp, E = pb.e;
+  const int op = x_dtype == kBF16 ? kBF16 : kF16;  // MFMA operand type (weights, h, q / k / v, ctx)
   char* ws = static_cast<char*>(workspace);
   void* wq = ws + pb.wq_off;
   float* bq = reinterpret_cast<float*>(ws + pb.bq_off);
@@ -159,24 +163,71 @@ int layer_fwd_padded(const void* x, int x_dtype, const uint8_t* valid_mask, cons
   for (const cobra::PadArgs* pa : {&p1, &p2, &p3, &p4})
     if ((e = cobra::run_pad(*pa)) != hipSuccess) return code(e);
   if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
-  cobra::LnArgs ln1{x, x_dtype, nullptr, 0, ln1_w, ln1_b, nullptr, h, kF16, T, (int)D, eps, s};
+  cobra::LnArgs ln1{x, x_dtype, nullptr, 0, ln1_w, ln1_b, nullptr, h, op, T, (int)D, eps, s};
   ln1.ldy = Dp;
   if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
-  cobra::GemmArgs proj{h, wq, bq, nullptr, kF16, qkv, kF16, T, (int)(3 * E), (int)Dp,
+  cobra::GemmArgs proj{h, wq, bq, nullptr, op, qkv, op, T, (int)(3 * E), (int)Dp,
                        nullptr, nullptr, nullptr, kF16, eps, s};
+  proj.ab_dtype = op;
   if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
   cobra::AttnArgs at{qkv, ctx, batch, (int)seq_len, (int)H, (int)hdp, (float)(1.0 / sqrt((double)hd)),
                      causal ? 1 : 0, s};
   at.key_bits = bits;
+  at.dtype = op;
   if ((e = cobra::run_attn(at)) != hipSuccess) return code(e);
   // Padded query rows: the attention output is zeroed before the residual add (TTB:121-122).
-  cobra::GemmArgs out{ctx, wo, bo, nullptr, kF16, r, kF32, T, (int)Dp, (int)E,
+  cobra::GemmArgs out{ctx, wo, bo, nullptr, op, r, kF32, T, (int)Dp, (int)E,
                       nullptr, nullptr, nullptr, kF16, eps, s};
+  out.ab_dtype = op;
   out.row_mask = valid_mask;
   out.epi = masked ? cobra::kEpiMaskBranch : 0;
   if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
   cobra::LnArgs ln2{x, x_dtype, r, 1, ln2_w, ln2_b, resid_out, y, x_dtype, T, (int)D, eps, s};
   ln2.ldb = Dp;
+  return code(cobra::run_ln(ln2));
+}
+
+// The staged sublayer with bf16 activations and weights (x_dtype kBF16): LN1 into the h
+// area (bf16), the QKV GEMM into the qkv area (bf16 q | k | v), the attention into the h
+// area, the out-projection with the residual x added in its epilogue storing r in fp32
+// (into resid_out, or the qkv area, dead by then: 4 T D of its 6 T D bytes), and LN2 from
+// r to y (bf16).  Every product is a bf16 MFMA with fp32 accumulation.
+int layer_fwd_bf16(const void* x, const uint8_t* valid_mask, const void* w_qkv, const float* b_qkv, const void* w_o,
+                   const float* b_o, const float* ln1_w, const float* ln1_b, const float* ln2_w, const float* ln2_b,
+                   void* y, float* resid_out, void* workspace, int64_t workspace_bytes, int64_t batch, int64_t seq_len,
+                   int64_t D, int64_t H, int causal, float eps, hipStream_t s) {
+  const bool masked = valid_mask != nullptr;
+  const LayerBuffers lb = layer_buffers(batch, seq_len, D, masked);
+  if (!workspace || workspace_bytes < lb.total) return kBad;
+  const int64_t T = batch * seq_len;
+  if (T == 0) return 0;
+  char* ws = static_cast<char*>(workspace);
+  void* h = ws + lb.h_off;
+  void* qkv = ws + lb.qkv_off;
+  void* ctx = h;  // h is dead once the QKV projection has read it
+  uint64_t* bits = masked ? reinterpret_cast<uint64_t*>(ws + lb.bits_off) : nullptr;
+  hipError_t e = hipSuccess;
+  if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
+  cobra::LnArgs ln1{x, kBF16, nullptr, 0, ln1_w, ln1_b, nullptr, h, kBF16, T, (int)D, eps, s};
+  if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
+  cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kBF16, qkv, kBF16, T, (int)(3 * D), (int)D,
+                       nullptr, nullptr, nullptr, kF16, eps, s};
+  proj.ab_dtype = kBF16;
+  if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
+  const int64_t hd = D / H;
+  cobra::AttnArgs at{qkv, ctx, batch, (int)seq_len, (int)H, (int)hd, (float)(1.0 / sqrt((double)hd)),
+                     causal ? 1 : 0, s};
+  at.key_bits = bits;
+  at.dtype = kBF16;
+  if ((e = cobra::run_attn(at)) != hipSuccess) return code(e);
+  // Padded query rows: the attention output is zeroed before the residual add (TTB:121-122).
+  float* r = resid_out ? resid_out : static_cast<float*>(qkv);
+  cobra::GemmArgs out{ctx, w_o, b_o, x, kBF16, r, kF32, T, (int)D, (int)D, nullptr, nullptr, nullptr, kF16, eps, s};
+  out.ab_dtype = kBF16;
+  out.row_mask = valid_mask;
+  out.epi = masked ? cobra::kEpiMaskBranch : 0;
+  if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
+  cobra::LnArgs ln2{r, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, kBF16, T, (int)D, eps, s};
   return code(cobra::run_ln(ln2));
 }
 
@@ -228,7 +279,7 @@ const char* cobra_error_string(int c) { return hipGetErrorString(static_cast<hip
 int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtype, const float* gamma,
                  const float* beta, const uint8_t* row_mask, int mask_flags, float* resid_out, void* y, int y_dtype,
                  int64_t rows, int64_t d, float eps, void* stream) {
-  if (!x || !y || !gamma || !beta || !is_dtype(x_dtype) || !is_dtype(y_dtype)) return kBad;
+  if (!x || !y || !gamma || !beta || !is_act_dtype(x_dtype) || !is_act_dtype(y_dtype)) return kBad;
   if ((mask_flags & ~(COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT)) != 0 || (mask_flags && !row_mask)) return kBad;
   if (branch && !is_dtype(branch_dtype)) return kBad;
   // Element alignment suffices; widths that are multiples of 8 on 16-byte aligned buffers
@@ -250,7 +301,7 @@ int cobra_ln_fwd_strided(const void* x, int x_dtype, int64_t ldx, const void* br
                          const float* gamma, const float* beta, const uint8_t* row_mask, int mask_flags,
                          float* resid_out, int64_t ldr, void* y, int y_dtype, int64_t ldy, int64_t rows, int64_t d,
                          float eps, void* stream) {
-  if (!x || !y || !gamma || !beta || !is_dtype(x_dtype) || !is_dtype(y_dtype)) return kBad;
+  if (!x || !y || !gamma || !beta || !is_act_dtype(x_dtype) || !is_act_dtype(y_dtype)) return kBad;
   if ((mask_flags & ~(COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT)) != 0 || (mask_flags && !row_mask)) return kBad;
   if (branch && !is_dtype(branch_dtype)) return kBad;
   if (!aligned_to(x, dtype_bytes(x_dtype)) || !aligned_to(y, dtype_bytes(y_dtype)) || !aligned_to(gamma, 4) ||
@@ -272,10 +323,12 @@ int cobra_ln_fwd_strided(const void* x, int x_dtype, int64_t ldx, const void* br
   return code(cobra::run_ln(a));
 }
 
-int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
+int cobra_linear_fwd(const void* a, const void* w, int ab_dtype, const float* bias, const void* resid, int resid_dtype,
                      const uint8_t* row_mask, int epi, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                      void* stream) {
-  if (!a || !w || !c || !is_dtype(c_dtype) || (resid && !is_dtype(resid_dtype))) return kBad;
+  // resid and c: fp16 or fp32 with fp16 operands, bf16 or fp32 with bf16 operands
+  auto out_ok = [&](int dt) { return dt == kF32 || dt == ab_dtype; };
+  if (!a || !w || !c || !is_op_dtype(ab_dtype) || !out_ok(c_dtype) || (resid && !out_ok(resid_dtype))) return kBad;
   if ((epi & ~kEpiAll) != 0 || (epi & COBRA_EPI_MASK_OUT) || ((epi & ~COBRA_EPI_GELU) && !row_mask)) return kBad;
   if (!aligned16(a) || !aligned16(w) || !aligned16(c) || !opt_aligned16(resid) || !opt_aligned16(bias)) return kBad;
   if (M < 0 || N <= 0 || K <= 0 || N > 0x7fffffff || K > 0x7fffffff) return kBad;
@@ -284,6 +337,7 @@ int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void
                     1e-5f,   static_cast<hipStream_t>(stream)};
   g.row_mask = row_mask;
   g.epi = epi;
+  g.ab_dtype = ab_dtype;
   return code(cobra::run_gemm(g));
 }
 
@@ -321,9 +375,9 @@ int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int6
   return code(cobra::run_mask_bits(mask, key_bits, batch, (int)seq_len, static_cast<hipStream_t>(stream)));
 }
 
-int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t batch, int64_t seq_len,
+int cobra_attn_fwd(const void* qkv, void* ctx, int dtype, const uint64_t* key_bits, int64_t batch, int64_t seq_len,
                    int64_t heads, int64_t head_dim, float scale, int causal, void* stream) {
-  if (!qkv || !ctx || !aligned16(qkv) || !aligned16(ctx)) return kBad;
+  if (!qkv || !ctx || !aligned16(qkv) || !aligned16(ctx) || !is_op_dtype(dtype)) return kBad;
   if (key_bits && (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
   if (batch < 0 || seq_len < 0 || seq_len > 0x7fffffff || heads <= 0 || heads > 0x7fffffff || head_dim <= 0 ||
       head_dim > 256 || !(scale > 0.f))
@@ -331,6 +385,7 @@ int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t
   cobra::AttnArgs a{qkv, ctx, batch, (int)seq_len, (int)heads, (int)head_dim, scale, causal ? 1 : 0,
                     static_cast<hipStream_t>(stream)};
   a.key_bits = key_bits;
+  a.dtype = dtype;
   return code(cobra::run_attn(a));
 }
 
@@ -374,9 +429,10 @@ int cobra_qkv_attn_fwd(const void* h, const void* w_qkv, const float* b_qkv, voi
 }
 
 int cobra_layer_plan(int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads, int masked, int x_dtype) {
-  if (!layer_shape_ok(batch, seq_len, d_model, heads) || !is_dtype(x_dtype)) return -1;
+  if (!layer_shape_ok(batch, seq_len, d_model, heads) || !is_act_dtype(x_dtype)) return -1;
   (void)masked;  // every plan takes a token mask
   if (layer_needs_pad(d_model, heads)) return COBRA_PLAN_PADDED;
+  if (x_dtype == kBF16) return COBRA_PLAN_STAGED;  // the fused kernels are fp16-operand
   return cobra::layer_fused_ok(batch, seq_len, d_model, heads, x_dtype) ? COBRA_PLAN_FUSED : COBRA_PLAN_STAGED;
 }
 
@@ -413,6 +469,9 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
   if (plan == COBRA_PLAN_PADDED)
     return layer_fwd_padded(x, x_dtype, valid_mask, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, resid_out,
                             workspace, workspace_bytes, batch, seq_len, d_model, heads, causal, eps, s);
+  if (x_dtype == kBF16)
+    return layer_fwd_bf16(x, valid_mask, w_qkv, b_qkv, w_o, b_o, ln1_w, ln1_b, ln2_w, ln2_b, y, resid_out, workspace,
+                          workspace_bytes, batch, seq_len, d_model, heads, causal, eps, s);
   const LayerBuffers lb = layer_buffers(batch, seq_len, D, masked);
   if (!workspace || workspace_bytes < lb.total) return kBad;
   if (T == 0) return 0;

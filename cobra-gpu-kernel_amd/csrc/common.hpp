@@ -23,14 +23,45 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+// bfloat16 (8-bit mantissa, fp32's exponent range): conversions from fp32 round to
+// nearest even (v_cvt_pk_bf16_f32), to fp32 are exact.
+typedef __bf16 bf16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // dtype codes of the C ABI (include/cobra_amd.h)
-enum : int { kF16 = 0, kF32 = 1 };
+enum : int { kF16 = 0, kF32 = 1, kBF16 = 2 };
+
+// 16-bit MFMA operand types: T is f16 or bf16; V8 / V4 / V2 its 8 / 4 / 2-element vectors.
+template <typename T>
+struct Op16;
+template <>
+struct Op16<f16> {
+  typedef f16x8 V8;
+  typedef f16x4 V4;
+  typedef f16x2 V2;
+};
+template <>
+struct Op16<bf16> {
+  typedef bf16x8 V8;
+  typedef bf16x4 V4;
+  typedef bf16x2 V2;
+};
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
 __device__ __forceinline__ f32x16 mfma32x32x16(const f16x8& a, const f16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// acc + a.x * b.x + a.y * b.y with fp32 accumulation (v_dot2_f32_f16 / v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float acc) { return __builtin_amdgcn_fdot2(a, b, acc, false); }
+__device__ __forceinline__ float dot2(bf16x2 a, bf16x2 b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
 }
 
 // a - b on both fp16 halves as one v_pk_add_f16 (with the second operand
@@ -58,6 +89,14 @@ __device__ __forceinline__ f16x8 zero8() {
   f16x8 z;
 #pragma unroll
   for (int i = 0; i < 8; ++i) z[i] = (f16)0.0f;
+  return z;
+}
+// Eight zeros of a 16-bit operand type.
+template <typename T>
+__device__ __forceinline__ typename Op16<T>::V8 zero8_of() {
+  typename Op16<T>::V8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (T)0.0f;
   return z;
 }
 
@@ -133,11 +172,22 @@ __device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
     v[i + 4] = b[i];
   }
 }
+__device__ __forceinline__ void load8(const bf16* p, float (&v)[8]) {
+  const bf16x8 h = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)h[i];
+}
 __device__ __forceinline__ void store8(f16* p, const float (&v)[8]) {
   f16x8 h;
 #pragma unroll
   for (int i = 0; i < 8; ++i) h[i] = (f16)v[i];
   *reinterpret_cast<f16x8*>(p) = h;
+}
+__device__ __forceinline__ void store8(bf16* p, const float (&v)[8]) {
+  bf16x8 h;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = (bf16)v[i];
+  *reinterpret_cast<bf16x8*>(p) = h;
 }
 __device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
   f32x4 a, b;

@@ -1,5 +1,5 @@
-// C[M,N] = A[M,K] . W[N,K]^T (+ bias[N]) (+ resid[M,N]), fp16 operands, fp32
-// accumulate, with an optional LayerNorm epilogue over whole rows.
+// C[M,N] = A[M,K] . W[N,K]^T (+ bias[N]) (+ resid[M,N]), fp16 or bf16 operands, fp32
+// accumulate, with an optional LayerNorm epilogue over whole rows (fp16 operands).
 //
 // Replaces the reference's _gemm_kernel/_tl_linear (torch_transformer_benchmark.py:283-381)
 // for the projections and _gemm_ln_kernel/_tl_linear_ln (TTB:394-488) for
@@ -55,8 +55,8 @@ __device__ __forceinline__ float epi_pre_resid(float v, int epi, const uint8_t* 
   return v;
 }
 
-template <int BM, int BN, int WM, int WN, typename TR, typename TC, bool LN_EPI, typename TY>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict__ A, const f16* __restrict__ W,
+template <int BM, int BN, int WM, int WN, typename TR, typename TC, bool LN_EPI, typename TY, typename TA>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const TA* __restrict__ A, const TA* __restrict__ W,
                                                           const float* __restrict__ bias, const TR* __restrict__ resid,
                                                           TC* __restrict__ C, int64_t M, int N, int K,
                                                           const float* __restrict__ gamma,
@@ -69,8 +69,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict
   constexpr int EPI_LDS = LN_EPI ? BM * LDC * 4 : 0;
   constexpr int LDS_BYTES = GEMM_LDS > EPI_LDS ? GEMM_LDS : EPI_LDS;
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
-  f16* As = reinterpret_cast<f16*>(smem);
-  f16* Ws = As + BM * LDK;
+  using V8 = typename Op16<TA>::V8;
+  TA* As = reinterpret_cast<TA*>(smem);
+  TA* Ws = As + BM * LDK;
 
   const int nbn = (N + BN - 1) / BN;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
@@ -81,33 +82,33 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict
   const int wm = wave / WN, wn = wave % WN;
   const int li = lane & 31, g = lane >> 5;
 
-  f16x8 ra[T::A_IT], rw[T::W_IT];
+  V8 ra[T::A_IT], rw[T::W_IT];
   auto gload = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < T::A_IT; ++i) {
       const int c = tid + i * NT;
       const int64_t m = m0 + c / (BK / 8);
       const int k = k0 + (c % (BK / 8)) * 8;
-      ra[i] = (m < M && k < K) ? *reinterpret_cast<const f16x8*>(A + m * K + k) : zero8();
+      ra[i] = (m < M && k < K) ? *reinterpret_cast<const V8*>(A + m * K + k) : zero8_of<TA>();
     }
 #pragma unroll
     for (int i = 0; i < T::W_IT; ++i) {
       const int c = tid + i * NT;
       const int n = n0 + c / (BK / 8);
       const int k = k0 + (c % (BK / 8)) * 8;
-      rw[i] = (n < N && k < K) ? *reinterpret_cast<const f16x8*>(W + (int64_t)n * K + k) : zero8();
+      rw[i] = (n < N && k < K) ? *reinterpret_cast<const V8*>(W + (int64_t)n * K + k) : zero8_of<TA>();
     }
   };
   auto sstore = [&]() {
 #pragma unroll
     for (int i = 0; i < T::A_IT; ++i) {
       const int c = tid + i * NT;
-      *reinterpret_cast<f16x8*>(As + (c / (BK / 8)) * LDK + (c % (BK / 8)) * 8) = ra[i];
+      *reinterpret_cast<V8*>(As + (c / (BK / 8)) * LDK + (c % (BK / 8)) * 8) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < T::W_IT; ++i) {
       const int c = tid + i * NT;
-      *reinterpret_cast<f16x8*>(Ws + (c / (BK / 8)) * LDK + (c % (BK / 8)) * 8) = rw[i];
+      *reinterpret_cast<V8*>(Ws + (c / (BK / 8)) * LDK + (c % (BK / 8)) * 8) = rw[i];
     }
   };
 
@@ -126,13 +127,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict
     if (more) gload((kt + 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      f16x8 af[T::TM], bf[T::TN];
+      V8 af[T::TM], bf[T::TN];
 #pragma unroll
       for (int i = 0; i < T::TM; ++i)
-        af[i] = *reinterpret_cast<const f16x8*>(As + (wm * T::WTM + i * 32 + li) * LDK + kk * 16 + g * 8);
+        af[i] = *reinterpret_cast<const V8*>(As + (wm * T::WTM + i * 32 + li) * LDK + kk * 16 + g * 8);
 #pragma unroll
       for (int j = 0; j < T::TN; ++j)
-        bf[j] = *reinterpret_cast<const f16x8*>(Ws + (wn * T::WTN + j * 32 + li) * LDK + kk * 16 + g * 8);
+        bf[j] = *reinterpret_cast<const V8*>(Ws + (wn * T::WTN + j * 32 + li) * LDK + kk * 16 + g * 8);
 #pragma unroll
       for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -237,23 +238,34 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const f16* __restrict
   }
 }
 
-template <int BM, int BN, int WM, int WN, typename TR, typename TC, bool LN_EPI, typename TY>
+template <int BM, int BN, int WM, int WN, typename TR, typename TC, bool LN_EPI, typename TY, typename TA = f16>
 static hipError_t launch_gemm(const GemmArgs& a) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * (int64_t)((a.N + BN - 1) / BN);
   if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, TR, TC, LN_EPI, TY>), dim3((unsigned)tiles), dim3(WM * WN * 64), 0,
-                     a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, TR, TC, LN_EPI, TY, TA>), dim3((unsigned)tiles), dim3(WM * WN * 64),
+                     0, a.stream, static_cast<const TA*>(a.a), static_cast<const TA*>(a.w), a.bias,
                      static_cast<const TR*>(a.resid), static_cast<TC*>(a.c), a.M, a.N, a.K, a.ln_gamma, a.ln_beta,
                      static_cast<TY*>(a.ln_y), a.eps, a.row_mask, a.epi);
   return hipGetLastError();
 }
 
 // Plain epilogue: pick the row tile so that the grid still covers the chip.
-template <typename TR, typename TC>
+template <typename TR, typename TC, typename TA = f16>
 static hipError_t dispatch_plain(const GemmArgs& a) {
   const int64_t big = ((a.M + 127) / 128) * (int64_t)((a.N + 127) / 128);
-  if (big >= 512) return launch_gemm<128, 128, 2, 2, TR, TC, false, f16>(a);
-  return launch_gemm<64, 128, 2, 2, TR, TC, false, f16>(a);
+  if (big >= 512) return launch_gemm<128, 128, 2, 2, TR, TC, false, f16, TA>(a);
+  return launch_gemm<64, 128, 2, 2, TR, TC, false, f16, TA>(a);
+}
+
+// bf16 operands: plain epilogue, residual bf16 or fp32, output bf16 or fp32.
+static hipError_t run_gemm_bf16(const GemmArgs& a) {
+  if (a.ln_gamma || !a.c) return hipErrorInvalidValue;
+  const bool rb = !a.resid || a.resid_dtype == kBF16;
+  if (!rb && a.resid_dtype != kF32) return hipErrorInvalidValue;
+  if (a.c_dtype != kBF16 && a.c_dtype != kF32) return hipErrorInvalidValue;
+  if (gemm_dma_ok(a)) return run_gemm_dma(a);
+  if (a.c_dtype == kBF16) return rb ? dispatch_plain<bf16, bf16, bf16>(a) : dispatch_plain<float, bf16, bf16>(a);
+  return rb ? dispatch_plain<bf16, float, bf16>(a) : dispatch_plain<float, float, bf16>(a);
 }
 
 template <typename TR, typename TY>
@@ -271,6 +283,8 @@ hipError_t run_gemm(const GemmArgs& a) {
   if ((a.epi & (kEpiMaskBranch | kEpiMaskResid | kEpiMaskOut)) && !a.row_mask) return hipErrorInvalidValue;
   if ((a.epi & kEpiMaskOut) && !a.ln_gamma) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;
+  if (a.ab_dtype == kBF16) return run_gemm_bf16(a);
+  if (a.ab_dtype != kF16) return hipErrorInvalidValue;
   const bool has_resid = a.resid != nullptr;
   if (has_resid && a.resid_dtype != kF16 && a.resid_dtype != kF32) return hipErrorInvalidValue;
   if (a.ln_gamma && gemm_ln_rows_ok(a)) return run_gemm_ln_rows(a);

@@ -1,5 +1,5 @@
 // C[M,N] = A[M,K] . W[N,K]^T (+ bias[N]) (+ resid[M,N]) for the large
-// projections: fp16 operands, fp32 accumulate, C in fp16 or fp32.
+// projections: fp16 or bf16 operands, fp32 accumulate, C in the operand type or fp32.
 //
 // Same contract as the register-staged GEMM (replaces the reference's
 // _gemm_kernel / _tl_linear, torch_transformer_benchmark.py:283-381): each
@@ -16,7 +16,7 @@
 //     of tile kt (vmcnt), the barrier makes every wave's DMA visible and
 //     retires the stage computed in the previous step, which then receives
 //     tile kt + ST - 1;
-//   * v_mfma_f32_32x32x16_f16 with the weight tile as the A operand, so the
+//   * v_mfma_f32_32x32x16_f16 (_bf16) with the weight tile as the A operand, so the
 //     accumulator holds C^T: each lane owns one output row and 4 consecutive
 //     columns per register quad;
 //   * epilogue through LDS: the fp32 tile (+ bias) is staged, then written in
@@ -62,16 +62,17 @@ __device__ __forceinline__ float to_float(T v) {
 
 }  // namespace
 
-template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __restrict__ A, const f16* __restrict__ W,
+template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC, typename TA>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const TA* __restrict__ A, const TA* __restrict__ W,
                                                               const float* __restrict__ bias,
                                                               const TR* __restrict__ resid, TC* __restrict__ C,
                                                               int64_t M, int N, int K,
                                                               const uint8_t* __restrict__ row_mask, int epi) {
   using T = DmaTile<BM, BN, WM, WN, ST>;
   constexpr int BK = T::BK, NT = T::NT, NW = T::NW, LPT = T::LPT;
+  using V8 = typename Op16<TA>::V8;
   __shared__ __attribute__((aligned(1024))) char smem[T::LDS];
-  f16* lds = reinterpret_cast<f16*>(smem);
+  TA* lds = reinterpret_cast<TA*>(smem);
 
   // Tile order: each XCD runs a contiguous range of tile ids; within it, ids
   // walk GM row blocks x all column blocks, so the tiles resident on one XCD
@@ -95,8 +96,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __rest
   // fills row 8b + lane/8, slot lane%8, i.e. logical chunk slot ^ swz(row).
   // Rows past M or N are clamped to the last valid row: their products land in
   // accumulator entries that are never stored.
-  const f16* Ablk = A + m0 * K;
-  const f16* Wblk = W + (int64_t)n0 * K;
+  const TA* Ablk = A + m0 * K;
+  const TA* Wblk = W + (int64_t)n0 * K;
   unsigned src_off[LPT];  // bytes from the block base (A rows) or W block base
 #pragma unroll
   for (int i = 0; i < LPT; ++i) {
@@ -153,14 +154,14 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __rest
 
     // Operand fragments double-buffered across the four 16-deep k-steps: the
     // LDS reads of step kk + 1 are in flight during the MFMAs of step kk.
-    const f16* sa = lds + (kt % ST) * T::STAGE;
-    f16x8 af[2][T::TM], wf[2][T::TN];
+    const TA* sa = lds + (kt % ST) * T::STAGE;
+    V8 af[2][T::TM], wf[2][T::TN];
     auto frags = [&](int kk, int b) {
       const int co = ((2 * kk + g) ^ sw) * 8;
 #pragma unroll
-      for (int i = 0; i < T::TM; ++i) af[b][i] = *reinterpret_cast<const f16x8*>(sa + arow + i * 32 * BK + co);
+      for (int i = 0; i < T::TM; ++i) af[b][i] = *reinterpret_cast<const V8*>(sa + arow + i * 32 * BK + co);
 #pragma unroll
-      for (int j = 0; j < T::TN; ++j) wf[b][j] = *reinterpret_cast<const f16x8*>(sa + wrow + j * 32 * BK + co);
+      for (int j = 0; j < T::TN; ++j) wf[b][j] = *reinterpret_cast<const V8*>(sa + wrow + j * 32 * BK + co);
     };
     frags(0, 0);
 #pragma unroll
@@ -244,10 +245,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __rest
         if constexpr (sizeof(TC) == 4) {
           *reinterpret_cast<f32x4*>(cp) = f32x4{v[0], v[1], v[2], v[3]};
         } else {
-          f16x8 hv;
+          typename Op16<TC>::V8 hv;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) hv[e] = (f16)v[e];
-          *reinterpret_cast<f16x8*>(cp) = hv;
+          for (int e = 0; e < 8; ++e) hv[e] = (TC)v[e];
+          *reinterpret_cast<typename Op16<TC>::V8*>(cp) = hv;
         }
       }
     }
@@ -255,12 +256,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const f16* __rest
   }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC>
+template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC, typename TA>
 static hipError_t launch_dma(const GemmArgs& a) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * (int64_t)((a.N + BN - 1) / BN);
   if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WM, WN, ST, GM, TR, TC>), dim3((unsigned)tiles), dim3(WM * WN * 64), 0,
-                     a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WM, WN, ST, GM, TR, TC, TA>), dim3((unsigned)tiles), dim3(WM * WN * 64),
+                     0, a.stream, static_cast<const TA*>(a.a), static_cast<const TA*>(a.w), a.bias,
                      static_cast<const TR*>(a.resid), static_cast<TC*>(a.c), a.M, a.N, a.K, a.row_mask, a.epi);
   return hipGetLastError();
 }
@@ -302,13 +303,13 @@ static int pick_tile(int64_t M, int N) {
   return best;
 }
 
-template <typename TR, typename TC>
+template <typename TR, typename TC, typename TA = f16>
 static hipError_t dispatch_dma(const GemmArgs& a) {
   switch (pick_tile(a.M, a.N)) {
-    case 0: return launch_dma<256, 256, 4, 2, 2, 4, TR, TC>(a);
-    case 1: return launch_dma<256, 192, 4, 2, 2, 4, TR, TC>(a);
-    case 2: return launch_dma<256, 128, 4, 2, 2, 4, TR, TC>(a);
-    default: return launch_dma<128, 128, 2, 2, 2, 8, TR, TC>(a);
+    case 0: return launch_dma<256, 256, 4, 2, 2, 4, TR, TC, TA>(a);
+    case 1: return launch_dma<256, 192, 4, 2, 2, 4, TR, TC, TA>(a);
+    case 2: return launch_dma<256, 128, 4, 2, 2, 4, TR, TC, TA>(a);
+    default: return launch_dma<128, 128, 2, 2, 2, 8, TR, TC, TA>(a);
   }
 }
 
@@ -322,6 +323,11 @@ bool gemm_dma_ok(const GemmArgs& a) {
 }
 
 hipError_t run_gemm_dma(const GemmArgs& a) {
+  if (a.ab_dtype == kBF16) {  // residual bf16 or fp32, output bf16 or fp32
+    const bool rb = !a.resid || a.resid_dtype == kBF16;
+    if (a.c_dtype == kBF16) return rb ? dispatch_dma<bf16, bf16, bf16>(a) : dispatch_dma<float, bf16, bf16>(a);
+    return rb ? dispatch_dma<bf16, float, bf16>(a) : dispatch_dma<float, float, bf16>(a);
+  }
   const bool c16 = a.c_dtype == kF16;
   if (!a.resid || a.resid_dtype == kF16) return c16 ? dispatch_dma<f16, f16>(a) : dispatch_dma<f16, float>(a);
   return c16 ? dispatch_dma<float, f16>(a) : dispatch_dma<float, float>(a);

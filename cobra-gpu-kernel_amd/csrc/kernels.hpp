@@ -21,7 +21,7 @@ enum : int {
 };
 
 struct LnArgs {
-  const void* x;           // [rows, d], x_dtype
+  const void* x;           // [rows, d], x_dtype (kF16, kF32 or kBF16; y_dtype likewise)
   int x_dtype;
   const void* branch;      // optional [rows, d] added to x before the norm
   int branch_f32;          // branch dtype: 1 = fp32, 0 = fp16
@@ -59,8 +59,8 @@ struct PadArgs {
 hipError_t run_pad(const PadArgs& a);
 
 struct GemmArgs {
-  const void* a;           // [M, K] fp16, row-major
-  const void* w;           // [N, K] fp16 (nn.Linear layout)
+  const void* a;           // [M, K] ab_dtype, row-major
+  const void* w;           // [N, K] ab_dtype (nn.Linear layout)
   const float* bias;       // optional [N] fp32
   const void* resid;       // optional [M, N] added in the epilogue
   int resid_dtype;
@@ -77,6 +77,9 @@ struct GemmArgs {
   hipStream_t stream;
   const uint8_t* row_mask = nullptr;  // [M] when a kEpiMask* flag is set
   int epi = 0;             // kEpi* flags
+  // Operand type of a and w: kF16, or kBF16 (then resid and c are kBF16 or kF32 and
+  // there is no LayerNorm epilogue).
+  int ab_dtype = 0;  // kF16
 };
 // Compute units of the current device (cached after the first call).
 inline int compute_units() {
@@ -122,8 +125,8 @@ bool gemm_ln_rows_ok(const GemmArgs& a);
 hipError_t run_gemm_ln_rows(const GemmArgs& a);
 
 struct AttnArgs {
-  const void* qkv;         // [B*S, 3*H*hd] fp16: q | k | v column blocks, head-major inside each
-  void* ctx;               // [B*S, H*hd] fp16
+  const void* qkv;         // [B*S, 3*H*hd] dtype: q | k | v column blocks, head-major inside each
+  void* ctx;               // [B*S, H*hd] dtype
   int64_t batch;
   int seq_len;
   int heads;
@@ -132,6 +135,7 @@ struct AttnArgs {
   int causal;
   hipStream_t stream;
   const uint64_t* key_bits = nullptr;  // optional [batch][ceil(S/64)]: bit j of word w = key 64w+j valid
+  int dtype = 0;           // element type of qkv and ctx: kF16 (0) or kBF16
 };
 hipError_t run_attn(const AttnArgs& a);
 

@@ -7,10 +7,11 @@
 // the square root, affine, cast on store.  The row mask m (0 for a padded row,
 // 1 otherwise) multiplies the residual (MASK_RESID) and/or the output
 // (MASK_OUT) as the reference kernel does (TTB:511-534).  A null gamma (and beta)
-// means a LayerNorm without elementwise affine.
+// means a LayerNorm without elementwise affine.  x and y are fp16, fp32 or bf16
+// each; the branch fp16 or fp32.
 //
 // Layout: LPR lanes own one row, each lane holds NCH chunks of 8 consecutive
-// elements (16 B of fp16, 32 B of fp32), so every global access is a full
+// elements (16 B of fp16 or bf16, 32 B of fp32), so every global access is a full
 // vector access and the row reductions never leave the LPR-lane group.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -284,6 +285,17 @@ static hipError_t dispatch_ln_geometry(const LnArgs& a) {
 
 static bool vec_aligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Element types of x and y (fp16, fp32 or bf16 each); vec: the 16-byte-chunk kernels.
+template <typename TX>
+static hipError_t ln_by_y(const LnArgs& a, bool vec) {
+  switch (a.y_dtype) {
+    case kF16: return vec ? dispatch_ln_geometry<TX, f16>(a) : dispatch_ln_any<TX, f16>(a);
+    case kF32: return vec ? dispatch_ln_geometry<TX, float>(a) : dispatch_ln_any<TX, float>(a);
+    case kBF16: return vec ? dispatch_ln_geometry<TX, bf16>(a) : dispatch_ln_any<TX, bf16>(a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t run_ln(const LnArgs& a) {
   if (a.rows < 0 || a.d <= 0 || a.d > kLnMaxD) return hipErrorInvalidValue;
   const int64_t d = a.d;
@@ -296,18 +308,12 @@ hipError_t run_ln(const LnArgs& a) {
   const bool vec = d % 8 == 0 && dense && vec_aligned(a.x) && vec_aligned(a.y) && (!a.branch || vec_aligned(a.branch)) &&
                    (!a.resid_out || vec_aligned(a.resid_out)) && (!a.gamma || vec_aligned(a.gamma)) &&
                    (!a.beta || vec_aligned(a.beta));
-  if (!vec) {
-    if (a.x_dtype == kF16 && a.y_dtype == kF16) return dispatch_ln_any<f16, f16>(a);
-    if (a.x_dtype == kF16 && a.y_dtype == kF32) return dispatch_ln_any<f16, float>(a);
-    if (a.x_dtype == kF32 && a.y_dtype == kF16) return dispatch_ln_any<float, f16>(a);
-    if (a.x_dtype == kF32 && a.y_dtype == kF32) return dispatch_ln_any<float, float>(a);
-    return hipErrorInvalidValue;
+  switch (a.x_dtype) {
+    case kF16: return ln_by_y<f16>(a, vec);
+    case kF32: return ln_by_y<float>(a, vec);
+    case kBF16: return ln_by_y<bf16>(a, vec);
+    default: return hipErrorInvalidValue;
   }
-  if (a.x_dtype == kF16 && a.y_dtype == kF16) return dispatch_ln_geometry<f16, f16>(a);
-  if (a.x_dtype == kF16 && a.y_dtype == kF32) return dispatch_ln_geometry<f16, float>(a);
-  if (a.x_dtype == kF32 && a.y_dtype == kF16) return dispatch_ln_geometry<float, f16>(a);
-  if (a.x_dtype == kF32 && a.y_dtype == kF32) return dispatch_ln_geometry<float, float>(a);
-  return hipErrorInvalidValue;
 }
 
 }  // namespace cobra

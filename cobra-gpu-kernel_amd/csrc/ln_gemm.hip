@@ -354,7 +354,8 @@ static hipError_t gemm_ln_rows_shape(const GemmArgs& a) {
 
 bool gemm_ln_rows_ok(const GemmArgs& a) {
   return a.ln_gamma && a.ln_beta && a.ln_y && (a.K == 64 || a.K == 128) && (a.N == 64 || a.N == 128) &&
-         !(a.epi & kEpiGelu) && (!a.c || a.c_dtype == kF32) && (a.ln_y_dtype == kF16 || a.ln_y_dtype == kF32);
+         !(a.epi & kEpiGelu) && (!a.c || a.c_dtype == kF32) && (a.ln_y_dtype == kF16 || a.ln_y_dtype == kF32) &&
+         a.ab_dtype == kF16;
 }
 
 hipError_t run_gemm_ln_rows(const GemmArgs& a) {

@@ -10,7 +10,8 @@
  * Conventions shared by every entry point:
  *   - all tensors are device pointers to row-major, densely packed buffers,
  *     16-byte aligned; the caller allocates every buffer (outputs included);
- *   - dtype codes: COBRA_F16 (IEEE half) or COBRA_F32;
+ *   - dtype codes: COBRA_F16 (IEEE half), COBRA_F32, and COBRA_BF16 (bfloat16)
+ *     where an entry point says so;
  *   - `stream` is a hipStream_t (NULL = legacy default stream).  Work is only
  *     enqueued: nothing allocates, frees or synchronises, so every call may be
  *     captured into a hipGraph;
@@ -27,9 +28,9 @@
 extern "C" {
 #endif
 
-#define COBRA_ABI_VERSION 10
+#define COBRA_ABI_VERSION 11
 
-enum { COBRA_F16 = 0, COBRA_F32 = 1 };
+enum { COBRA_F16 = 0, COBRA_F32 = 1, COBRA_BF16 = 2 };
 
 /*
  * Epilogue / row-mask flags (bit set), applied in this order.  A row mask is
@@ -61,7 +62,8 @@ const char* cobra_error_string(int code);
  *     resid_out = r (optional, fp32);
  *     y = (r - mean(r)) * rsqrt(var(r) + eps) * gamma + beta     (biased var)
  *     y *= m (COBRA_EPI_MASK_OUT)
- * x, branch, y: [rows, d]; gamma, beta: [d] fp32; row_mask: [rows] bytes
+ * x, branch, y: [rows, d]; x and y in any of the three dtypes, branch COBRA_F16 or
+ * COBRA_F32; gamma, beta: [d] fp32; row_mask: [rows] bytes
  * (required when mask_flags != 0; only the two flags above are accepted).
  * d <= 4096; pointers aligned to their element size (widths that are multiples of
  * 8 on 16-byte aligned buffers take the vector kernels).  Replaces _tl_add_ln /
@@ -90,13 +92,15 @@ int cobra_ln_fwd_strided(const void* x, int x_dtype, int64_t ldx, const void* br
  * Projection GEMM with fused epilogue:
  *     v = a . w^T + bias;  then the epi flags GELU, MASK_BRANCH;  v += resid;
  *     then MASK_RESID;  c = v
- * a: [M, K] fp16, w: [N, K] fp16 (nn.Linear weight layout), bias: [N] fp32
- * (optional), resid: [M, N] (optional), row_mask: [M] bytes (required by the
- * mask flags), c: [M, N] in c_dtype.  fp32 accumulate and epilogue.
+ * a: [M, K] and w: [N, K] (nn.Linear weight layout) in ab_dtype, COBRA_F16 or
+ * COBRA_BF16 (v_mfma_f32_32x32x16_bf16); bias: [N] fp32 (optional), resid: [M, N]
+ * (optional), row_mask: [M] bytes (required by the mask flags), c: [M, N] in
+ * c_dtype.  resid and c are COBRA_F16 / COBRA_F32 with fp16 operands, COBRA_BF16 /
+ * COBRA_F32 with bf16 operands.  fp32 accumulate and epilogue.
  * K % 8 == 0; COBRA_EPI_MASK_OUT is rejected (no LayerNorm here).  Replaces
  * _tl_linear / _gemm_kernel (TTB:355-381, 283-353).
  */
-int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
+int cobra_linear_fwd(const void* a, const void* w, int ab_dtype, const float* bias, const void* resid, int resid_dtype,
                      const uint8_t* row_mask, int epi, void* c, int c_dtype, int64_t M, int64_t N, int64_t K,
                      void* stream);
 
@@ -104,8 +108,8 @@ int cobra_linear_fwd(const void* a, const void* w, const float* bias, const void
  * Projection GEMM + residual + LayerNorm over whole rows:
  *     r = a . w^T + bias (GELU, MASK_BRANCH) + resid (MASK_RESID);
  *     resid_out = r (optional, fp32);  y = LayerNorm(r) * gamma + beta (MASK_OUT)
- * Shapes as cobra_linear_fwd; requires N <= 128 (one workgroup owns a row) and
- * N % 8 == 0.  Replaces _tl_linear_ln / _gemm_ln_kernel (TTB:465-488, 394-463).
+ * Shapes as cobra_linear_fwd with fp16 operands; requires N <= 128 (one workgroup owns
+ * a row) and N % 8 == 0.  Replaces _tl_linear_ln / _gemm_ln_kernel (TTB:465-488, 394-463).
  */
 int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
                         const uint8_t* row_mask, int epi, float* resid_out, const float* gamma, const float* beta,
@@ -135,9 +139,12 @@ int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int6
 
 /*
  * Multi-head attention on a packed projection buffer:
- *     qkv: [batch*seq_len, 3*D] fp16 with column blocks q | k | v, each split
- *          into `heads` contiguous slices of head_dim (D = heads*head_dim);
- *     ctx: [batch*seq_len, D] fp16, ctx_i = softmax((q_i k^T) * scale) v per head.
+ *     qkv: [batch*seq_len, 3*D] in dtype (COBRA_F16 or COBRA_BF16) with column
+ *          blocks q | k | v, each split into `heads` contiguous slices of head_dim
+ *          (D = heads*head_dim);
+ *     ctx: [batch*seq_len, D] in dtype, ctx_i = softmax((q_i k^T) * scale) v per head
+ *          (fp32 scores and softmax; the probabilities rounded to dtype for the P.V
+ *          product, as the reference's fp16 kernel does).
  * causal != 0 masks keys j > i; key_bits (optional, from cobra_mask_bits)
  * masks padded keys (TTB:106-109).  A query left with no valid key gets a
  * zero row (the reference's softmax would give NaN there; the sublayer zeroes
@@ -145,7 +152,7 @@ int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int6
  * Replaces _tl_attn / _attn_kernel (TTB:828-854, 572-649; causal only there)
  * and the SDPA call used for non-causal and masked attention (TTB:1240-1253).
  */
-int cobra_attn_fwd(const void* qkv, void* ctx, const uint64_t* key_bits, int64_t batch, int64_t seq_len,
+int cobra_attn_fwd(const void* qkv, void* ctx, int dtype, const uint64_t* key_bits, int64_t batch, int64_t seq_len,
                    int64_t heads, int64_t head_dim, float scale, int causal, void* stream);
 
 /*
@@ -183,7 +190,9 @@ enum {
  * kernel, TTB:578, 763-765, and masks its GEMM loads).  FUSED covers seq_len <= 128 with
  * d_model 128 (head_dim 32 or 64), 64 (32, 64) or 96 (32), with or without a
  * token mask; and, for fp16 activations while batch * ceil(seq_len / 32) <= 2 x
- * the device's compute units, d_model 128 at head_dim 8 or 128.  `masked` (a token
+ * the device's compute units, d_model 128 at head_dim 8 or 128.  bf16 activations
+ * (x_dtype COBRA_BF16) take STAGED (or PADDED): LN1, the QKV GEMM, the attention and
+ * the out-projection with bf16 operands.  `masked` (a token
  * mask will be passed) only changes the STAGED plan's workspace.  Host-only: no
  * device work.  The reference's counterpart is the gate set of
  * UserOptimizedTransformer._prepare (TTB:1030-1071), which also looks at the
@@ -203,9 +212,12 @@ int64_t cobra_layer_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_mo
  * keys are masked in the attention (TTB:106-109) and padded rows get a zero
  * attention output, r = x (TTB:121-122); the workspace must then be sized
  * with masked = 1.
- * x, y: [batch*seq_len, d_model] in x_dtype; w_qkv: [3*d_model, d_model] fp16
- * (rows: q_proj, k_proj, v_proj weights, in that order); b_qkv: [3*d_model]
- * fp32; w_o: [d_model, d_model] fp16; b_o and the LayerNorm parameters fp32.
+ * x, y: [batch*seq_len, d_model] in x_dtype (COBRA_F16, COBRA_F32 or COBRA_BF16);
+ * w_qkv: [3*d_model, d_model] (rows: q_proj, k_proj, v_proj weights, in that order)
+ * and w_o: [d_model, d_model] in fp16, or in bf16 when x_dtype is COBRA_BF16;
+ * b_qkv: [3*d_model], b_o and the LayerNorm parameters fp32.  With bf16
+ * activations h, q, k, v, the probabilities and the context are bf16 MFMA operands
+ * and r = x + branch is formed in fp32.
  * ln1_w and ln1_b may both be NULL: LN1 without elementwise affine, for a
  * caller that has folded it into the projection (w_qkv . diag(ln1_w) and
  * b_qkv + w_qkv . ln1_b), which spares the kernels those reads; exactly one

@@ -72,7 +72,9 @@ class OracleSelfAttention(nn.Module):
         last query + 1 under causality (the keys beyond it would be -inf).
         """
         kv_end = k.shape[-2]
-        scores = torch.matmul(q, k.transpose(-2, -1)) * self.scale  # TTB:98
+        # k^T made contiguous: bf16 batched products with a transposed right operand have
+        # faulted this GPU, so no reference ever passes one.
+        scores = torch.matmul(q, k.transpose(-2, -1).contiguous()) * self.scale  # TTB:98
         if causal:  # TTB:100-104 (triu(diagonal=1) -> -inf)
             rows = torch.arange(q0, q0 + q.shape[-2], device=q.device)
             cols = torch.arange(kv_end, device=q.device)

@@ -22,8 +22,8 @@ def build_pair(d_model: int, heads: int, seed: int = 0, dtype: torch.dtype = tor
     from cobra_amd import CobraAttentionSublayer
 
     ref = make_sublayer(d_model, heads, seed=seed)
-    if dtype == torch.float16:
-        quantize_like(ref, torch.float16)
+    if dtype in (torch.float16, torch.bfloat16):
+        quantize_like(ref, dtype)
     mod = CobraAttentionSublayer(d_model, heads, graph=graph)
     mod.load_state_dict(ref.state_dict(), strict=True)
     mod = mod.to(device=DEV, dtype=dtype).eval()

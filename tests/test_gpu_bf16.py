@@ -1,0 +1,235 @@
+"""GPU parity of the bf16 path: bf16 activations and weights, bf16 MFMA operands
+(v_mfma_f32_32x32x16_bf16), fp32 accumulation, softmax and residual.
+
+The reference runs a bf16 model through its unmodified PyTorch ops (TTB:952-968) and
+validates it only against itself (tools/validate.py:82-85, the case-1 shape); its own
+comment there notes that any other arithmetic order fails its fp16-sized gate by many
+elements in bf16.  Here the oracle is the fp32 restatement on the same bf16-rounded
+inputs and weights, and the gate is the reference's scaled to bf16: abs <= 1.6e-2
+(the reference's 2e-3 times 8, bf16's unit roundoff 2^-8 over fp16's 2^-11) or
+rel <= 2e-2, zero failing elements.  Op-level checks compare against fp32 torch on the
+same bf16 values with tolerances derived from the roundings each op performs.
+"""
+
+import pytest
+import torch
+
+from oracle import OracleTransformerConfig, compare_outputs, make_input, make_model, model_forward, quantize_like
+
+from _gpu_util import DEV, build_pair, log, oracle_on
+
+pytestmark = pytest.mark.gpu
+
+BF16_ATOL, BF16_RTOL = 1.6e-2, 2e-2
+U_BF16 = 2.0 ** -8  # unit roundoff of bf16 (8 significant bits)
+
+
+def bf16_gate(want, got, what):
+    res = compare_outputs(want, got, rtol=BF16_RTOL, atol=BF16_ATOL)
+    err = (got.float() - want.float()).abs()
+    ratio = (err / torch.maximum(torch.full_like(err, BF16_ATOL), BF16_RTOL * want.float().abs())).max().item()
+    log(f"[bf16] {what}: max_abs={res.max_abs_error:.3e} max_rel={res.max_relative_error:.3e} "
+        f"gate_ratio={ratio:.3f} failed={res.failed_elements}/{res.total_elements}")
+    return res
+
+
+# ---- op level ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(300, 384, 128), (8192, 1024, 1024), (4096, 3072, 1024), (96, 200, 64)])
+@pytest.mark.parametrize("out_fp32", [False, True])
+def test_linear_bf16(M, N, K, out_fp32):
+    """bf16 operands, fp32 accumulation: the products are exact in fp32, so the fp32
+    output differs from fp32 torch only in summation order; the bf16 output by one rounding."""
+    from cobra_amd import ops
+
+    log(f"[bf16 linear] M{M} N{N} K{K} out_fp32={out_fp32}")
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).to(torch.bfloat16)
+    b = torch.randn(N, generator=g)
+    r = torch.randn(M, N, generator=g)
+    want = a.float() @ w.float().t() + b
+    with torch.inference_mode():
+        got = ops.linear(a.to(DEV), w.to(DEV), b.to(DEV), out_fp32=out_fp32).float().cpu()
+        got_r = ops.linear(a.to(DEV), w.to(DEV), b.to(DEV), out_fp32=True, resid=r.to(DEV)).cpu()
+        got_rb = ops.linear(a.to(DEV), w.to(DEV), b.to(DEV), resid=r.to(torch.bfloat16).to(DEV)).float().cpu()
+        got_g = ops.linear(a.to(DEV), w.to(DEV), b.to(DEV), gelu=True, out_fp32=True).cpu()
+    assert got.dtype == torch.float32
+    tol32 = dict(atol=1e-4, rtol=1e-4)
+    if out_fp32:
+        torch.testing.assert_close(got, want, **tol32)
+    else:
+        torch.testing.assert_close(got, want, atol=1e-4, rtol=U_BF16)
+    torch.testing.assert_close(got_r, want + r, **tol32)
+    torch.testing.assert_close(got_rb, want + r.to(torch.bfloat16).float(), atol=1e-4, rtol=U_BF16)
+    torch.testing.assert_close(got_g, torch.nn.functional.gelu(want), **tol32)
+
+
+def test_linear_bf16_masks():
+    """MASK_BRANCH (padded rows come out as the residual) and MASK_RESID with bf16 operands."""
+    from cobra_amd import ops
+
+    M, N, K = 500, 256, 128
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).to(torch.bfloat16)
+    b = torch.randn(N, generator=g)
+    r = torch.randn(M, N, generator=g)
+    m = torch.rand(M, generator=g) < 0.7
+    want = a.float() @ w.float().t() + b
+    with torch.inference_mode():
+        br = ops.linear(a.to(DEV), w.to(DEV), b.to(DEV), out_fp32=True, resid=r.to(DEV), rmask=m.to(DEV),
+                        mask_branch=True).cpu()
+        mr = ops.linear(a.to(DEV), w.to(DEV), b.to(DEV), out_fp32=True, resid=r.to(DEV), rmask=m.to(DEV)).cpu()
+    torch.testing.assert_close(br, torch.where(m[:, None], want + r, r), atol=1e-4, rtol=1e-4)
+    assert torch.equal(br[~m], r[~m])
+    torch.testing.assert_close(mr, (want + r) * m[:, None], atol=1e-4, rtol=1e-4)
+
+
+def _attn_reference(qkv, B, S, H, hd, causal, mask=None):
+    """fp32 attention on the bf16 values (contiguous operands throughout)."""
+    D = H * hd
+    q, k, v = qkv.float().view(B, S, 3, H, hd).permute(2, 0, 3, 1, 4).contiguous()
+    s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * hd ** -0.5
+    if causal:
+        s = s.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    if mask is not None:
+        s = s.masked_fill(~mask[:, None, None, :], float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    out = torch.matmul(p, v).permute(0, 2, 1, 3).reshape(B * S, D)
+    if mask is not None:
+        out = torch.nan_to_num(out)
+    return out
+
+
+@pytest.mark.parametrize("B,S,H,hd,causal", [(2, 300, 4, 32, False), (2, 300, 4, 32, True), (3, 200, 2, 64, True),
+                                             (2, 500, 8, 16, False), (2, 257, 2, 128, False),
+                                             (4, 100, 2, 256, True), (4, 128, 4, 128, False), (2, 40, 4, 64, False)])
+def test_attn_bf16(B, S, H, hd, causal):
+    """The probabilities are rounded to bf16 for the P.V product (as the reference's fp16
+    kernel rounds them to fp16) and ctx once on output: within the bf16 gate of fp32.
+    qkv ~ N(0, 1), the reference's input distribution.  The kernel also rounds Q * scale *
+    log2(e) to bf16, so a probability's relative error grows with its logit's magnitude:
+    with qkv ~ 1.5 N(0, 1) (logits 2.25 x larger) 1-5 elements per case reached 1.36 x the gate."""
+    from cobra_amd import ops
+
+    log(f"[bf16 attn] B{B} S{S} H{H} hd{hd} causal={causal}")
+    g = torch.Generator().manual_seed(S + hd)
+    qkv = torch.randn(B * S, 3 * H * hd, generator=g).to(torch.bfloat16)
+    mask = torch.rand(B, S, generator=g) < 0.8
+    mask[:, 0] = True
+    with torch.inference_mode():
+        got = ops.attn(qkv.to(DEV), B, S, H, hd, hd ** -0.5, causal=causal).float().cpu()
+        got_m = ops.attn(qkv.to(DEV), B, S, H, hd, hd ** -0.5, causal=causal, key_mask=mask.to(DEV)).float().cpu()
+    assert bf16_gate(_attn_reference(qkv, B, S, H, hd, causal), got, f"attn hd{hd}").passed
+    assert bf16_gate(_attn_reference(qkv, B, S, H, hd, causal, mask), got_m, f"attn hd{hd} masked").passed
+
+
+@pytest.mark.parametrize("rows,d", [(1000, 128), (333, 1024), (64, 96), (50, 100)])
+def test_layernorm_bf16(rows, d):
+    from cobra_amd import ops
+
+    g = torch.Generator().manual_seed(rows + d)
+    x = (torch.randn(rows, d, generator=g) * 2 + 1).to(torch.bfloat16)
+    w, b = torch.rand(d, generator=g) + 0.5, torch.randn(d, generator=g) * 0.2
+    want = torch.nn.functional.layer_norm(x.float(), (d,), w, b, 1e-5)
+    with torch.inference_mode():
+        y16 = ops.ln_strided(x.to(DEV), d, w.to(DEV), b.to(DEV)).cpu()
+        y32 = ops.ln_strided(x.to(DEV), d, w.to(DEV), b.to(DEV), out_dtype=torch.float32).cpu()
+    assert y16.dtype == torch.bfloat16
+    torch.testing.assert_close(y32, want, atol=2e-5, rtol=2e-5)
+    torch.testing.assert_close(y16.float(), want, atol=1e-5, rtol=U_BF16)
+
+
+# ---- the sublayer ------------------------------------------------------------------------
+
+SUBLAYER = [(64, 128, 128, 4, False), (64, 128, 128, 4, True), (64, 128, 1024, 4, False), (64, 128, 128, 16, True),
+            (64, 128, 128, 1, False), (8, 1024, 128, 4, True), (3, 77, 96, 3, True), (3, 50, 100, 4, False),
+            (5, 333, 256, 4, False)]
+
+
+@pytest.mark.parametrize("B,S,D,H,causal", SUBLAYER, ids=[f"B{c[0]}-S{c[1]}-D{c[2]}-H{c[3]}-{'c' if c[4] else 'n'}"
+                                                           for c in SUBLAYER])
+@pytest.mark.parametrize("masked", [False, True])
+def test_sublayer_bf16(B, S, D, H, causal, masked):
+    from cobra_amd import ops
+
+    log(f"[bf16 sublayer] B{B} S{S} D{D} H{H} causal={causal} masked={masked}")
+    ref, mod = build_pair(D, H, seed=1, dtype=torch.bfloat16)
+    x = make_input(B, S, D, seed=2).to(torch.bfloat16)
+    mask = None
+    if masked:
+        mask = torch.rand(B, S, generator=torch.Generator().manual_seed(B + S)) < 0.75
+        mask[:, 0] = True
+    with torch.inference_mode():
+        r, y = mod(x.to(DEV), None if mask is None else mask.to(DEV), causal=causal, return_residual=True)
+        y2 = mod(x.to(DEV), None if mask is None else mask.to(DEV), causal=causal)
+        torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16 and r.dtype == torch.float32
+    assert mod.plan == (ops.PLAN_PADDED if D % 8 or (D // H) % 8 else ops.PLAN_STAGED)
+    assert torch.equal(y, y2)  # the residual request does not change y (fp32 r either way)
+    dev = "cpu" if B * S * D <= (1 << 21) else DEV
+    want_r, want = oracle_on(ref, x.float(), causal, dev, return_residual=True, mask=mask)
+    assert bf16_gate(want, y.float().cpu(), f"sublayer B{B} S{S} D{D} H{H}").passed
+    # r = x + branch in fp32: the branch's error only (no output rounding)
+    assert bf16_gate(want_r, r.cpu(), "residual").passed
+
+
+def test_sublayer_bf16_graph_and_bound_launch():
+    """bf16 through the bound launch (steady-state path) and a hipGraph replay, equal to eager."""
+    ref, mod = build_pair(128, 4, seed=3, dtype=torch.bfloat16)
+    _, gmod = build_pair(128, 4, seed=3, dtype=torch.bfloat16, graph=True)
+    x = make_input(16, 128, 128, seed=4).to(torch.bfloat16).to(DEV)
+    with torch.inference_mode():
+        a = mod(x).clone()
+        b = mod(x).clone()  # bound launch
+        c = gmod(x).clone()
+        d = gmod(x).clone()
+        torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
+    assert gmod._graph is not None
+
+
+def test_module_cast_to_bf16():
+    """A module built in fp32 and cast with .to(torch.bfloat16): its weights round to bf16
+    there, and the forward matches the oracle on the same rounded weights."""
+    ref, mod = build_pair(128, 4, seed=5, dtype=torch.float32)
+    x = make_input(8, 128, 128, seed=6)
+    xb = x.to(torch.bfloat16)
+    mb = mod.to(torch.bfloat16)
+    with torch.inference_mode():
+        yb = mb(xb.to(DEV)).float().cpu()
+    quantize_like(ref, torch.bfloat16)
+    assert bf16_gate(oracle_on(ref, xb.float(), False, "cpu"), yb, "module bf16").passed
+
+
+# ---- the stack ---------------------------------------------------------------------------
+
+STACK = [(64, 128, 128, 4, 128, 4, True), (8, 128, 256, 4, 512, 2, False), (4, 96, 96, 3, 160, 2, True)]
+
+
+@pytest.mark.parametrize("cfg", STACK, ids=[f"B{c[0]}-S{c[1]}-D{c[2]}-H{c[3]}-F{c[4]}-L{c[5]}" for c in STACK])
+@pytest.mark.parametrize("masked", [False, True])
+def test_stack_bf16(cfg, masked):
+    """The reference's bf16 check (tools/validate.py:82-85: the case-1 shape, causal, 4
+    layers) and two more geometries, against the fp32 oracle model on bf16-rounded weights."""
+    from cobra_amd import CobraTransformer, TransformerConfig
+
+    B, S = cfg[0], cfg[1]
+    log(f"[bf16 stack] {cfg} masked={masked}")
+    ref = make_model(OracleTransformerConfig(*cfg), seed=7)
+    quantize_like(ref, torch.bfloat16)
+    mod = CobraTransformer(TransformerConfig(*cfg))
+    mod.load_state_dict(ref.state_dict(), strict=True)
+    mod = mod.to(device=DEV, dtype=torch.bfloat16).eval()
+    x = make_input(B, S, cfg[2], seed=8).to(torch.bfloat16)
+    mask = None
+    if masked:
+        lengths = torch.randint(max(1, S // 2), S + 1, (B,), generator=torch.Generator().manual_seed(9))
+        mask = torch.arange(S)[None, :] < lengths[:, None]
+        x = x.masked_fill(~mask[..., None], 0)
+    with torch.inference_mode():
+        y = mod(x.to(DEV), None if mask is None else mask.to(DEV)).float().cpu()
+        torch.cuda.synchronize()
+    want = model_forward(ref, x.float(), mask)
+    assert bf16_gate(want, y, f"stack {cfg}").passed

@@ -32,7 +32,6 @@ def test_defaults_are_the_reference_flags():
     (["--rtol", "-1"], "rtol"),
     (["--warmup", "-1"], "warmup"),
     (["--repeats", "0"], "repeats"),
-    (["--dtype", "bfloat16"], "bfloat16"),
     (["--compile-user"], "compile"),
 ])
 def test_validation_rejects(argv, msg):
@@ -83,6 +82,7 @@ def test_random_case_padding_semantics():
     ["--dtype", "float16", "--causal", "--padding-ratio", "0.3"],
     ["--dtype", "float16", "--d-model", "128", "--heads", "4", "--ffn-dim", "128"],
     ["--dtype", "float32", "--reference-precision", "harness"],
+    ["--dtype", "bfloat16", "--causal", "--padding-ratio", "0.3", "--atol", "0.016"],
 ])
 def test_harness_end_to_end(extra, capsys):
     argv = ["--device", "cuda", "--batch-size", "4", "--seq-len", "48", "--d-model", "64", "--heads", "2",

@@ -42,11 +42,22 @@ def test_argument_validation_rejects_before_any_launch():
     # a mask flag without a mask, an unknown flag
     assert lib.cobra_ln_fwd(256, 0, None, 0, 256, 256, None, _lib.EPI_MASK_OUT, None, 256, 0, 8, 128, 1e-5,
                             None) != 0
-    assert lib.cobra_linear_fwd(256, 256, None, None, 0, 256, 64, 256, 0, 8, 8, 8, None) != 0
-    assert lib.cobra_linear_fwd(256, 256, None, None, 0, 256, _lib.EPI_MASK_OUT, 256, 0, 8, 8, 8, None) != 0
-    assert lib.cobra_linear_fwd(256, 256, None, None, 0, None, _lib.EPI_MASK_RESID, 256, 0, 8, 8, 8, None) != 0
-    assert lib.cobra_attn_fwd(16, 16, None, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
-    assert lib.cobra_attn_fwd(256, 256, 12, 1, 4, 1, 16, 0.1, 0, None) != 0  # misaligned key bits
+    F16, BF16, F32 = _lib.F16, _lib.BF16, _lib.F32
+    assert lib.cobra_linear_fwd(256, 256, F16, None, None, 0, 256, 64, 256, 0, 8, 8, 8, None) != 0
+    assert lib.cobra_linear_fwd(256, 256, F16, None, None, 0, 256, _lib.EPI_MASK_OUT, 256, 0, 8, 8, 8, None) != 0
+    assert lib.cobra_linear_fwd(256, 256, F16, None, None, 0, None, _lib.EPI_MASK_RESID, 256, 0, 8, 8, 8, None) != 0
+    assert lib.cobra_linear_fwd(256, 256, F32, None, None, 0, None, 0, 256, F32, 8, 8, 8, None) != 0  # operand type
+    assert lib.cobra_linear_fwd(256, 256, BF16, None, None, 0, None, 0, 256, F16, 8, 8, 8, None) != 0  # bf16 -> fp16
+    assert lib.cobra_linear_fwd(256, 256, F16, None, None, 0, None, 0, 256, BF16, 8, 8, 8, None) != 0  # fp16 -> bf16
+    assert lib.cobra_attn_fwd(16, 16, F16, None, 1, 4, 1, 12, 0.1, 0, None) != 0  # misaligned pointers
+    assert lib.cobra_attn_fwd(256, 256, F16, 12, 1, 4, 1, 16, 0.1, 0, None) != 0  # misaligned key bits
+    assert lib.cobra_attn_fwd(256, 256, F32, None, 1, 4, 1, 16, 0.1, 0, None) != 0  # operand type
+    assert lib.cobra_ln_fwd(256, BF16, 256, BF16, 256, 256, None, 0, None, 256, BF16, 8, 128, 1e-5,
+                            None) != 0  # bf16 branch
+    assert lib.cobra_layer_plan(2, 16, 128, 4, 0, BF16) == _lib.PLAN_STAGED   # bf16: the staged kernels
+    assert lib.cobra_layer_plan(2, 16, 100, 4, 0, BF16) == _lib.PLAN_PADDED
+    assert lib.cobra_layer_workspace_bytes(2, 16, 128, 4, 0, BF16) == \
+        lib.cobra_layer_workspace_bytes(2, 16, 128, 16, 0, F32)
     assert lib.cobra_mask_bits(256, 12, 1, 4, None) != 0                   # misaligned key bits
     assert lib.cobra_layer_workspace_bytes(2, 16, 528, 2, 0, _lib.F16) == -1       # head_dim 264
     assert lib.cobra_layer_workspace_bytes(2, 16, 100, 3, 0, _lib.F16) == -1       # d_model % heads
@@ -246,8 +257,10 @@ def test_plan_selection_per_config():
     assert ops.layer_plan(64, 128, 128, 4, dtype=torch.float32) == ops.PLAN_FUSED
     assert ops.layer_workspace_bytes(64, 128, 128, 1) == 0
     assert ops.layer_workspace_bytes(64, 128, 128, 1, dtype=torch.float32) == 8192 * 128 * 2 + 8192 * 384 * 2
+    assert ops.layer_plan(2, 16, 128, 4, dtype=torch.bfloat16) == ops.PLAN_STAGED  # bf16: staged kernels
+    assert ops.layer_plan(2, 16, 120, 10, dtype=torch.bfloat16) == ops.PLAN_PADDED
     with pytest.raises(TypeError):
-        ops.layer_plan(2, 16, 128, 4, dtype=torch.bfloat16)
+        ops.layer_plan(2, 16, 128, 4, dtype=torch.float64)
     with pytest.raises(ValueError):
         ops.layer_plan(2, 16, 528, 2)  # head_dim 264
     assert ops.layer_plan(2, 16, 120, 10) == ops.PLAN_PADDED

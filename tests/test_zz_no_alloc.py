@@ -17,17 +17,17 @@ from _gpu_util import DEV, build_pair, log, oracle_on
 pytestmark = pytest.mark.gpu
 
 
-def _packed(mod):
-    return mod._packed()
+def _packed(mod, dtype=torch.float16):
+    return mod._packed(dtype)
 
 
-def _run_both(mod, B, S, causal, masked, seed, resid):
+def _run_both(mod, B, S, causal, masked, seed, resid, dtype=torch.float16):
     from cobra_amd import ops
 
     D = mod.attention.d_model
     H = mod.attention.num_heads
-    p = _packed(mod)
-    x = make_input(B, S, D, seed=seed).half().to(DEV)
+    p = _packed(mod, dtype)
+    x = make_input(B, S, D, seed=seed).to(dtype).to(DEV)
     m = None
     if masked:
         m = torch.rand(B, S, generator=torch.Generator().manual_seed(seed)) < 0.8
@@ -37,8 +37,8 @@ def _run_both(mod, B, S, causal, masked, seed, resid):
     y_ws, y_na = torch.empty_like(x), torch.full_like(x, float("nan"))
     r_ws = torch.empty(B, S, D, dtype=torch.float32, device=DEV) if resid else None
     r_na = torch.full_like(r_ws, float("nan")) if resid else None
-    log(f"[noalloc] B{B} S{S} D{D} H{H} causal={causal} masked={masked} plan={ops.layer_plan(B, S, D, H, masked)} "
-        f"scratch={ws.numel()} bytes")
+    log(f"[noalloc] B{B} S{S} D{D} H{H} causal={causal} masked={masked} {dtype} "
+        f"plan={ops.layer_plan(B, S, D, H, masked, dtype)} scratch={ws.numel()} bytes")
     with torch.inference_mode():
         ops.layer_fwd(x, p.w_qkv, p.b_qkv, p.w_o, p.b_o, p.ln1_w, p.ln1_b, p.ln2_w, p.ln2_b, y_ws, ws, H, causal,
                       resid_out=r_ws, valid_mask=m)
@@ -72,6 +72,26 @@ def test_noalloc_equals_workspace_entry_point(first, second, causal, masked):
             want = oracle_on(ref, x.float().cpu(), causal, "cpu", mask=None if m is None else m.bool().cpu())
             res = compare_outputs(want, y_na.float().cpu())
             log(f"[noalloc] second call vs oracle: max_abs={res.max_abs_error:.3e} failed={res.failed_elements}")
+            assert res.passed, res
+
+
+@pytest.mark.parametrize("first,second", [((8, 256, 128, 4), (3, 100, 256, 4)), ((4, 100, 120, 4), (2, 50, 96, 8))])
+def test_noalloc_bf16(first, second):
+    """bf16 activations (the staged and padded plans with bf16 operands) through the
+    scratch: bit-equal to the workspace entry point, and within the bf16 gate (the
+    reference's scaled by bf16's unit roundoff over fp16's: abs 1.6e-2 or rel 2e-2) of the
+    oracle on the same bf16-rounded weights."""
+    for i, (B, S, D, H) in enumerate((first, second)):
+        ref, mod = build_pair(D, H, seed=i, dtype=torch.bfloat16)
+        x, m, y_ws, y_na, r_ws, r_na = _run_both(mod, B, S, True, True, seed=50 + i, resid=i == 1,
+                                                 dtype=torch.bfloat16)
+        assert torch.equal(y_ws, y_na), (B, S, D, H)
+        if i == 1:
+            assert torch.equal(r_ws, r_na), (B, S, D, H)
+            want = oracle_on(ref, x.float().cpu(), True, "cpu", mask=m.bool().cpu())
+            res = compare_outputs(want, y_na.float().cpu(), rtol=2e-2, atol=1.6e-2)
+            log(f"[noalloc] bf16 second call vs oracle: max_abs={res.max_abs_error:.3e} "
+                f"failed={res.failed_elements}")
             assert res.passed, res
 
 
