@@ -18,7 +18,8 @@ Also on the same line:
   * ``long``: BASELINE config 5, B=32 d=1024 H=16 S=100000 (``--no-long`` skips), its
     input built per sequence from seeds (``synthetic_sequence``), with its own CPU
     baseline (the query-blocked oracle on one sequence, x32 extrapolated);
-  * ``sweep``: every other BASELINE configuration, ms and TFLOP/s per forward;
+  * ``sweep``: every other BASELINE configuration, ms and TFLOP/s per forward, and three
+    shapes with bf16 activations (the staged kernels with bf16 operands);
   * ``model``: the whole ``CobraTransformer`` stack on three of the reference's
     model cases (tools/sweep.py:31-47), causal, fp16;
   * ``measured_peaks``: fp16 GEMM TFLOP/s and device-copy GB/s on this box;
@@ -77,11 +78,11 @@ def synthetic_sequence(b, S, D, seed=0):
     return torch.randn(1, S, D, generator=g, dtype=torch.float32)[0]
 
 
-def make_layer(D, H, dev, graph=None):
+def make_layer(D, H, dev, graph=None, dtype=torch.float16):
     from cobra_amd import CobraAttentionSublayer
 
     torch.manual_seed(0)
-    return CobraAttentionSublayer(D, H, graph=graph).to(device=dev, dtype=torch.float16).eval()
+    return CobraAttentionSublayer(D, H, graph=graph).to(device=dev, dtype=dtype).eval()
 
 
 def event_ms(fn, iters, stream=None):
@@ -129,7 +130,7 @@ def layer_launcher(layer, x, y):
     """The module's own kernel launch for (x -> y), allocation-free (graph-capturable)."""
     from cobra_amd import ops
 
-    p = layer._packed()
+    p = layer._packed(x.dtype)
     B, S, D = x.shape
     ws = torch.empty(ops.layer_workspace_bytes(B, S, D, layer.attention.num_heads, False, x.dtype), dtype=torch.uint8,
                      device=x.device)
@@ -283,20 +284,24 @@ def cpu_baseline_long(budget_s=20.0, block_q=2048):
                       f"(labelled extrapolation)"}
 
 
-SWEEP = [  # name, B, S, D, H  (BASELINE configs other than the headline one)
+SWEEP = [  # name, B, S, D, H[, activation dtype]  (BASELINE configs other than the headline one)
     ("b1", 1, 128, 128, 4), ("b4", 4, 128, 128, 4), ("b16", 16, 128, 128, 4), ("b128", 128, 128, 128, 4),
     ("b10000", 10000, 128, 128, 4), ("s32", 64, 32, 128, 4), ("s1024", 64, 1024, 128, 4),
     ("h1", 64, 128, 128, 1), ("h2", 64, 128, 128, 2), ("h16", 64, 128, 128, 16), ("gemm", 64, 128, 1024, 4),
+    # bf16 activations and weights (the staged kernels with bf16 operands), not a BASELINE config
+    ("base_bf16", 64, 128, 128, 4, torch.bfloat16), ("gemm_bf16", 64, 128, 1024, 4, torch.bfloat16),
+    ("s1024_bf16", 64, 1024, 128, 4, torch.bfloat16),
 ]
 
 
 def sweep(dev, only=None):
     out = {}
-    for name, B, S, D, H in SWEEP:
+    for name, B, S, D, H, *dt in SWEEP:
         if only and name not in only:
             continue
-        layer = make_layer(D, H, dev)
-        x = torch.randn(B, S, D, device=dev, dtype=torch.float16)
+        dtype = dt[0] if dt else torch.float16
+        layer = make_layer(D, H, dev, dtype=dtype)
+        x = torch.randn(B, S, D, device=dev, dtype=dtype)
         with torch.inference_mode():
             layer(x)
             iters = 20 if B * S * D < 50_000_000 else 5
@@ -306,7 +311,8 @@ def sweep(dev, only=None):
             kms = in_graph_ms(layer_launcher(layer, x, torch.empty_like(x)), n=10 if B * S < 1_000_000 else 3,
                               reps=3)
         fl = layer_flops(B, S, D)
-        out[name] = {"B": B, "S": S, "D": D, "H": H, "plan": "fused" if layer.plan == 0 else "staged",
+        out[name] = {"B": B, "S": S, "D": D, "H": H, "dtype": str(dtype).replace("torch.", ""),
+                     "plan": "fused" if layer.plan == 0 else "staged",
                      "ms_per_forward": ms, "tflops": fl / (ms / 1e3) / 1e12,
                      "kernels_ms_in_graph": kms, "tflops_in_graph": fl / (kms / 1e3) / 1e12,
                      "hbm_gbs_in_graph": layer_bytes(B, S, D) / (kms / 1e3) / 1e9}
