@@ -34,10 +34,14 @@
 //   * the Q fragments are pre-scaled by scale * log2(e) and each score tile's
 //     accumulator starts at -m (the query's running max), so the matrix cores
 //     deliver s - m in the exp2 domain and p = exp2 of the accumulator;
-//   * lazy rescale: a query's running max only moves (rescaling O and the sum)
-//     when a block raises it by more than 2^8 -- the probabilities stay below
-//     256, well inside fp16 -- and the whole wave skips the rescale when no
-//     lane needs it;
+//   * no block maximum in the common case: once a wave's queries have a
+//     running max (block 0), a block's probabilities are formed against it
+//     directly and accepted if every lane's block sum is <= 2^16 (so every
+//     probability is, well inside fp16); a block that fails the check -- a
+//     score ~10-16 above the running max -- forms its scores again and takes
+//     the max path: the running max then moves (rescaling O and the sum) only
+//     when the block raises it by more than 2^8, and the whole wave skips the
+//     rescale when no lane needs it;
 //   * the running sum adds the fp16 probabilities the P.V product consumes
 //     (v_dot2_f32_f16 against ones, fp32 accumulation), and the max/sum
 //     exchange with lane ^ 32 uses v_permlane32_swap;
@@ -84,6 +88,7 @@ __device__ __forceinline__ int swz(int row) {
 }
 
 constexpr float kLazyRescale = 8.0f;  // log2 units
+constexpr float kAcceptSum = 65536.0f;  // a lane's tile sum accepted without a block max
 
 __device__ __forceinline__ f32x16 splat16(float v) {
   f32x16 r;
@@ -307,111 +312,156 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const TQ* __restrict_
     const TQ* Vc = reinterpret_cast<const TQ*>(smem + (n % ST) * SB + TB);
     // s = scores in the exp2 domain minus the running max: the accumulator
     // starts at -m_run (every register of a lane belongs to the lane's query).
-    f32x16 s[BN / 32];
-#pragma unroll
-    for (int t = 0; t < BN / 32; ++t) {
-      s[t] = splat16(-m_run);
-      const int row = t * 32 + li;
-      const TQ* krow = Kc + row * HD;
-      const int sw = swz<HD>(row);
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const V8 a = *reinterpret_cast<const V8*>(krow + (((2 * kk + g) ^ sw) * 8));
-        s[t] = mfma32x32x16(a, qf[kk], s[t]);
-      }
-    }
-
     // Masks only where a block reaches past S, causally past this wave's first
     // query, or holds a padded key.
-    if (kb + BN > S || (CAUSAL && kb + BN > q0w + 1) || kpart) {
-      uint64_t lw[KW];  // this lane's view: bit c = key kb + 32*(word half) + 4g + c
+    const bool need_mask = kb + BN > S || (CAUSAL && kb + BN > q0w + 1) || kpart;
+    auto scores = [&](f32x16(&s)[BN / 32]) {
 #pragma unroll
-      for (int k = 0; k < KW; ++k) lw[k] = MASKED ? kw[k] >> (4 * g) : 0;
+      for (int t = 0; t < BN / 32; ++t) {
+        s[t] = splat16(-m_run);
+        const int row = t * 32 + li;
+        const TQ* kr = Kc + row * HD;
+        const int sw = swz<HD>(row);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+          const V8 a = *reinterpret_cast<const V8*>(kr + (((2 * kk + g) ^ sw) * 8));
+          s[t] = mfma32x32x16(a, qf[kk], s[t]);
+        }
+      }
+      if (need_mask) {
+        // Register r of tile t holds key kb + 4g + kc with kc = 32t + 8(r/4) + r%4,
+        // a constant: the key is past S or causally after the query iff kc > lim.
+        // A tile whose keys are all live for every lane of the wave is skipped
+        // (a uniform branch per tile, which also keeps the predicates of one tile
+        // at a time in scalar registers).
+        const int lim = CAUSAL ? min(S - 1, qi) - kb - 4 * g : S - 1 - kb - 4 * g;
+        uint64_t lw[KW];  // this lane's view: bit c = key kb + 32*(word half) + 4g + c
+#pragma unroll
+        for (int k = 0; k < KW; ++k) lw[k] = MASKED ? kw[k] >> (4 * g) : 0;
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t) {
+          const uint32_t tw = MASKED ? (uint32_t)(lw[t >> 1] >> ((t & 1) * 32)) : 0u;
+          bool part = t * 32 + 27 > lim;  // the tile's last key for this lane: kc = 32t + 27
+          if constexpr (MASKED) part = part || (tw & 0x0F0F0F0Fu) != 0x0F0F0F0Fu;
+          if (__builtin_amdgcn_ballot_w64(part)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kc = t * 32 + 8 * (r >> 2) + (r & 3);
+              bool dead = kc > lim;
+              if constexpr (MASKED) dead = dead || !((tw >> (8 * (r >> 2) + (r & 3))) & 1);
+              if (dead) s[t][r] = kNegInf;
+            }
+          }
+        }
+      }
+    };
+    // The running max moves (rescaling O and the sum, and the scores still to be
+    // exponentiated: tiles t0 ..) only when the wave's max over those scores is
+    // more than kLazyRescale above it; block 0 (or, with key masks, the first
+    // block with a valid key for the query) sets it.
+    auto rescale = [&](f32x16(&s)[BN / 32], int t0, bool first) {
+      float mx = kNegInf;
 #pragma unroll
       for (int t = 0; t < BN / 32; ++t)
+        if (t >= t0)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb + t * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          bool dead = key >= S || (CAUSAL && key > qi);
-          if constexpr (MASKED) dead = dead || !((lw[t >> 1] >> ((t & 1) * 32 + 8 * (r >> 2) + (r & 3))) & 1);
-          if (dead) s[t][r] = kNegInf;
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+      mx = max_xor32(mx);  // relative to m_run
+      if constexpr (MASKED) {
+        const bool live = mx != kNegInf;
+        if (__builtin_amdgcn_ballot_w64(started ? mx > kLazyRescale : live)) {
+          const float inc = started ? fmaxf(mx, 0.f) : (live ? mx : 0.f);
+          const float alpha = started ? __builtin_amdgcn_exp2f(-inc) : 1.f;
+          l_run *= alpha;
+#pragma unroll
+          for (int j = 0; j < ND; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+#pragma unroll
+          for (int t = 0; t < BN / 32; ++t)
+            if (t >= t0)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) s[t][r] -= inc;
+          m_run += inc;
+          started = started || live;
         }
-    }
-    float mx = kNegInf;
+      } else if (first || __builtin_amdgcn_ballot_w64(mx > kLazyRescale)) {
+        // Block 0 holds key 0, valid for every query, so its mx is finite.
+        const float inc = first ? mx : fmaxf(mx, 0.f);
+        if (!first) {
+          const float alpha = __builtin_amdgcn_exp2f(-inc);
+          l_run *= alpha;
 #pragma unroll
-    for (int t = 0; t < BN / 32; ++t)
+          for (int j = 0; j < ND; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-    mx = max_xor32(mx);  // this block's max relative to m_run
-    if constexpr (MASKED) {
-      // The first block with a valid key for the query sets its running max
-      // (until then the accumulators start at 0 and every probability is 0).
-      const bool live = mx != kNegInf;
-      if (__builtin_amdgcn_ballot_w64(started ? mx > kLazyRescale : live)) {
-        const float inc = started ? fmaxf(mx, 0.f) : (live ? mx : 0.f);
-        const float alpha = started ? __builtin_amdgcn_exp2f(-inc) : 1.f;
-        l_run *= alpha;
-#pragma unroll
-        for (int j = 0; j < ND; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+            for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+        }
 #pragma unroll
         for (int t = 0; t < BN / 32; ++t)
+          if (t >= t0)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[t][r] -= inc;
+            for (int r = 0; r < 16; ++r) s[t][r] -= inc;
         m_run += inc;
-        started = started || live;
       }
-    } else if (n == 0 || __builtin_amdgcn_ballot_w64(mx > kLazyRescale)) {
-      // Block 0 sets the running max (it holds key 0, valid for every query, so
-      // mx is finite); later blocks raise it only past the lazy threshold.
-      const float inc = n == 0 ? mx : fmaxf(mx, 0.f);
-      if (n != 0) {
-        const float alpha = __builtin_amdgcn_exp2f(-inc);
-        l_run *= alpha;
-#pragma unroll
-        for (int j = 0; j < ND; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
-      }
-#pragma unroll
-      for (int t = 0; t < BN / 32; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[t][r] -= inc;
-      m_run += inc;
-    }
+    };
 
-    V8 pf[BN / 16];
+    f32x16 s[BN / 32];
+    scores(s);
+    // Once every query of the wave has a running max, no block maximum is formed:
+    // each 32-key tile's probabilities are taken against the running max directly
+    // and accepted when every lane's tile sum is at most 2^16, so that no
+    // probability exceeds 2^16 (fp16 holds each one; an fp16 overflow reads as an
+    // infinite sum) and the fp32 sums and products stay far from overflow.  A
+    // tile that fails the check -- a score more than ~12-16 above the running
+    // max, rare after the first block -- rescales over the block's remaining
+    // tiles and is exponentiated again.  Tile by tile, the P.V products of one
+    // tile overlap the exponentials of the next.
+    const bool direct = MASKED ? !__builtin_amdgcn_ballot_w64(!started) : n != 0;
+    if (!direct) rescale(s, 0, !MASKED);
 #pragma unroll
-    for (int t = 0; t < BN / 32; ++t)
+    for (int t = 0; t < BN / 32; ++t) {
+      // p = exp2(s) rounded to the operand type, in the P.V B-operand layout (two
+      // 16-key steps), and this lane's share of the tile's row sum over those
+      // rounded values (the ones the P.V product uses), fp32 accumulation.
+      V8 pf[2];
+      float lt;
+      auto probs = [&]() {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pf[t * 2 + (r >> 3)][r & 7] = (TQ)__builtin_amdgcn_exp2f(s[t][r]);
-    // Row sum of the fp16 probabilities (the values the P.V product uses), fp32 accumulation.
+        for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = (TQ)__builtin_amdgcn_exp2f(s[t][r]);
+        lt = 0.f;
 #pragma unroll
-    for (int k = 0; k < BN / 16; ++k)
+        for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const V2 pr = {pf[k][2 * e], pf[k][2 * e + 1]};
-        l_run = dot2(pr, ones, l_run);
+          for (int e = 0; e < 4; ++e) {
+            const V2 pr = {pf[k][2 * e], pf[k][2 * e + 1]};
+            lt = dot2(pr, ones, lt);
+          }
+      };
+      probs();
+      if (direct && __builtin_amdgcn_ballot_w64(!(lt <= kAcceptSum))) {
+        rescale(s, t, false);
+        probs();
       }
-
+      l_run += lt;
 #pragma unroll
-    for (int ks = 0; ks < BN / 16; ++ks)
+      for (int kh = 0; kh < 2; ++kh) {
+        const int ks = 2 * t + kh;
 #pragma unroll
-      for (int j = 0; j < ND; ++j) {
-        V4 lo, hi;
-        if (HD >= 32 || vc < HD) {
-          const int c = j * 32 + vc;
-          const int r0 = ks * 16 + vr, r1 = r0 + 8;
-          lo = lds_read_tr16(Vc + r0 * HD + (((c >> 3) ^ swz<HD>(r0)) * 8) + (c & 7));
-          hi = lds_read_tr16(Vc + r1 * HD + (((c >> 3) ^ swz<HD>(r1)) * 8) + (c & 7));
-        } else {
-          lo = hi = V4{(TQ)0.0f, (TQ)0.0f, (TQ)0.0f, (TQ)0.0f};  // d beyond a 16-wide head
+        for (int j = 0; j < ND; ++j) {
+          V4 lo, hi;
+          if (HD >= 32 || vc < HD) {
+            const int c = j * 32 + vc;
+            const int r0 = ks * 16 + vr, r1 = r0 + 8;
+            lo = lds_read_tr16(Vc + r0 * HD + (((c >> 3) ^ swz<HD>(r0)) * 8) + (c & 7));
+            hi = lds_read_tr16(Vc + r1 * HD + (((c >> 3) ^ swz<HD>(r1)) * 8) + (c & 7));
+          } else {
+            lo = hi = V4{(TQ)0.0f, (TQ)0.0f, (TQ)0.0f, (TQ)0.0f};  // d beyond a 16-wide head
+          }
+          const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[j] = mfma32x32x16(a, pf[kh], o[j]);
         }
-        const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[j] = mfma32x32x16(a, pf[ks], o[j]);
       }
-
+    }
   }
 
   // Output through LDS: O^T quads into [BM][HD] rows, then whole 16-byte chunks per
