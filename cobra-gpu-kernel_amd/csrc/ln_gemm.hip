@@ -16,6 +16,9 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "layer_common.hpp"
+#include "lds_dma.hpp"
+
+#include <type_traits>
 
 namespace cobra {
 
@@ -41,6 +44,35 @@ __device__ __forceinline__ void load_affine8(const float* gamma, const float* be
       gv[e] = 1.f;
       bv[e] = 0.f;
     }
+  }
+}
+
+// Eight consecutive elements of a row as loaded (fp16: one 16-byte load; fp32:
+// two), converted to fp32 only when used, so that loads in flight hold half the
+// registers for fp16 rows.
+template <typename TX>
+struct RowChunk;
+template <>
+struct RowChunk<f16> {
+  f16x8 v;
+};
+template <>
+struct RowChunk<float> {
+  f32x4 lo, hi;
+};
+__device__ __forceinline__ RowChunk<f16> load_chunk(const f16* p) { return {*reinterpret_cast<const f16x8*>(p)}; }
+__device__ __forceinline__ RowChunk<float> load_chunk(const float* p) {
+  return {*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4)};
+}
+__device__ __forceinline__ void to_float8(const RowChunk<f16>& c, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)c.v[e];
+}
+__device__ __forceinline__ void to_float8(const RowChunk<float>& c, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = c.lo[e];
+    v[4 + e] = c.hi[e];
   }
 }
 
@@ -222,6 +254,19 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
     const int c = tid + i * kLgThreads;
     wr[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)(c / CPR) * K + 8 * (c % CPR));
   }
+  // The residual chunks of the row pass below, requested now so that they arrive
+  // under the products instead of after them.
+  constexpr int LPR = N / 8, RPP = kLgThreads / LPR;
+  static_assert(BM % RPP == 0, "row pass covers the block");
+  const int cl = tid % LPR;
+  RowChunk<TR> rr[BM / RPP];
+  if (resid) {
+#pragma unroll
+    for (int it = 0; it < BM / RPP; ++it) {
+      const int64_t m = m0 + it * RPP + tid / LPR;
+      rr[it] = load_chunk(resid + (m < M ? m : M - 1) * N + 8 * cl);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
     const int c = tid + i * kLgThreads, r = c / CPR;
@@ -278,22 +323,18 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
   __syncthreads();
 
   // row pass: LPR lanes per row, 8 consecutive columns per lane
-  constexpr int LPR = N / 8, RPP = kLgThreads / LPR;
-  static_assert(BM % RPP == 0, "row pass covers the block");
-  const int cl = tid % LPR;
   float gv[8], bv[8];
   load_affine8(gamma, beta, 8 * cl, gv, bv);
 #pragma unroll
-  for (int rr0 = 0; rr0 < BM; rr0 += RPP) {
-    const int row = rr0 + tid / LPR;
+  for (int it = 0; it < BM / RPP; ++it) {
+    const int row = it * RPP + tid / LPR;
     const int64_t m = m0 + row;
     const bool ok = m < M;
-    const int64_t mm = ok ? m : M - 1;
     float v[8], rv[8];
     const f32x4 c0 = *reinterpret_cast<const f32x4*>(Cs + row * LDC + 8 * cl);
     const f32x4 c1 = *reinterpret_cast<const f32x4*>(Cs + row * LDC + 8 * cl + 4);
     if (resid) {
-      load8(resid + mm * N + 8 * cl, rv);
+      to_float8(rr[it], rv);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) rv[e] = 0.f;
@@ -326,23 +367,17 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
 
 template <int K, int N, typename TR, typename TY>
 static hipError_t launch_gemm_ln_rows(const GemmArgs& a) {
-  // 128-row blocks while they still give every CU a workgroup, else the smallest
-  // block whose wave tiles are still 32 columns wide (32 rows at N = 128, 64 at 64).
+  // The smallest block whose wave tiles are still 32 columns wide (32 rows at N = 128,
+  // 64 at 64): several workgroups per CU in different phases, so that one's loads
+  // overlap another's products.  (128-row blocks -- at B64 S1024 one round of 512
+  // workgroups, all loading, then all computing -- measured 1.6 us slower there.)
   constexpr int SBM = N == 128 ? 32 : 64;
-  if (a.M >= (int64_t)128 * compute_units()) {
-    const int64_t blocks = (a.M + 127) / 128;
-    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_ln_rows_kernel<K, N, 128, TR, TY>), dim3((unsigned)blocks), dim3(kLgThreads), 0,
-                       a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
-                       static_cast<const TR*>(a.resid), static_cast<float*>(a.c), a.ln_gamma, a.ln_beta,
-                       static_cast<TY*>(a.ln_y), a.M, a.eps, a.row_mask, a.epi);
-  } else {
-    const int64_t blocks = (a.M + SBM - 1) / SBM;
-    hipLaunchKernelGGL((gemm_ln_rows_kernel<K, N, SBM, TR, TY>), dim3((unsigned)blocks), dim3(kLgThreads), 0,
-                       a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
-                       static_cast<const TR*>(a.resid), static_cast<float*>(a.c), a.ln_gamma, a.ln_beta,
-                       static_cast<TY*>(a.ln_y), a.M, a.eps, a.row_mask, a.epi);
-  }
+  const int64_t blocks = (a.M + SBM - 1) / SBM;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_ln_rows_kernel<K, N, SBM, TR, TY>), dim3((unsigned)blocks), dim3(kLgThreads), 0,
+                     a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+                     static_cast<const TR*>(a.resid), static_cast<float*>(a.c), a.ln_gamma, a.ln_beta,
+                     static_cast<TY*>(a.ln_y), a.M, a.eps, a.row_mask, a.epi);
   return hipGetLastError();
 }
 
@@ -369,8 +404,8 @@ hipError_t run_gemm_ln_rows(const GemmArgs& a) {
 // ---------------------------------------------------------------------------------------
 // Persistent form for d_model 128 and N = 128 NT columns (the QKV projection: N = 384):
 // a workgroup per CU keeps all of W in LDS and walks blocks of BM rows, so W is read
-// once per CU rather than once per tile, and the next block's rows are loaded into
-// registers while the current block's products run.  Wave w owns output columns
+// once per CU rather than once per tile, and the rows two blocks ahead are loaded into
+// registers while the current block's products and stores run.  Wave w owns output columns
 // 32 NT w .. 32 NT w + 32 NT - 1 of every block (NT x BM/32 accumulators, started
 // from the bias); the fp16 results leave as 16-byte row pieces after one exchange
 // with the partner lane.  The tile-per-workgroup kernel above serialises load,
@@ -426,60 +461,73 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
   float gv[8], bv[8];
   load_affine8(gamma, beta, 8 * cl, gv, bv);
   // Bias of this wave's columns in the accumulator layout: tile t, register r ->
-  // column 32 NT w + 32 t + 8 (r / 4) + 4 g + r % 4.
+  // column 128 t + 32 w + 8 (r / 4) + 4 g + r % 4 (tile t of the four column waves
+  // together covers the 128 columns 128 t .. 128 t + 127: q, k, v at N = 384).
   f32x16 bt[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = 32 * NT * w + 32 * t + 8 * q + 4 * g;
+      const int n = 128 * t + 32 * w + 8 * q + 4 * g;
       const f32x4 b4 = bias ? *reinterpret_cast<const f32x4*>(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) bt[t][4 * q + e] = b4[e];
     }
 
-  // Rows of block `blk` for this thread's LayerNorm slots (zeros past M).
-  float xv[PASSES][8];
-  auto load_rows = [&](int64_t blk) {
+  // Rows of block `blk` for this thread's LayerNorm slots, as loaded.  Two register
+  // slots: the rows of block n + 2 are requested while block n's products and stores
+  // run, so a block's loads have two blocks' time to land.  Rows past M (and blocks
+  // past the last) load row M - 1, never stored: a load on every path, so that the
+  // compiler's wait for a slot counts only the memory operations issued after it
+  // (a zero fill on some paths made it wait for every store at the loop head).
+  RowChunk<TX> xr[2][PASSES];
+  auto load_rows = [&](RowChunk<TX>(&dst)[PASSES], int64_t blk) {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int64_t row = blk * BM + RPP * p + rp;
-      if (blk < nblk && row < M) {
-        load8(x + row * D + 8 * cl, xv[p]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[p][e] = 0.f;
-      }
+      dst[p] = load_chunk(x + (row < M ? row : M - 1) * D + 8 * cl);
     }
   };
-  load_rows(blockIdx.x);
-  int buf = 0;
-  for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x, buf ^= 1) {
-    char* const H = Hs + buf * BM * ROWB;
+  const int64_t G = gridDim.x;
+  load_rows(xr[0], blockIdx.x);
+  asm volatile("" ::: "memory");
+  load_rows(xr[1], blockIdx.x + G);
+  // Slot 0 landed before the loop: the loop head's wait then only has to cover the
+  // back edge, where slot 0's loads are followed by a whole block's stores and
+  // slot 1's loads (otherwise the compiler's wait there, sized for this entry
+  // path, drains most of the previous block's stores every second block).
+  wait_vmcnt<PASSES * (int)(sizeof(RowChunk<TX>) / 16)>();
+
+  // One block: LayerNorm of its rows (from slot S) into H buffer S, products, stores.
+  auto block = [&](auto slot, int64_t blk) {
+    constexpr int S = decltype(slot)::value;
+    char* const H = Hs + S * BM * ROWB;
     // ---- LayerNorm of the block's rows into H ----------------------------------------
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
+      float xv[8];
+      to_float8(xr[S][p], xv);
       float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += xv[p][e];
+      for (int e = 0; e < 8; ++e) s += xv[e];
       const float mean = group_sum<CPR>(s) * (1.0f / D);
       float q = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float t = xv[p][e] - mean;
+        const float t = xv[e] - mean;
         q += t * t;
       }
       const float rstd = rsqrtf(group_sum<CPR>(q) * (1.0f / D) + eps);
       f16x8 h;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[p][e] - mean) * rstd * gv[e] + bv[e]);
+      for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[e] - mean) * rstd * gv[e] + bv[e]);
       const int r = RPP * p + rp;
       *reinterpret_cast<f16x8*>(H + r * ROWB + 16 * (cl ^ (r & 15))) = h;
     }
     // One barrier per block: H of this block is complete, and (double buffering)
     // every wave finished the previous block's reads of the other buffer.
     __syncthreads();
-    load_rows(blk + gridDim.x);
+    load_rows(xr[S], blk + 2 * G);
 
     // ---- products: NT column tiles x RT row tiles per wave ----------------------------
     f32x16 acc[NT][RT];
@@ -487,7 +535,7 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int i = 0; i < RT; ++i) acc[t][i] = bt[t];
-    const int sw = li & 15;  // rows 32i + li and 32 NT w + 32t + li share this swizzle
+    const int sw = li & 15;  // rows 32i + li and 128t + 32w + li share this swizzle
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
       const int co = 16 * ((2 * kk + g) ^ sw);
@@ -496,36 +544,54 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
       for (int i = 0; i < RT; ++i) hf[i] = *reinterpret_cast<const f16x8*>(H + (32 * (RT * rg + i) + li) * ROWB + co);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        wf[t] = *reinterpret_cast<const f16x8*>(Ws + (32 * NT * w + 32 * t + li) * ROWB + co);
+        wf[t] = *reinterpret_cast<const f16x8*>(Ws + (128 * t + 32 * w + li) * ROWB + co);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int i = 0; i < RT; ++i) acc[t][i] = mfma32x32x16(wf[t], hf[i], acc[t][i]);
     }
 
-    // ---- fp16 out: lane (li, g) of tile (t, i) holds row 32i + li, columns
-    // 32 NT w + 32t + 8q + 4g + {0..3}; pairs of quads become 16-byte pieces.  (Staging
-    // the block through LDS for whole-row stores measured no faster: the kernel is
-    // bound by how few writes one workgroup per CU keeps in flight, not their shape.)
+    // ---- fp16 out through LDS, one 128-column slab (tile t of every wave) at a time:
+    // the slab's BM rows x 256 bytes go to an H buffer (chunk c of row r at c ^ (r & 15)),
+    // then leave as whole 256-byte row segments, 16 lanes per row.  Written straight
+    // from the accumulator layout, every store instruction would touch 32 rows with
+    // 32 bytes each, which ran the projection at ~1/3 of the copy rate.  Slabs 0 and 2
+    // use this block's H buffer, slab 1 the other one (free: the previous block is
+    // done with it, and the next block's LayerNorm into it comes after slab 2's barrier).
+    __syncthreads();  // every wave is done reading H for the products
 #pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      const int64_t m = blk * BM + 32 * (RT * rg + i) + li;
+    for (int t = 0; t < NT; ++t) {
+      char* const O = Hs + ((S + t) & 1) * BM * ROWB;
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+      for (int i = 0; i < RT; ++i) {
+        const int r = 32 * (RT * rg + i) + li;
 #pragma unroll
-        for (int pr = 0; pr < 2; ++pr) {
-          f16x4 h0, h1;
+        for (int q = 0; q < 4; ++q) {
+          f16x4 h;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            h0[e] = (f16)acc[t][i][8 * pr + e];
-            h1[e] = (f16)acc[t][i][8 * pr + 4 + e];
-          }
-          swap_halves(h0, h1);  // g = 0: both lanes' quad 2pr; g = 1: both lanes' quad 2pr + 1
-          if (m < M)
-            *reinterpret_cast<f16x8*>(C + m * N + 32 * NT * w + 32 * t + 16 * pr + 8 * g) =
-                f16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+          for (int e = 0; e < 4; ++e) h[e] = (f16)acc[t][i][4 * q + e];
+          *reinterpret_cast<f16x4*>(O + r * ROWB + 16 * ((4 * w + q) ^ (r & 15)) + 8 * g) = h;
         }
+      }
+      __syncthreads();
+      // Rows past M hold row M - 1's x, hence row M - 1's output: they store it there
+      // again (unconditional stores keep the compiler's memory waits exact).
+#pragma unroll
+      for (int k = 0; k < BM * CPR / THREADS; ++k) {
+        const int idx = tid + THREADS * k, r = idx / CPR, c = idx % CPR;
+        const int64_t m = blk * BM + r;
+        *reinterpret_cast<f16x8*>(C + (m < M ? m : M - 1) * N + 128 * t + 8 * c) =
+            *reinterpret_cast<const f16x8*>(O + r * ROWB + 16 * (c ^ (r & 15)));
+      }
+      // No barrier here: slab t + 1 goes to the other buffer, and slab t + 2, which
+      // reuses this one, is written after the barrier that follows slab t + 1's
+      // writes, which every wave reaches only after its reads of slab t.
     }
+  };
+  for (int64_t blk = blockIdx.x; blk < nblk; blk += 2 * G) {
+    block(std::integral_constant<int, 0>{}, blk);
+    if (blk + G >= nblk) break;
+    block(std::integral_constant<int, 1>{}, blk + G);
   }
 }
 
