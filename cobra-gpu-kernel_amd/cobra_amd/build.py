@@ -45,10 +45,11 @@ DEVICE_FLAGS = [
 # Per-file backend options.  The attention kernels keep MFMA results in VGPRs:
 # their accumulators feed VALU softmax / rescale / LayerNorm work directly, and
 # the default AGPR form adds an accumulator copy per use (~900 instructions in
-# the fused sublayer kernel, ~160 per key block in flash attention).
+# the fused sublayer kernel, ~160 per key block in flash attention).  The fused
+# sublayer kernel's first eight (scalar) arguments are preloaded into SGPRs.
 FILE_FLAGS = {
     "layer_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-    "layer_split.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "layer_split.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=8"],
     "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 

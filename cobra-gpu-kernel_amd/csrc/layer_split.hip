@@ -177,15 +177,24 @@ struct SplitKArgs<true> : SplitArgs {
 };
 
 // AFF1: LN1 with an elementwise affine (g1 / be1 non-null; never in whole-block mode).
+//
+// The first eight arguments repeat fields of `ka` as scalars: the ones the first
+// transfers need.  Built with -amdgpu-kernarg-preload-count, they arrive in SGPRs
+// when the wave starts (gfx950 kernel-argument preloading), so the token tile and the
+// parameter segments are requested without waiting for the kernel-argument loads;
+// the rest of `ka` loads meanwhile.
 template <int D, int HD, bool CAUSAL, bool MASKED, bool BLK, bool AFF1>
-__global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(const SplitKArgs<BLK> ka) {
-  const int S = ka.S, nblk = ka.nblk;
-  const f16* __restrict__ x = ka.x;
-  const f16* __restrict__ wqkv = ka.wqkv;
-  const float* __restrict__ bqkv = ka.bqkv;
-  const float* __restrict__ bo = ka.bo;
-  const float* __restrict__ g2 = ka.g2;
-  const float* __restrict__ be2 = ka.be2;
+__global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(int S_, int nblk_, const f16* x_, const f16* wqkv_,
+                                                                     const float* bqkv_, const float* bo_,
+                                                                     const float* g2_, const float* be2_,
+                                                                     const SplitKArgs<BLK> ka) {
+  const int S = S_, nblk = nblk_;
+  const f16* __restrict__ x = x_;
+  const f16* __restrict__ wqkv = wqkv_;
+  const float* __restrict__ bqkv = bqkv_;
+  const float* __restrict__ bo = bo_;
+  const float* __restrict__ g2 = g2_;
+  const float* __restrict__ be2 = be2_;
   const f16* __restrict__ wo = ka.wo;
   const float* __restrict__ g1 = ka.g1;
   const float* __restrict__ be1 = ka.be1;
@@ -1092,7 +1101,7 @@ hipError_t launch_layer_split(const SplitLaunch& l, const void* x, const uint8_t
   k.vmask = valid_mask;
   k.y = y;
   k.resid_out = resid_out;
-  void* args[] = {&k};
+  void* args[] = {&k.S, &k.nblk, &k.x, &k.wqkv, &k.bqkv, &k.bo, &k.g2, &k.be2, &k};
   return hipLaunchKernel(l.fn[valid_mask ? 1 : 0], dim3(l.grid), dim3(l.block), args, 0, stream);
 }
 
@@ -1125,7 +1134,8 @@ static hipError_t launch_block(const BlockArgs& a, float c2) {
                      a.lnn_b, a.out_dtype == kF32, a.mask_out};
   auto kern = a.valid_mask ? layer_split_kernel<128, HD, CAUSAL, true, true, false>
                            : layer_split_kernel<128, HD, CAUSAL, false, true, false>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, k);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kSplitWaves), 0, a.stream, k.S, k.nblk, k.x, k.wqkv,
+                     k.bqkv, k.bo, k.g2, k.be2, k);
   return hipGetLastError();
 }
 
