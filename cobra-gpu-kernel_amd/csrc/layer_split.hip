@@ -229,9 +229,11 @@ __global__ __launch_bounds__(64 * kSplitWaves) void layer_split_kernel(int S_, i
 
   // The S/32 slices of a sequence run on one XCD, so its L2 serves the token
   // tiles they all read.
-  const int NS = (S + 31) >> 5;  // query slices per sequence
+  const int NS = (S + 31) >> 5;  // query slices per sequence: 1-4 (S <= 128)
   const int item = xcd_remap(blockIdx.x, nblk);
-  const int b = item / NS;
+  // item / NS by a shift or, for 3, a multiply (exact for every 32-bit item): the
+  // division's reciprocal sequence sat on the path to the first transfer.
+  const int b = NS == 3 ? (int)(((uint64_t)(uint32_t)item * 0xAAAAAAABull) >> 33) : item >> (NS >> 1);
   const int s = item - b * NS;  // query slice
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
