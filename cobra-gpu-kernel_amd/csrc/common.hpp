@@ -177,6 +177,44 @@ __device__ __forceinline__ void load8(const bf16* p, float (&v)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = (float)h[i];
 }
+// Eight consecutive elements of a row as loaded (fp16: one 16-byte load; fp32:
+// two), converted to fp32 only when used, so that loads in flight hold half the
+// registers for fp16 rows.
+template <typename TX>
+struct RowChunk;
+template <>
+struct RowChunk<f16> {
+  f16x8 v;
+};
+template <>
+struct RowChunk<float> {
+  f32x4 lo, hi;
+};
+template <>
+struct RowChunk<bf16> {
+  bf16x8 v;
+};
+__device__ __forceinline__ RowChunk<f16> load_chunk(const f16* p) { return {*reinterpret_cast<const f16x8*>(p)}; }
+__device__ __forceinline__ RowChunk<float> load_chunk(const float* p) {
+  return {*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4)};
+}
+__device__ __forceinline__ RowChunk<bf16> load_chunk(const bf16* p) { return {*reinterpret_cast<const bf16x8*>(p)}; }
+__device__ __forceinline__ void to_float8(const RowChunk<bf16>& c, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)c.v[e];
+}
+__device__ __forceinline__ void to_float8(const RowChunk<f16>& c, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)c.v[e];
+}
+__device__ __forceinline__ void to_float8(const RowChunk<float>& c, float (&v)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = c.lo[e];
+    v[4 + e] = c.hi[e];
+  }
+}
+
 __device__ __forceinline__ void store8(f16* p, const float (&v)[8]) {
   f16x8 h;
 #pragma unroll

@@ -47,35 +47,6 @@ __device__ __forceinline__ void load_affine8(const float* gamma, const float* be
   }
 }
 
-// Eight consecutive elements of a row as loaded (fp16: one 16-byte load; fp32:
-// two), converted to fp32 only when used, so that loads in flight hold half the
-// registers for fp16 rows.
-template <typename TX>
-struct RowChunk;
-template <>
-struct RowChunk<f16> {
-  f16x8 v;
-};
-template <>
-struct RowChunk<float> {
-  f32x4 lo, hi;
-};
-__device__ __forceinline__ RowChunk<f16> load_chunk(const f16* p) { return {*reinterpret_cast<const f16x8*>(p)}; }
-__device__ __forceinline__ RowChunk<float> load_chunk(const float* p) {
-  return {*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4)};
-}
-__device__ __forceinline__ void to_float8(const RowChunk<f16>& c, float (&v)[8]) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = (float)c.v[e];
-}
-__device__ __forceinline__ void to_float8(const RowChunk<float>& c, float (&v)[8]) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    v[e] = c.lo[e];
-    v[4 + e] = c.hi[e];
-  }
-}
-
 }  // namespace
 
 template <int D, typename TX>
