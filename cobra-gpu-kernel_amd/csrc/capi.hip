@@ -208,12 +208,22 @@ int layer_fwd_bf16(const void* x, const uint8_t* valid_mask, const void* w_qkv, 
   uint64_t* bits = masked ? reinterpret_cast<uint64_t*>(ws + lb.bits_off) : nullptr;
   hipError_t e = hipSuccess;
   if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
-  cobra::LnArgs ln1{x, kBF16, nullptr, 0, ln1_w, ln1_b, nullptr, h, kBF16, T, (int)D, eps, s};
-  if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
-  cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kBF16, qkv, kBF16, T, (int)(3 * D), (int)D,
-                       nullptr, nullptr, nullptr, kF16, eps, s};
-  proj.ab_dtype = kBF16;
-  if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
+  // d_model 64 / 128: LN1 in the QKV projection's prologue and LN2 in the out-projection's
+  // epilogue, as for fp16 (three launches); otherwise LN1 -> projection -> attention ->
+  // out-projection (r in fp32) -> LN2.
+  const bool fused_ln = cobra::ln_gemm_ok(D, kBF16, kBF16);
+  if (fused_ln) {
+    cobra::LnGemmArgs proj{x, kBF16, ln1_w, ln1_b, w_qkv, b_qkv, qkv, T, (int)(3 * D), D, eps, s};
+    proj.ab_dtype = kBF16;
+    if ((e = cobra::run_ln_gemm(proj)) != hipSuccess) return code(e);
+  } else {
+    cobra::LnArgs ln1{x, kBF16, nullptr, 0, ln1_w, ln1_b, nullptr, h, kBF16, T, (int)D, eps, s};
+    if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
+    cobra::GemmArgs proj{h, w_qkv, b_qkv, nullptr, kBF16, qkv, kBF16, T, (int)(3 * D), (int)D,
+                         nullptr, nullptr, nullptr, kF16, eps, s};
+    proj.ab_dtype = kBF16;
+    if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
+  }
   const int64_t hd = D / H;
   cobra::AttnArgs at{qkv, ctx, batch, (int)seq_len, (int)H, (int)hd, (float)(1.0 / sqrt((double)hd)),
                      causal ? 1 : 0, s};
@@ -221,6 +231,14 @@ int layer_fwd_bf16(const void* x, const uint8_t* valid_mask, const void* w_qkv, 
   at.dtype = kBF16;
   if ((e = cobra::run_attn(at)) != hipSuccess) return code(e);
   // Padded query rows: the attention output is zeroed before the residual add (TTB:121-122).
+  if (fused_ln) {
+    cobra::GemmArgs out{ctx, w_o, b_o, x, kBF16, resid_out, kF32, T, (int)D, (int)D,
+                        ln2_w, ln2_b, y, kBF16, eps, s};
+    out.ab_dtype = kBF16;
+    out.row_mask = valid_mask;
+    out.epi = masked ? cobra::kEpiMaskBranch : 0;
+    return code(cobra::run_gemm(out));
+  }
   float* r = resid_out ? resid_out : static_cast<float*>(qkv);
   cobra::GemmArgs out{ctx, w_o, b_o, x, kBF16, r, kF32, T, (int)D, (int)D, nullptr, nullptr, nullptr, kF16, eps, s};
   out.ab_dtype = kBF16;

@@ -259,7 +259,8 @@ static hipError_t dispatch_plain(const GemmArgs& a) {
 
 // bf16 operands: plain epilogue, residual bf16 or fp32, output bf16 or fp32.
 static hipError_t run_gemm_bf16(const GemmArgs& a) {
-  if (a.ln_gamma || !a.c) return hipErrorInvalidValue;
+  if (a.ln_gamma) return gemm_ln_rows_ok(a) ? run_gemm_ln_rows(a) : hipErrorInvalidValue;  // K, N in {64, 128}
+  if (!a.c) return hipErrorInvalidValue;
   const bool rb = !a.resid || a.resid_dtype == kBF16;
   if (!rb && a.resid_dtype != kF32) return hipErrorInvalidValue;
   if (a.c_dtype != kBF16 && a.c_dtype != kF32) return hipErrorInvalidValue;

@@ -77,8 +77,8 @@ struct GemmArgs {
   hipStream_t stream;
   const uint8_t* row_mask = nullptr;  // [M] when a kEpiMask* flag is set
   int epi = 0;             // kEpi* flags
-  // Operand type of a and w: kF16, or kBF16 (then resid and c are kBF16 or kF32 and
-  // there is no LayerNorm epilogue).
+  // Operand type of a and w: kF16, or kBF16 (then resid, c and ln_y are kBF16 or kF32,
+  // and the LayerNorm epilogue is the K, N in {64, 128} kernel's only).
   int ab_dtype = 0;  // kF16
 };
 // Compute units of the current device (cached after the first call).
@@ -108,16 +108,17 @@ struct LnGemmArgs {
   int x_dtype;
   const float* gamma;      // [d]
   const float* beta;       // [d]
-  const void* w;           // [N, d] fp16
+  const void* w;           // [N, d], ab_dtype
   const float* bias;       // optional [N]
-  void* c;                 // [M, N] fp16
+  void* c;                 // [M, N], ab_dtype
   int64_t M;
   int N;
   int64_t d;
   float eps;
   hipStream_t stream;
+  int ab_dtype = 0;        // operands and output: kF16, or kBF16 (x then bf16 or fp32)
 };
-bool ln_gemm_ok(int64_t d, int x_dtype);
+bool ln_gemm_ok(int64_t d, int x_dtype, int ab_dtype = 0);
 hipError_t run_ln_gemm(const LnGemmArgs& a);
 // LayerNorm epilogue for K = 64 / 128 and N = 64 / 128 (ln_gemm.hip); run_gemm
 // routes eligible calls there.

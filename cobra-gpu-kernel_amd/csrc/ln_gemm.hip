@@ -49,11 +49,13 @@ __device__ __forceinline__ void load_affine8(const float* gamma, const float* be
 
 }  // namespace
 
-template <int D, typename TX>
+template <int D, typename TX, typename TA>
 __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restrict__ x, const float* __restrict__ gamma,
-                                                           const float* __restrict__ beta, const f16* __restrict__ W,
-                                                           const float* __restrict__ bias, f16* __restrict__ C,
+                                                           const float* __restrict__ beta, const TA* __restrict__ W,
+                                                           const float* __restrict__ bias, TA* __restrict__ C,
                                                            int64_t M, int N, float eps) {
+  using V8 = typename Op16<TA>::V8;
+  using V4 = typename Op16<TA>::V4;
   static_assert(D == 64 || D == 128, "one k-tile per row");
   constexpr int ROWB = D * 2;               // bytes of one fp16 row
   constexpr int CPR = D / 8;                // 16-byte chunks per row (= lanes per row in the LN)
@@ -78,12 +80,12 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
   const int li = lane & 31, g = lane >> 5;
 
   // ---- loads: the W tile (rows past N repeat row N-1; never stored) and x rows ------
-  f16x8 wr[WCH];
+  V8 wr[WCH];
 #pragma unroll
   for (int i = 0; i < WCH; ++i) {
     const int c = tid + i * kLgThreads;
     const int r = c / CPR, ch = c % CPR;
-    wr[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)min(n0 + r, N - 1) * D + 8 * ch);
+    wr[i] = *reinterpret_cast<const V8*>(W + (int64_t)min(n0 + r, N - 1) * D + 8 * ch);
   }
   const int cl = lane % CPR;  // this lane's 8 columns: 8cl .. 8cl+7
   float xv[PASSES][8];
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
   for (int i = 0; i < WCH; ++i) {
     const int c = tid + i * kLgThreads;
     const int r = c / CPR, ch = c % CPR;
-    *reinterpret_cast<f16x8*>(Ws + r * ROWB + 16 * (ch ^ lg_swz<D>(r))) = wr[i];
+    *reinterpret_cast<V8*>(Ws + r * ROWB + 16 * (ch ^ lg_swz<D>(r))) = wr[i];
   }
   // ---- LayerNorm of every row into the h tile ---------------------------------------
 #pragma unroll
@@ -115,10 +117,10 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
       q += t * t;
     }
     const float rstd = rsqrtf(group_sum<CPR>(q) * (1.0f / D) + eps);
-    f16x8 h;
+    V8 h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[p][e] - mean) * rstd * gv[e] + bv[e]);
-    *reinterpret_cast<f16x8*>(Hs + r * ROWB + 16 * (cl ^ lg_swz<D>(r))) = h;
+    for (int e = 0; e < 8; ++e) h[e] = (TA)((xv[p][e] - mean) * rstd * gv[e] + bv[e]);
+    *reinterpret_cast<V8*>(Hs + r * ROWB + 16 * (cl ^ lg_swz<D>(r))) = h;
   }
   __syncthreads();
 
@@ -133,11 +135,11 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
     const int co = 16 * ((2 * kk + g) ^ sw);
-    f16x8 af[2], wf[2];
+    V8 af[2], wf[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const f16x8*>(Hs + (64 * wm + 32 * i + li) * ROWB + co);
+    for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const V8*>(Hs + (64 * wm + 32 * i + li) * ROWB + co);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) wf[j] = *reinterpret_cast<const f16x8*>(Ws + (64 * wn + 32 * j + li) * ROWB + co);
+    for (int j = 0; j < 2; ++j) wf[j] = *reinterpret_cast<const V8*>(Ws + (64 * wn + 32 * j + li) * ROWB + co);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -158,10 +160,10 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int row = 64 * wm + 32 * i + li;
-        f16x4 o;
+        V4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (f16)(acc[j][i][4 * q + e] + bq[e]);
-        *reinterpret_cast<f16x4*>(smem + row * OUTB + 16 * ((col >> 3) ^ (row & 15)) + 8 * g) = o;
+        for (int e = 0; e < 4; ++e) o[e] = (TA)(acc[j][i][4 * q + e] + bq[e]);
+        *reinterpret_cast<V4*>(smem + row * OUTB + 16 * ((col >> 3) ^ (row & 15)) + 8 * g) = o;
       }
     }
   __syncthreads();
@@ -173,8 +175,7 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
     const int64_t m = m0 + row;
     const int n = n0 + 8 * c;
     if (m < M && n < N)  // N % 8 == 0: a chunk is all in or all out
-      *reinterpret_cast<f16x8*>(C + m * N + n) =
-          *reinterpret_cast<const f16x8*>(smem + row * OUTB + 16 * (c ^ (row & 15)));
+      *reinterpret_cast<V8*>(C + m * N + n) = *reinterpret_cast<const V8*>(smem + row * OUTB + 16 * (c ^ (row & 15)));
   }
 }
 
@@ -188,11 +189,12 @@ __global__ __launch_bounds__(kLgThreads) void ln_gemm_kernel(const TX* __restric
 // writes r and y as whole row segments.  Replaces _gemm_ln_kernel / _tl_linear_ln
 // (TTB:394-488) for these shapes; its k loop and per-element residual loads are
 // what the register-staged GEMM's LayerNorm epilogue spends its time on.
-template <int K, int N, int BM, typename TR, typename TY>
+template <int K, int N, int BM, typename TR, typename TY, typename TA>
 __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
-    const f16* __restrict__ A, const f16* __restrict__ W, const float* __restrict__ bias, const TR* __restrict__ resid,
+    const TA* __restrict__ A, const TA* __restrict__ W, const float* __restrict__ bias, const TR* __restrict__ resid,
     float* __restrict__ resid_out, const float* __restrict__ gamma, const float* __restrict__ beta, TY* __restrict__ Y,
     int64_t M, float eps, const uint8_t* __restrict__ row_mask, int epi) {
+  using V8 = typename Op16<TA>::V8;
   static_assert((K == 64 || K == 128) && (N == 64 || N == 128), "one k-tile, whole rows");
   constexpr int ROWB = K * 2;
   constexpr int CPR = K / 8;
@@ -214,16 +216,16 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
   const int lane = tid & 63, w = tid >> 6;
   const int li = lane & 31, g = lane >> 5;
 
-  f16x8 ar[ACH], wr[WCH];
+  V8 ar[ACH], wr[WCH];
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
     const int c = tid + i * kLgThreads;
-    ar[i] = *reinterpret_cast<const f16x8*>(A + min(m0 + c / CPR, M - 1) * K + 8 * (c % CPR));
+    ar[i] = *reinterpret_cast<const V8*>(A + min(m0 + c / CPR, M - 1) * K + 8 * (c % CPR));
   }
 #pragma unroll
   for (int i = 0; i < WCH; ++i) {
     const int c = tid + i * kLgThreads;
-    wr[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)(c / CPR) * K + 8 * (c % CPR));
+    wr[i] = *reinterpret_cast<const V8*>(W + (int64_t)(c / CPR) * K + 8 * (c % CPR));
   }
   // The residual chunks of the row pass below, requested now so that they arrive
   // under the products instead of after them.
@@ -241,12 +243,12 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
     const int c = tid + i * kLgThreads, r = c / CPR;
-    *reinterpret_cast<f16x8*>(As + r * ROWB + 16 * ((c % CPR) ^ lg_swz<K>(r))) = ar[i];
+    *reinterpret_cast<V8*>(As + r * ROWB + 16 * ((c % CPR) ^ lg_swz<K>(r))) = ar[i];
   }
 #pragma unroll
   for (int i = 0; i < WCH; ++i) {
     const int c = tid + i * kLgThreads, r = c / CPR;
-    *reinterpret_cast<f16x8*>(Ws + r * ROWB + 16 * ((c % CPR) ^ lg_swz<K>(r))) = wr[i];
+    *reinterpret_cast<V8*>(Ws + r * ROWB + 16 * ((c % CPR) ^ lg_swz<K>(r))) = wr[i];
   }
   __syncthreads();
 
@@ -260,11 +262,11 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
 #pragma unroll
   for (int kk = 0; kk < K / 16; ++kk) {
     const int co = 16 * ((2 * kk + g) ^ sw);
-    f16x8 af[TM], wf[TN];
+    V8 af[TM], wf[TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f16x8*>(As + (wm * WTM + 32 * i + li) * ROWB + co);
+    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const V8*>(As + (wm * WTM + 32 * i + li) * ROWB + co);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) wf[j] = *reinterpret_cast<const f16x8*>(Ws + (wn * WTN + 32 * j + li) * ROWB + co);
+    for (int j = 0; j < TN; ++j) wf[j] = *reinterpret_cast<const V8*>(Ws + (wn * WTN + 32 * j + li) * ROWB + co);
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -336,7 +338,7 @@ __global__ __launch_bounds__(kLgThreads) void gemm_ln_rows_kernel(
   }
 }
 
-template <int K, int N, typename TR, typename TY>
+template <int K, int N, typename TR, typename TY, typename TA>
 static hipError_t launch_gemm_ln_rows(const GemmArgs& a) {
   // The smallest block whose wave tiles are still 32 columns wide (32 rows at N = 128,
   // 64 at 64): several workgroups per CU in different phases, so that one's loads
@@ -345,31 +347,40 @@ static hipError_t launch_gemm_ln_rows(const GemmArgs& a) {
   constexpr int SBM = N == 128 ? 32 : 64;
   const int64_t blocks = (a.M + SBM - 1) / SBM;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_ln_rows_kernel<K, N, SBM, TR, TY>), dim3((unsigned)blocks), dim3(kLgThreads), 0,
-                     a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+  hipLaunchKernelGGL((gemm_ln_rows_kernel<K, N, SBM, TR, TY, TA>), dim3((unsigned)blocks), dim3(kLgThreads), 0,
+                     a.stream, static_cast<const TA*>(a.a), static_cast<const TA*>(a.w), a.bias,
                      static_cast<const TR*>(a.resid), static_cast<float*>(a.c), a.ln_gamma, a.ln_beta,
                      static_cast<TY*>(a.ln_y), a.M, a.eps, a.row_mask, a.epi);
   return hipGetLastError();
 }
 
-template <typename TR, typename TY>
+template <typename TR, typename TY, typename TA>
 static hipError_t gemm_ln_rows_shape(const GemmArgs& a) {
-  if (a.K == 128) return a.N == 128 ? launch_gemm_ln_rows<128, 128, TR, TY>(a) : launch_gemm_ln_rows<128, 64, TR, TY>(a);
-  return a.N == 128 ? launch_gemm_ln_rows<64, 128, TR, TY>(a) : launch_gemm_ln_rows<64, 64, TR, TY>(a);
+  if (a.K == 128)
+    return a.N == 128 ? launch_gemm_ln_rows<128, 128, TR, TY, TA>(a) : launch_gemm_ln_rows<128, 64, TR, TY, TA>(a);
+  return a.N == 128 ? launch_gemm_ln_rows<64, 128, TR, TY, TA>(a) : launch_gemm_ln_rows<64, 64, TR, TY, TA>(a);
 }
 
+// Operands fp16 or bf16; y and the residual in the operand type or fp32.
 bool gemm_ln_rows_ok(const GemmArgs& a) {
+  const int op = a.ab_dtype;
   return a.ln_gamma && a.ln_beta && a.ln_y && (a.K == 64 || a.K == 128) && (a.N == 64 || a.N == 128) &&
-         !(a.epi & kEpiGelu) && (!a.c || a.c_dtype == kF32) && (a.ln_y_dtype == kF16 || a.ln_y_dtype == kF32) &&
-         a.ab_dtype == kF16;
+         !(a.epi & kEpiGelu) && (!a.c || a.c_dtype == kF32) && (op == kF16 || op == kBF16) &&
+         (a.ln_y_dtype == op || a.ln_y_dtype == kF32) && (!a.resid || a.resid_dtype == op || a.resid_dtype == kF32);
+}
+
+template <typename TA>
+static hipError_t gemm_ln_rows_typed(const GemmArgs& a) {
+  const bool y16 = a.ln_y_dtype != kF32;
+  if (!a.resid || a.resid_dtype == kF32)
+    return y16 ? gemm_ln_rows_shape<float, TA, TA>(a) : gemm_ln_rows_shape<float, float, TA>(a);
+  return y16 ? gemm_ln_rows_shape<TA, TA, TA>(a) : gemm_ln_rows_shape<TA, float, TA>(a);
 }
 
 hipError_t run_gemm_ln_rows(const GemmArgs& a) {
   if (!gemm_ln_rows_ok(a)) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;
-  const bool y16 = a.ln_y_dtype == kF16;
-  if (!a.resid || a.resid_dtype == kF32) return y16 ? gemm_ln_rows_shape<float, f16>(a) : gemm_ln_rows_shape<float, float>(a);
-  return y16 ? gemm_ln_rows_shape<f16, f16>(a) : gemm_ln_rows_shape<f16, float>(a);
+  return a.ab_dtype == kBF16 ? gemm_ln_rows_typed<bf16>(a) : gemm_ln_rows_typed<f16>(a);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -377,20 +388,22 @@ hipError_t run_gemm_ln_rows(const GemmArgs& a) {
 // a workgroup per CU keeps all of W in LDS and walks blocks of BM rows, so W is read
 // once per CU rather than once per tile, and the rows two blocks ahead are loaded into
 // registers while the current block's products and stores run.  Wave w owns output columns
-// 32 NT w .. 32 NT w + 32 NT - 1 of every block (NT x BM/32 accumulators, started
-// from the bias); the fp16 results leave as 16-byte row pieces after one exchange
-// with the partner lane.  The tile-per-workgroup kernel above serialises load,
-// LayerNorm, products and stores inside each workgroup, two per CU.
+// 128 t + 32 w .. + 31 (t < NT) of every block (NT x BM/32 accumulators, started from the
+// bias); the results leave through LDS as whole row segments.  The tile-per-workgroup
+// kernel above serialises load, LayerNorm, products and stores inside each workgroup,
+// two per CU.  Operands (normalised rows, W, output) fp16 or bf16 (TA).
 //
 // NWV waves: with 8, waves w and w + 4 own the same columns and split the block's
 // row tiles, so twice the loads and stores are in flight per CU (all of W in LDS
 // leaves room for one workgroup per CU, and the kernel is bound by how many
 // memory operations that workgroup keeps outstanding).
-template <int NT, int BM, int NWV, typename TX>
+template <int NT, int BM, int NWV, typename TX, typename TA>
 __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restrict__ x, const float* __restrict__ gamma,
-                                                           const float* __restrict__ beta, const f16* __restrict__ W,
-                                                           const float* __restrict__ bias, f16* __restrict__ C,
+                                                           const float* __restrict__ beta, const TA* __restrict__ W,
+                                                           const float* __restrict__ bias, TA* __restrict__ C,
                                                            int64_t M, float eps) {
+  using V8 = typename Op16<TA>::V8;
+  using V4 = typename Op16<TA>::V4;
   constexpr int D = 128, ROWB = 2 * D, CPR = D / 8;  // 16 chunks of 16 bytes per row
   constexpr int N = 128 * NT;
   constexpr int THREADS = 64 * NWV;
@@ -417,16 +430,16 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
   // W rows, swizzled: chunk c of row r at c ^ (r & 15).
 #pragma unroll
   for (int b0 = 0; b0 < WCH; b0 += SG) {
-    f16x8 v[SG];
+    V8 v[SG];
 #pragma unroll
     for (int i = 0; i < SG; ++i) {
       const int c = tid + THREADS * (b0 + i);
-      v[i] = *reinterpret_cast<const f16x8*>(W + (int64_t)(c / CPR) * D + 8 * (c % CPR));
+      v[i] = *reinterpret_cast<const V8*>(W + (int64_t)(c / CPR) * D + 8 * (c % CPR));
     }
 #pragma unroll
     for (int i = 0; i < SG; ++i) {
       const int c = tid + THREADS * (b0 + i), r = c / CPR;
-      *reinterpret_cast<f16x8*>(Ws + r * ROWB + 16 * ((c % CPR) ^ (r & 15))) = v[i];
+      *reinterpret_cast<V8*>(Ws + r * ROWB + 16 * ((c % CPR) ^ (r & 15))) = v[i];
     }
   }
   float gv[8], bv[8];
@@ -489,11 +502,11 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
         q += t * t;
       }
       const float rstd = rsqrtf(group_sum<CPR>(q) * (1.0f / D) + eps);
-      f16x8 h;
+      V8 h;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = (f16)((xv[e] - mean) * rstd * gv[e] + bv[e]);
+      for (int e = 0; e < 8; ++e) h[e] = (TA)((xv[e] - mean) * rstd * gv[e] + bv[e]);
       const int r = RPP * p + rp;
-      *reinterpret_cast<f16x8*>(H + r * ROWB + 16 * (cl ^ (r & 15))) = h;
+      *reinterpret_cast<V8*>(H + r * ROWB + 16 * (cl ^ (r & 15))) = h;
     }
     // One barrier per block: H of this block is complete, and (double buffering)
     // every wave finished the previous block's reads of the other buffer.
@@ -510,12 +523,12 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
       const int co = 16 * ((2 * kk + g) ^ sw);
-      f16x8 hf[RT], wf[NT];
+      V8 hf[RT], wf[NT];
 #pragma unroll
-      for (int i = 0; i < RT; ++i) hf[i] = *reinterpret_cast<const f16x8*>(H + (32 * (RT * rg + i) + li) * ROWB + co);
+      for (int i = 0; i < RT; ++i) hf[i] = *reinterpret_cast<const V8*>(H + (32 * (RT * rg + i) + li) * ROWB + co);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        wf[t] = *reinterpret_cast<const f16x8*>(Ws + (128 * t + 32 * w + li) * ROWB + co);
+        wf[t] = *reinterpret_cast<const V8*>(Ws + (128 * t + 32 * w + li) * ROWB + co);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -538,10 +551,10 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
         const int r = 32 * (RT * rg + i) + li;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          f16x4 h;
+          V4 h;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = (f16)acc[t][i][4 * q + e];
-          *reinterpret_cast<f16x4*>(O + r * ROWB + 16 * ((4 * w + q) ^ (r & 15)) + 8 * g) = h;
+          for (int e = 0; e < 4; ++e) h[e] = (TA)acc[t][i][4 * q + e];
+          *reinterpret_cast<V4*>(O + r * ROWB + 16 * ((4 * w + q) ^ (r & 15)) + 8 * g) = h;
         }
       }
       __syncthreads();
@@ -551,8 +564,8 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
       for (int k = 0; k < BM * CPR / THREADS; ++k) {
         const int idx = tid + THREADS * k, r = idx / CPR, c = idx % CPR;
         const int64_t m = blk * BM + r;
-        *reinterpret_cast<f16x8*>(C + (m < M ? m : M - 1) * N + 128 * t + 8 * c) =
-            *reinterpret_cast<const f16x8*>(O + r * ROWB + 16 * (c ^ (r & 15)));
+        *reinterpret_cast<V8*>(C + (m < M ? m : M - 1) * N + 128 * t + 8 * c) =
+            *reinterpret_cast<const V8*>(O + r * ROWB + 16 * (c ^ (r & 15)));
       }
       // No barrier here: slab t + 1 goes to the other buffer, and slab t + 2, which
       // reuses this one, is written after the barrier that follows slab t + 1's
@@ -566,42 +579,53 @@ __global__ __launch_bounds__(64 * NWV) void ln_gemm_p_kernel(const TX* __restric
   }
 }
 
-template <int NT, typename TX>
+template <int NT, typename TX, typename TA>
 static hipError_t launch_ln_gemm_p(const LnGemmArgs& a) {
   const int64_t cus = compute_units();
   if (a.M >= (int64_t)64 * 2 * cus) {
     const int64_t nblk = (a.M + 63) / 64;
-    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 64, 8, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(512), 0,
-                       a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
-                       static_cast<f16*>(a.c), a.M, a.eps);
+    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 64, 8, TX, TA>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(512), 0,
+                       a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const TA*>(a.w), a.bias,
+                       static_cast<TA*>(a.c), a.M, a.eps);
   } else {
     const int64_t nblk = (a.M + 31) / 32;
-    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 32, 4, TX>), dim3((unsigned)(nblk < cus ? nblk : cus)), dim3(kLgThreads), 0,
-                       a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
-                       static_cast<f16*>(a.c), a.M, a.eps);
+    hipLaunchKernelGGL((ln_gemm_p_kernel<NT, 32, 4, TX, TA>), dim3((unsigned)(nblk < cus ? nblk : cus)),
+                       dim3(kLgThreads), 0, a.stream, static_cast<const TX*>(a.x), a.gamma, a.beta,
+                       static_cast<const TA*>(a.w), a.bias, static_cast<TA*>(a.c), a.M, a.eps);
   }
   return hipGetLastError();
 }
 
-template <int D, typename TX>
+template <int D, typename TX, typename TA>
 static hipError_t launch_ln_gemm(const LnGemmArgs& a) {
   const int64_t tiles = ((a.M + kLgBM - 1) / kLgBM) * (int64_t)((a.N + kLgBN - 1) / kLgBN);
   if (tiles > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((ln_gemm_kernel<D, TX>), dim3((unsigned)tiles), dim3(kLgThreads), 0, a.stream,
-                     static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const f16*>(a.w), a.bias,
-                     static_cast<f16*>(a.c), a.M, a.N, a.eps);
+  hipLaunchKernelGGL((ln_gemm_kernel<D, TX, TA>), dim3((unsigned)tiles), dim3(kLgThreads), 0, a.stream,
+                     static_cast<const TX*>(a.x), a.gamma, a.beta, static_cast<const TA*>(a.w), a.bias,
+                     static_cast<TA*>(a.c), a.M, a.N, a.eps);
   return hipGetLastError();
 }
 
-bool ln_gemm_ok(int64_t d, int x_dtype) { return (d == 64 || d == 128) && (x_dtype == kF16 || x_dtype == kF32); }
+template <typename TX, typename TA>
+static hipError_t ln_gemm_typed(const LnGemmArgs& a) {
+  if (a.d == 128 && a.N == 384) return launch_ln_gemm_p<3, TX, TA>(a);
+  return a.d == 128 ? launch_ln_gemm<128, TX, TA>(a) : launch_ln_gemm<64, TX, TA>(a);
+}
+
+// fp16 operands with fp16 or fp32 x; bf16 operands with bf16 or fp32 x.
+bool ln_gemm_ok(int64_t d, int x_dtype, int ab_dtype) {
+  if (d != 64 && d != 128) return false;
+  if (ab_dtype == kBF16) return x_dtype == kBF16 || x_dtype == kF32;
+  return ab_dtype == kF16 && (x_dtype == kF16 || x_dtype == kF32);
+}
 
 hipError_t run_ln_gemm(const LnGemmArgs& a) {
-  if (!ln_gemm_ok(a.d, a.x_dtype) || a.M < 0 || a.N <= 0 || a.N % 8 != 0 || a.N > 3 * a.d) return hipErrorInvalidValue;
+  if (!ln_gemm_ok(a.d, a.x_dtype, a.ab_dtype) || a.M < 0 || a.N <= 0 || a.N % 8 != 0 || a.N > 3 * a.d)
+    return hipErrorInvalidValue;
   if (!a.x || !a.w || !a.c || (a.gamma == nullptr) != (a.beta == nullptr)) return hipErrorInvalidValue;
   if (a.M == 0) return hipSuccess;
-  if (a.d == 128 && a.N == 384) return a.x_dtype == kF16 ? launch_ln_gemm_p<3, f16>(a) : launch_ln_gemm_p<3, float>(a);
-  if (a.d == 128) return a.x_dtype == kF16 ? launch_ln_gemm<128, f16>(a) : launch_ln_gemm<128, float>(a);
-  return a.x_dtype == kF16 ? launch_ln_gemm<64, f16>(a) : launch_ln_gemm<64, float>(a);
+  if (a.ab_dtype == kBF16) return a.x_dtype == kBF16 ? ln_gemm_typed<bf16, bf16>(a) : ln_gemm_typed<float, bf16>(a);
+  return a.x_dtype == kF16 ? ln_gemm_typed<f16, f16>(a) : ln_gemm_typed<float, f16>(a);
 }
 
 }  // namespace cobra
