@@ -510,6 +510,18 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
     if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
     cobra::QkvAttnArgs f{h, w_qkv, b_qkv, qkv, batch, seq_len, heads, hd, (float)(1.0 / sqrt((double)hd)),
                          causal ? 1 : 0, bits, s};
+    if (x_dtype == kF16 && !resid_out && cobra::gemm_rowln_ok(T, (int)D, (int)D)) {
+      // fp16 activations, r not requested, the out-projection grid resident at once:
+      // LN2 in the out-projection's epilogue (row statistics exchanged between the column
+      // tiles of a row block through a sync area past ctx, which the fused QKV kernel
+      // marks unwritten).
+      void* sync = static_cast<char*>(qkv) + round256(T * D * 2);
+      f.fill = static_cast<uint64_t*>(sync);
+      f.nfill = cobra::gemm_rowln_sync_bytes(T, (int)D) / 8;
+      if ((e = cobra::run_qkv_attn_head(f)) != hipSuccess) return code(e);
+      cobra::GemmRowLnArgs out{qkv, w_o, b_o, x, ln2_w, ln2_b, y, T, (int)D, (int)D, eps, valid_mask, sync, s};
+      return code(cobra::run_gemm_rowln(out));
+    }
     if ((e = cobra::run_qkv_attn_head(f)) != hipSuccess) return code(e);
     // fp32 r (fp32 x): the qkv area past ctx, 4 T D bytes.
     float* r32 = reinterpret_cast<float*>(static_cast<char*>(qkv) + T * D * 2);

@@ -62,30 +62,16 @@ __device__ __forceinline__ float to_float(T v) {
 
 }  // namespace
 
-template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC, typename TA>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const TA* __restrict__ A, const TA* __restrict__ W,
-                                                              const float* __restrict__ bias,
-                                                              const TR* __restrict__ resid, TC* __restrict__ C,
-                                                              int64_t M, int N, int K,
-                                                              const uint8_t* __restrict__ row_mask, int epi) {
+// The k-loop of the LDS-DMA GEMMs: acc[j][i] += (W rows n0 + wn*WTN + 32j ..) x
+// (A rows m0 + wm*WTM + 32i ..)^T over all of K.
+template <int BM, int BN, int WM, int WN, int ST, typename TA>
+__device__ __forceinline__ void dma_mainloop(const TA* __restrict__ A, const TA* __restrict__ W, int64_t M, int N,
+                                             int K, int64_t m0, int n0, char* smem,
+                                             f32x16 (&acc)[BN / WN / 32][BM / WM / 32]) {
   using T = DmaTile<BM, BN, WM, WN, ST>;
-  constexpr int BK = T::BK, NT = T::NT, NW = T::NW, LPT = T::LPT;
+  constexpr int BK = T::BK, NW = T::NW, LPT = T::LPT;
   using V8 = typename Op16<TA>::V8;
-  __shared__ __attribute__((aligned(1024))) char smem[T::LDS];
-  TA* lds = reinterpret_cast<TA*>(smem);
-
-  // Tile order: each XCD runs a contiguous range of tile ids; within it, ids
-  // walk GM row blocks x all column blocks, so the tiles resident on one XCD
-  // at a time share a few A row blocks and W column blocks in its L2.
-  const int nbn = (N + BN - 1) / BN;
-  const int nbm = (int)((M + BM - 1) / BM);
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int group = tile / (GM * nbn);
-  const int first_m = group * GM;
-  const int gm = min(nbm - first_m, GM);
-  const int in_group = tile - group * GM * nbn;
-  const int64_t m0 = (int64_t)(first_m + in_group % gm) * BM;
-  const int n0 = (in_group / gm) * BN;
+  const TA* lds = reinterpret_cast<const TA*>(smem);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -122,7 +108,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const TA* __restr
     }
   };
 
-  f32x16 acc[T::TN][T::TM];
 #pragma unroll
   for (int j = 0; j < T::TN; ++j)
 #pragma unroll
@@ -173,6 +158,38 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const TA* __restr
         for (int i = 0; i < T::TM; ++i) acc[j][i] = mfma32x32x16(wf[kk & 1][j], af[kk & 1][i], acc[j][i]);
     }
   }
+}
+
+template <int BM, int BN, int WM, int WN, int ST, int GM, typename TR, typename TC, typename TA>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_dma_kernel(const TA* __restrict__ A, const TA* __restrict__ W,
+                                                              const float* __restrict__ bias,
+                                                              const TR* __restrict__ resid, TC* __restrict__ C,
+                                                              int64_t M, int N, int K,
+                                                              const uint8_t* __restrict__ row_mask, int epi) {
+  using T = DmaTile<BM, BN, WM, WN, ST>;
+  constexpr int NT = T::NT;
+  __shared__ __attribute__((aligned(1024))) char smem[T::LDS];
+
+  // Tile order: each XCD runs a contiguous range of tile ids; within it, ids
+  // walk GM row blocks x all column blocks, so the tiles resident on one XCD
+  // at a time share a few A row blocks and W column blocks in its L2.
+  const int nbn = (N + BN - 1) / BN;
+  const int nbm = (int)((M + BM - 1) / BM);
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int group = tile / (GM * nbn);
+  const int first_m = group * GM;
+  const int gm = min(nbm - first_m, GM);
+  const int in_group = tile - group * GM * nbn;
+  const int64_t m0 = (int64_t)(first_m + in_group % gm) * BM;
+  const int n0 = (in_group / gm) * BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int li = lane & 31, g = lane >> 5;
+
+  f32x16 acc[T::TN][T::TM];
+  dma_mainloop<BM, BN, WM, WN, ST>(A, W, M, N, K, m0, n0, smem, acc);
   __syncthreads();  // every wave is done with the operand stages
 
   // Epilogue in TN slices: slice j holds, for every wave column wn, the 32
@@ -310,6 +327,222 @@ static hipError_t dispatch_dma(const GemmArgs& a) {
     case 1: return launch_dma<256, 192, 4, 2, 2, 4, TR, TC, TA>(a);
     case 2: return launch_dma<256, 128, 4, 2, 2, 4, TR, TC, TA>(a);
     default: return launch_dma<128, 128, 2, 2, 2, 8, TR, TC, TA>(a);
+  }
+}
+
+// Out-projection with LayerNorm over whole rows wider than one tile (N = NB * BN, fp16
+// activations): y = LN(x + mask(a W^T + bias)) * gamma + beta, without the branch ever
+// reaching memory (the reference's _gemm_kernel + _add_ln_kernel pair for d_model > 128,
+// torch_transformer_benchmark.py:1274-1283, 491-535).
+//
+// The NB column tiles of a BM-row block hold disjoint column ranges of the same rows.
+// Each reduces its rows to (mean, M2) over its BN columns (two passes over registers)
+// and publishes them as one 64-bit word per row; the row-phase lanes then read the
+// words of all NB tiles, polling until none holds the "not yet written" pattern the
+// preceding kernel of the sublayer filled the area with, and combine them exactly (Chan
+// et al.: mean of the tile means, M2 = sum M2_t + BN sum (mean_t - mean)^2).  The words
+// move through agent-scope atomics (stores and loads at the device coherence point,
+// past the XCD-local L2s); a 64-bit word is written whole, so a reader sees either the
+// fill pattern or the published statistics, and needs no fence, counter or barrier.
+//
+// Co-residency: the launcher runs this kernel only when the whole grid fits the chip
+// at one workgroup per CU.  Tile ids are dealt to XCDs in contiguous ranges
+// (xcd_remap) and a row block's tiles are consecutive ids, so each XCD dispatches the
+// tiles of one row block before those of the next: a tile only ever waits for tiles
+// dispatched no later than the ones its XCD has already placed, so the waits end even
+// when fewer CUs are free.  The wait is bounded all the same (spin_limit polls); a
+// wave that gives up writes NaN rows rather than hanging.
+template <int BM, int BN, int WM, int WN, int ST, int NB, bool MASKED, typename TA>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_dma_rowln_kernel(
+    const TA* __restrict__ A, const TA* __restrict__ W, const float* __restrict__ bias, const f16* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta, f16* __restrict__ y, int64_t M, int K,
+    float eps, const uint8_t* __restrict__ row_mask, uint64_t* __restrict__ stats, int spin_limit) {
+  using T = DmaTile<BM, BN, WM, WN, ST>;
+  constexpr int NT = T::NT, N = NB * BN;
+  constexpr int LDC = BN + 4;          // fp32 staging row stride (floats)
+  constexpr int LPR = BN / 8;          // lanes per row in the row phase, 8 columns each
+  constexpr int RPP = NT / LPR;        // rows per pass
+  constexpr int NP = BM / RPP;         // passes
+  constexpr int LDSB = T::LDS > BM * LDC * 4 ? T::LDS : BM * LDC * 4;
+  static_assert(NB >= 2 && NB <= LPR && (NB & (NB - 1)) == 0, "one tile's statistics per lane of a row group");
+  static_assert(NT % LPR == 0 && BM % RPP == 0 && LDSB <= 163840, "row-phase geometry");
+  __shared__ __attribute__((aligned(1024))) char smem[LDSB];
+
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int rb = tile / NB, tc = tile % NB;
+  const int64_t m0 = (int64_t)rb * BM;
+  const int n0 = tc * BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int li = lane & 31, g = lane >> 5;
+  const int cl = (tid % LPR) * 8;  // row phase: this lane's 8 columns of the tile
+  const int rl = tid / LPR;        // and its row within each pass
+
+  // Everything the epilogue reads from memory is requested before the k-loop: the
+  // residual rows of the row phase, the bias of this lane's accumulator columns, the
+  // row-mask bytes, gamma and beta.  The first k-tile waits for all transfers in flight
+  // anyway (its LDS-DMA), so these cost one round trip there and none later (issued
+  // inside the loop, the LDS reads after them would wait for them).
+  f16x8 xr[NP];
+  f32x4 bq[T::TN][4];
+  uint8_t mb[T::TM];
+  f32x4 gv4[2], bv4[2];
+  {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int64_t m = min(m0 + p * RPP + rl, M - 1);
+      xr[p] = *reinterpret_cast<const f16x8*>(x + m * N + n0 + cl);
+    }
+#pragma unroll
+    for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bq[j][q] = *reinterpret_cast<const f32x4*>(bias + n0 + wn * T::WTN + j * 32 + 8 * q + 4 * g);
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i) mb[i] = row_mask[min(m0 + wm * T::WTM + i * 32 + li, M - 1)];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      gv4[h] = *reinterpret_cast<const f32x4*>(gamma + n0 + cl + 4 * h);
+      bv4[h] = *reinterpret_cast<const f32x4*>(beta + n0 + cl + 4 * h);
+    }
+  }
+  f32x16 acc[T::TN][T::TM];
+  dma_mainloop<BM, BN, WM, WN, ST>(A, W, M, N, K, m0, n0, smem, acc);
+  __syncthreads();  // every wave is done with the operand stages
+
+  // Branch a W^T + bias, zero on padded rows, staged as fp32 rows of the tile.
+  float* Cs = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int j = 0; j < T::TN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = wn * T::WTN + j * 32 + 8 * q + 4 * g;
+#pragma unroll
+      for (int i = 0; i < T::TM; ++i) {
+        const int row = wm * T::WTM + i * 32 + li;
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[j][i][4 * q + e] + bq[j][q][e];
+        if constexpr (MASKED) {
+          if (mb[i] == 0) v = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        *reinterpret_cast<f32x4*>(Cs + row * LDC + col) = v;
+      }
+    }
+  __syncthreads();
+
+  // r = x + branch; per row of the tile, LPR lanes hold 8 columns each: the tile's
+  // mean, then M2 around it, published as one 64-bit word per row.
+  float r[NP][8];
+  uint64_t* my_stats = stats + ((int64_t)rb * NB + tc) * BM;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int row = p * RPP + rl;
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(Cs + row * LDC + cl);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(Cs + row * LDC + cl + 4);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      r[p][e] = (float)xr[p][e] + (e < 4 ? c0[e] : c1[e - 4]);
+      s += r[p][e];
+    }
+    const float mean_t = group_sum<LPR>(s) * (1.0f / BN);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = r[p][e] - mean_t;
+      q += d * d;
+    }
+    q = group_sum<LPR>(q);
+    if (tid % LPR == 0) {
+      const uint64_t word = (uint64_t)__float_as_uint(mean_t) | ((uint64_t)__float_as_uint(q) << 32);
+      __hip_atomic_store(my_stats + row, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  // Lane j of a row group reads tile j % NB's word of each of its rows, until none is
+  // the fill pattern (the wave polls as one); each aligned group of NB lanes then holds
+  // every tile once.
+  const uint64_t* row_stats = stats + ((int64_t)rb * NB + (tid % LPR) % NB) * BM + rl;
+  uint64_t w[NP];
+  bool ok = true;
+  for (int polls = 0;; ++polls) {
+    bool pending = false;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      w[p] = __hip_atomic_load(row_stats + p * RPP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pending = pending || w[p] == kRowLnUnset;
+    }
+    if (!__builtin_amdgcn_ballot_w64(pending)) break;
+    if (polls >= spin_limit) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+
+  float gv[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    gv[e] = gv4[e >> 2][e & 3];
+    bv[e] = bv4[e >> 2][e & 3];
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const float mean_t = __uint_as_float((uint32_t)w[p]);
+    const float m2_t = __uint_as_float((uint32_t)(w[p] >> 32));
+    const float mean = group_sum<NB>(mean_t) * (1.0f / NB);
+    const float d = mean_t - mean;
+    const float m2 = group_sum<NB>(m2_t + (float)BN * d * d);
+    const float rstd = ok ? rsqrtf(m2 * (1.0f / N) + eps) : __builtin_nanf("");
+    const int64_t m = m0 + p * RPP + rl;
+    if (m < M) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (r[p][e] - mean) * rstd * gv[e] + bv[e];
+      store8(y + m * N + n0 + cl, o);
+    }
+  }
+}
+
+template <int NB, bool MASKED>
+static hipError_t launch_rowln(const GemmRowLnArgs& a) {
+  constexpr int BM = 256, BN = 128;
+  const int64_t nbm = (a.M + BM - 1) / BM;
+  hipLaunchKernelGGL((gemm_dma_rowln_kernel<BM, BN, 4, 2, 2, NB, MASKED, f16>), dim3((unsigned)(nbm * NB)), dim3(512),
+                     0, a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
+                     static_cast<const f16*>(a.x), a.gamma, a.beta, static_cast<f16*>(a.y), a.M, a.K, a.eps,
+                     a.row_mask, static_cast<uint64_t*>(a.sync), 1 << 20);
+  return hipGetLastError();
+}
+
+template <int NB>
+static hipError_t launch_rowln(const GemmRowLnArgs& a) {
+  return a.row_mask ? launch_rowln<NB, true>(a) : launch_rowln<NB, false>(a);
+}
+
+bool gemm_rowln_ok(int64_t M, int N, int K) {
+  // 128-wide column tiles, 2 .. 16 per row; K in whole k-tiles with 32-bit block offsets;
+  // the whole grid resident at once (one 256 x 128 tile per CU).
+  if (M <= 0 || K <= 0 || K % 64 != 0 || (int64_t)256 * K * 2 >= ((int64_t)1 << 32)) return false;
+  if (N != 256 && N != 512 && N != 1024 && N != 2048) return false;
+  return ((M + 255) / 256) * (N / 128) <= compute_units();
+}
+
+int64_t gemm_rowln_sync_bytes(int64_t M, int N) { return (M + 255) / 256 * (N / 128) * 256 * 8; }
+
+hipError_t run_gemm_rowln(const GemmRowLnArgs& a) {
+  if (!a.a || !a.w || !a.bias || !a.x || !a.gamma || !a.beta || !a.y || !a.sync || !gemm_rowln_ok(a.M, a.N, a.K))
+    return hipErrorInvalidValue;
+  switch (a.N / 128) {
+    case 2: return launch_rowln<2>(a);
+    case 4: return launch_rowln<4>(a);
+    case 8: return launch_rowln<8>(a);
+    default: return launch_rowln<16>(a);
   }
 }
 

@@ -101,6 +101,33 @@ hipError_t run_gemm(const GemmArgs& a);
 bool gemm_dma_ok(const GemmArgs& a);
 hipError_t run_gemm_dma(const GemmArgs& a);
 
+// Out-projection with LayerNorm over rows of N = 256 .. 2048 in its epilogue
+// (gemm_dma.hip): y = LN(x + mask(a W^T + bias)) * gamma + beta, fp16 a / w / x / y.
+// The column tiles of a row block exchange per-row statistics through `sync`
+// (gemm_rowln_sync_bytes, 64-bit words that must all hold kRowLnUnset at launch), so
+// the whole grid has to fit the chip at once: gemm_rowln_ok.  Launches that share a
+// sync area must not overlap.
+constexpr uint64_t kRowLnUnset = ~0ull;
+struct GemmRowLnArgs {
+  const void* a;           // [M, K] fp16
+  const void* w;           // [N, K] fp16
+  const float* bias;       // [N]
+  const void* x;           // [M, N] fp16 residual
+  const float* gamma;      // [N]
+  const float* beta;       // [N]
+  void* y;                 // [M, N] fp16
+  int64_t M;
+  int N;
+  int K;
+  float eps;
+  const uint8_t* row_mask; // optional [M]: 0 = padded row, whose branch is zeroed
+  void* sync;
+  hipStream_t stream;
+};
+bool gemm_rowln_ok(int64_t M, int N, int K);
+int64_t gemm_rowln_sync_bytes(int64_t M, int N);
+hipError_t run_gemm_rowln(const GemmRowLnArgs& a);
+
 // LayerNorm in the prologue of the projection that consumes it (ln_gemm.hip):
 // c = (LayerNorm(x) * gamma + beta) w^T + bias, rows of d = 64 or 128, fp16 out.
 struct LnGemmArgs {
@@ -152,6 +179,8 @@ struct QkvAttnArgs {
   int causal;
   const uint64_t* key_bits;  // optional [batch][ceil(S/64)]
   hipStream_t stream;
+  uint64_t* fill = nullptr;  // optional: nfill words set to kRowLnUnset (for the kernel that follows)
+  int64_t nfill = 0;
 };
 bool qkv_attn_head_ok(int64_t seq_len, int64_t heads, int64_t head_dim);
 hipError_t run_qkv_attn_head(const QkvAttnArgs& a);

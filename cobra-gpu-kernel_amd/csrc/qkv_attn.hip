@@ -72,8 +72,11 @@ template <bool CAUSAL, bool MASKED>
 __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
     int S, int H, int D, int B, const f16* __restrict__ h, const f16* __restrict__ wqkv,
     const float* __restrict__ bqkv, f16* __restrict__ ctx, float c2, const uint64_t* __restrict__ key_bits,
-    int nwords) {
+    int nwords, uint64_t* __restrict__ fill, int64_t nfill) {
   __shared__ __attribute__((aligned(1024))) char smem[kQaLds];
+  // The statistics words the out-projection that follows expects unwritten.
+  for (int64_t i = (int64_t)blockIdx.x * (64 * kQaWaves) + threadIdx.x; i < nfill; i += (int64_t)gridDim.x * 64 * kQaWaves)
+    fill[i] = kRowLnUnset;
 
   // Consecutive ids share the head, so the workgroups on one XCD share that head's
   // 1.5 MB of weights in its L2.
@@ -293,12 +296,13 @@ static hipError_t launch_qkv_attn_head(const QkvAttnArgs& a, float c2) {
   hipLaunchKernelGGL((qkv_attn_head_kernel<CAUSAL, MASKED>), dim3((unsigned)grid), dim3(64 * kQaWaves), 0, a.stream,
                      (int)a.seq_len, (int)a.heads, (int)(a.heads * a.head_dim), (int)a.batch,
                      static_cast<const f16*>(a.h), static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<f16*>(a.ctx),
-                     c2, a.key_bits, (int)mask_words(a.seq_len));
+                     c2, a.key_bits, (int)mask_words(a.seq_len), a.fill, a.fill ? a.nfill : (int64_t)0);
   return hipGetLastError();
 }
 
 hipError_t run_qkv_attn_head(const QkvAttnArgs& a) {
-  if (!qkv_attn_head_ok(a.seq_len, a.heads, a.head_dim) || a.batch < 0 || !(a.scale > 0.f)) return hipErrorInvalidValue;
+  if (!qkv_attn_head_ok(a.seq_len, a.heads, a.head_dim) || a.batch < 0 || !(a.scale > 0.f) || a.nfill < 0)
+    return hipErrorInvalidValue;
   if (a.batch == 0) return hipSuccess;
   const float c2 = a.scale * 1.4426950408889634f;
   if (a.key_bits)
