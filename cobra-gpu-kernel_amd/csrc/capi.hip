@@ -208,6 +208,36 @@ int layer_fwd_bf16(const void* x, const uint8_t* valid_mask, const void* w_qkv, 
   uint64_t* bits = masked ? reinterpret_cast<uint64_t*>(ws + lb.bits_off) : nullptr;
   hipError_t e = hipSuccess;
   if (masked && (e = cobra::run_mask_bits(valid_mask, bits, batch, (int)seq_len, s)) != hipSuccess) return code(e);
+  const int64_t hd = D / H;
+  if (cobra::qkv_attn_head_ok(seq_len, H, hd)) {
+    // head_dim 256, S <= 128: as for fp16 -- LN1, the QKV projection fused into the
+    // attention (ctx into the qkv area), then the out-projection with LN2 in its epilogue
+    // when its grid fits the chip, else the out-projection storing r in fp32 (past ctx in
+    // the qkv area, or resid_out) and LN2 reading it.
+    cobra::LnArgs ln1{x, kBF16, nullptr, 0, ln1_w, ln1_b, nullptr, h, kBF16, T, (int)D, eps, s};
+    if ((e = cobra::run_ln(ln1)) != hipSuccess) return code(e);
+    cobra::QkvAttnArgs f{h, w_qkv, b_qkv, qkv, batch, seq_len, H, hd, (float)(1.0 / sqrt((double)hd)),
+                         causal ? 1 : 0, bits, s};
+    f.dtype = kBF16;
+    void* past_ctx = static_cast<char*>(qkv) + round256(T * D * 2);
+    if (!resid_out && cobra::gemm_rowln_ok(T, (int)D, (int)D)) {
+      f.fill = static_cast<uint64_t*>(past_ctx);
+      f.nfill = cobra::gemm_rowln_sync_bytes(T, (int)D) / 8;
+      if ((e = cobra::run_qkv_attn_head(f)) != hipSuccess) return code(e);
+      cobra::GemmRowLnArgs out{qkv, w_o, b_o, x, ln2_w, ln2_b, y, T, (int)D, (int)D, eps, valid_mask, past_ctx, s};
+      out.dtype = kBF16;
+      return code(cobra::run_gemm_rowln(out));
+    }
+    if ((e = cobra::run_qkv_attn_head(f)) != hipSuccess) return code(e);
+    float* r = resid_out ? resid_out : static_cast<float*>(past_ctx);
+    cobra::GemmArgs out{qkv, w_o, b_o, x, kBF16, r, kF32, T, (int)D, (int)D, nullptr, nullptr, nullptr, kF16, eps, s};
+    out.ab_dtype = kBF16;
+    out.row_mask = valid_mask;
+    out.epi = masked ? cobra::kEpiMaskBranch : 0;
+    if ((e = cobra::run_gemm(out)) != hipSuccess) return code(e);
+    cobra::LnArgs ln2{r, kF32, nullptr, 0, ln2_w, ln2_b, nullptr, y, kBF16, T, (int)D, eps, s};
+    return code(cobra::run_ln(ln2));
+  }
   // d_model 64 / 128: LN1 in the QKV projection's prologue and LN2 in the out-projection's
   // epilogue, as for fp16 (three launches); otherwise LN1 -> projection -> attention ->
   // out-projection (r in fp32) -> LN2.
@@ -224,7 +254,6 @@ int layer_fwd_bf16(const void* x, const uint8_t* valid_mask, const void* w_qkv, 
     proj.ab_dtype = kBF16;
     if ((e = cobra::run_gemm(proj)) != hipSuccess) return code(e);
   }
-  const int64_t hd = D / H;
   cobra::AttnArgs at{qkv, ctx, batch, (int)seq_len, (int)H, (int)hd, (float)(1.0 / sqrt((double)hd)),
                      causal ? 1 : 0, s};
   at.key_bits = bits;

@@ -330,8 +330,8 @@ static hipError_t dispatch_dma(const GemmArgs& a) {
   }
 }
 
-// Out-projection with LayerNorm over whole rows wider than one tile (N = NB * BN, fp16
-// activations): y = LN(x + mask(a W^T + bias)) * gamma + beta, without the branch ever
+// Out-projection with LayerNorm over whole rows wider than one tile (N = NB * BN; a, W, x
+// and y fp16 or bf16): y = LN(x + mask(a W^T + bias)) * gamma + beta, without the branch ever
 // reaching memory (the reference's _gemm_kernel + _add_ln_kernel pair for d_model > 128,
 // torch_transformer_benchmark.py:1274-1283, 491-535).
 //
@@ -354,8 +354,8 @@ static hipError_t dispatch_dma(const GemmArgs& a) {
 // wave that gives up writes NaN rows rather than hanging.
 template <int BM, int BN, int WM, int WN, int ST, int NB, bool MASKED, typename TA>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_rowln_kernel(
-    const TA* __restrict__ A, const TA* __restrict__ W, const float* __restrict__ bias, const f16* __restrict__ x,
-    const float* __restrict__ gamma, const float* __restrict__ beta, f16* __restrict__ y, int64_t M, int K,
+    const TA* __restrict__ A, const TA* __restrict__ W, const float* __restrict__ bias, const TA* __restrict__ x,
+    const float* __restrict__ gamma, const float* __restrict__ beta, TA* __restrict__ y, int64_t M, int K,
     float eps, const uint8_t* __restrict__ row_mask, uint64_t* __restrict__ stats, int spin_limit) {
   using T = DmaTile<BM, BN, WM, WN, ST>;
   constexpr int NT = T::NT, N = NB * BN;
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_rowln_kernel(
   // row-mask bytes, gamma and beta.  The first k-tile waits for all transfers in flight
   // anyway (its LDS-DMA), so these cost one round trip there and none later (issued
   // inside the loop, the LDS reads after them would wait for them).
-  f16x8 xr[NP];
+  typename Op16<TA>::V8 xr[NP];
   f32x4 bq[T::TN][4];
   uint8_t mb[T::TM];
   f32x4 gv4[2], bv4[2];
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_rowln_kernel(
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int64_t m = min(m0 + p * RPP + rl, M - 1);
-      xr[p] = *reinterpret_cast<const f16x8*>(x + m * N + n0 + cl);
+      xr[p] = *reinterpret_cast<const typename Op16<TA>::V8*>(x + m * N + n0 + cl);
     }
 #pragma unroll
     for (int j = 0; j < T::TN; ++j)
@@ -509,20 +509,22 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_rowln_kernel(
   }
 }
 
-template <int NB, bool MASKED>
+template <int NB, bool MASKED, typename TA>
 static hipError_t launch_rowln(const GemmRowLnArgs& a) {
   constexpr int BM = 256, BN = 128;
   const int64_t nbm = (a.M + BM - 1) / BM;
-  hipLaunchKernelGGL((gemm_dma_rowln_kernel<BM, BN, 4, 2, 2, NB, MASKED, f16>), dim3((unsigned)(nbm * NB)), dim3(512),
-                     0, a.stream, static_cast<const f16*>(a.a), static_cast<const f16*>(a.w), a.bias,
-                     static_cast<const f16*>(a.x), a.gamma, a.beta, static_cast<f16*>(a.y), a.M, a.K, a.eps,
+  hipLaunchKernelGGL((gemm_dma_rowln_kernel<BM, BN, 4, 2, 2, NB, MASKED, TA>), dim3((unsigned)(nbm * NB)), dim3(512),
+                     0, a.stream, static_cast<const TA*>(a.a), static_cast<const TA*>(a.w), a.bias,
+                     static_cast<const TA*>(a.x), a.gamma, a.beta, static_cast<TA*>(a.y), a.M, a.K, a.eps,
                      a.row_mask, static_cast<uint64_t*>(a.sync), 1 << 20);
   return hipGetLastError();
 }
 
 template <int NB>
 static hipError_t launch_rowln(const GemmRowLnArgs& a) {
-  return a.row_mask ? launch_rowln<NB, true>(a) : launch_rowln<NB, false>(a);
+  if (a.dtype == kBF16)
+    return a.row_mask ? launch_rowln<NB, true, bf16>(a) : launch_rowln<NB, false, bf16>(a);
+  return a.row_mask ? launch_rowln<NB, true, f16>(a) : launch_rowln<NB, false, f16>(a);
 }
 
 bool gemm_rowln_ok(int64_t M, int N, int K) {
@@ -538,6 +540,7 @@ int64_t gemm_rowln_sync_bytes(int64_t M, int N) { return (M + 255) / 256 * (N / 
 hipError_t run_gemm_rowln(const GemmRowLnArgs& a) {
   if (!a.a || !a.w || !a.bias || !a.x || !a.gamma || !a.beta || !a.y || !a.sync || !gemm_rowln_ok(a.M, a.N, a.K))
     return hipErrorInvalidValue;
+  if (a.dtype != kF16 && a.dtype != kBF16) return hipErrorInvalidValue;
   switch (a.N / 128) {
     case 2: return launch_rowln<2>(a);
     case 4: return launch_rowln<4>(a);

@@ -102,20 +102,21 @@ bool gemm_dma_ok(const GemmArgs& a);
 hipError_t run_gemm_dma(const GemmArgs& a);
 
 // Out-projection with LayerNorm over rows of N = 256 .. 2048 in its epilogue
-// (gemm_dma.hip): y = LN(x + mask(a W^T + bias)) * gamma + beta, fp16 a / w / x / y.
+// (gemm_dma.hip): y = LN(x + mask(a W^T + bias)) * gamma + beta, a / w / x / y all fp16 or
+// all bf16.
 // The column tiles of a row block exchange per-row statistics through `sync`
 // (gemm_rowln_sync_bytes, 64-bit words that must all hold kRowLnUnset at launch), so
 // the whole grid has to fit the chip at once: gemm_rowln_ok.  Launches that share a
 // sync area must not overlap.
 constexpr uint64_t kRowLnUnset = ~0ull;
 struct GemmRowLnArgs {
-  const void* a;           // [M, K] fp16
-  const void* w;           // [N, K] fp16
+  const void* a;           // [M, K] dtype
+  const void* w;           // [N, K] dtype
   const float* bias;       // [N]
-  const void* x;           // [M, N] fp16 residual
+  const void* x;           // [M, N] dtype residual
   const float* gamma;      // [N]
   const float* beta;       // [N]
-  void* y;                 // [M, N] fp16
+  void* y;                 // [M, N] dtype
   int64_t M;
   int N;
   int K;
@@ -123,6 +124,7 @@ struct GemmRowLnArgs {
   const uint8_t* row_mask; // optional [M]: 0 = padded row, whose branch is zeroed
   void* sync;
   hipStream_t stream;
+  int dtype = 0;           // a, w, x and y: kF16 (0) or kBF16
 };
 bool gemm_rowln_ok(int64_t M, int N, int K);
 int64_t gemm_rowln_sync_bytes(int64_t M, int N);
@@ -170,10 +172,10 @@ hipError_t run_attn(const AttnArgs& a);
 // QKV projection fused into exact attention, one workgroup per (sequence, head):
 // head_dim 256, S <= 128 (qkv_attn.hip).  ctx must not overlap h.
 struct QkvAttnArgs {
-  const void* h;           // [B*S, D] fp16 (D = heads * head_dim)
-  const void* w_qkv;       // [3D, D] fp16: q | k | v rows
+  const void* h;           // [B*S, D] dtype (D = heads * head_dim)
+  const void* w_qkv;       // [3D, D] dtype: q | k | v rows
   const float* b_qkv;      // [3D] or null
-  void* ctx;               // [B*S, D] fp16
+  void* ctx;               // [B*S, D] dtype
   int64_t batch, seq_len, heads, head_dim;
   float scale;
   int causal;
@@ -181,6 +183,7 @@ struct QkvAttnArgs {
   hipStream_t stream;
   uint64_t* fill = nullptr;  // optional: nfill words set to kRowLnUnset (for the kernel that follows)
   int64_t nfill = 0;
+  int dtype = 0;             // h, w_qkv and ctx: kF16 (0) or kBF16
 };
 bool qkv_attn_head_ok(int64_t seq_len, int64_t heads, int64_t head_dim);
 hipError_t run_qkv_attn_head(const QkvAttnArgs& a);

@@ -27,7 +27,9 @@
 //      key is present, one pass, no rescale); wave w then forms output d-tile w for
 //      all four query tiles and stores ctx.
 // Operand conventions as in common.hpp.  Rows past S read row S - 1 (finite); their
-// keys get probability 0 and their queries are never stored.
+// keys get probability 0 and their queries are never stored.  h, the weights and ctx
+// are fp16 or bf16 (a template type: v_mfma_f32_32x32x16_bf16 and bf16 probabilities
+// for the latter), everything else is the same code.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "layer_common.hpp"
@@ -62,17 +64,40 @@ static_assert(kQaLpt < 64, "vmcnt range");
 // Rows of a k-tile are 64 bytes (4 chunks of 16); chunk c of row R sits at chunk
 // c ^ ((R >> 2) & 3), so the 16 rows one fragment read touches at one logical chunk
 // hit 16 distinct 4-bank groups.
-__device__ __forceinline__ f16x8 qa_frag(const char* stage, int row, int chunk) {
-  return *reinterpret_cast<const f16x8*>(stage + row * kQaRowB + 16 * (chunk ^ ((row >> 2) & 3)));
+template <typename T>
+__device__ __forceinline__ typename Op16<T>::V8 qa_frag(const char* stage, int row, int chunk) {
+  return *reinterpret_cast<const typename Op16<T>::V8*>(stage + row * kQaRowB + 16 * (chunk ^ ((row >> 2) & 3)));
+}
+
+// Registers 8 half .. 8 half + 7 of an accumulator in the operand type.
+template <typename T>
+__device__ __forceinline__ typename Op16<T>::V8 acc_op(const f32x16& acc, int half) {
+  typename Op16<T>::V8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (T)acc[8 * half + e];
+  return o;
+}
+
+// a += p0 + p2 + p4 + p6, b += p1 + p3 + p5 + p7 in pairs (v_dot2 against ones), fp32 sums.
+template <typename T>
+__device__ __forceinline__ void add_probs_op(const typename Op16<T>::V8& p, float& a, float& b) {
+  using V2 = typename Op16<T>::V2;
+  const V2 one2 = {(T)1.0f, (T)1.0f};
+  a = dot2(V2{p[0], p[1]}, one2, a);
+  b = dot2(V2{p[2], p[3]}, one2, b);
+  a = dot2(V2{p[4], p[5]}, one2, a);
+  b = dot2(V2{p[6], p[7]}, one2, b);
 }
 
 }  // namespace
 
-template <bool CAUSAL, bool MASKED>
+template <bool CAUSAL, bool MASKED, typename T>
 __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
-    int S, int H, int D, int B, const f16* __restrict__ h, const f16* __restrict__ wqkv,
-    const float* __restrict__ bqkv, f16* __restrict__ ctx, float c2, const uint64_t* __restrict__ key_bits,
+    int S, int H, int D, int B, const T* __restrict__ h, const T* __restrict__ wqkv,
+    const float* __restrict__ bqkv, T* __restrict__ ctx, float c2, const uint64_t* __restrict__ key_bits,
     int nwords, uint64_t* __restrict__ fill, int64_t nfill) {
+  using V8 = typename Op16<T>::V8;
+  using V4 = typename Op16<T>::V4;
   __shared__ __attribute__((aligned(1024))) char smem[kQaLds];
   // The statistics words the out-projection that follows expects unwritten.
   for (int64_t i = (int64_t)blockIdx.x * (64 * kQaWaves) + threadIdx.x; i < nfill; i += (int64_t)gridDim.x * 64 * kQaWaves)
@@ -87,7 +112,7 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 31, g = lane >> 5;
   const int KT = D / kQaBk;
-  const f16* hseq = h + (int64_t)b * S * D;
+  const T* hseq = h + (int64_t)b * S * D;
   const char* hbytes = reinterpret_cast<const char*>(hseq);
   const char* wbytes = reinterpret_cast<const char*>(wqkv);
 
@@ -134,12 +159,12 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int c = 2 * kk + g;
-      f16x8 af[2], hf[4], vf;
+      V8 af[2], hf[4], vf;
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) af[dt] = qa_frag(st, kQaTok + 64 * w + 32 * dt + li, c);
+      for (int dt = 0; dt < 2; ++dt) af[dt] = qa_frag<T>(st, kQaTok + 64 * w + 32 * dt + li, c);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) hf[tt] = qa_frag(st, 32 * tt + li, c);
-      vf = qa_frag(st, kQaTok + 2 * kQaHd + 32 * w + li, c);
+      for (int tt = 0; tt < 4; ++tt) hf[tt] = qa_frag<T>(st, 32 * tt + li, c);
+      vf = qa_frag<T>(st, kQaTok + 2 * kQaHd + 32 * w + li, c);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         acc[0][tt] = mfma32x32x16(af[0], hf[tt], acc[0][tt]);
@@ -153,7 +178,7 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
     // + bias, fp16, into the K^T / Q^T fragment areas: k-step ks = 2 (2 (w % 4) + dt) + half
     // of the head's 16, token tile tt (the A operand of S^T = K Q^T for K, the B operand for Q).
     const bool isq = w < 4;
-    f16x8* const dstf = reinterpret_cast<f16x8*>(smem + (isq ? kQaOffQ : kQaOffK));
+    V8* const dstf = reinterpret_cast<V8*>(smem + (isq ? kQaOffQ : kQaOffK));
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
       const int grow0 = (isq ? 0 : D) + hh * kQaHd + 64 * (w & 3) + 32 * dt;
@@ -168,12 +193,12 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
         for (int r = 0; r < 16; ++r) v[r] += bq[r >> 2][r & 3];
 #pragma unroll
         for (int half = 0; half < 2; ++half)
-          dstf[(tt * 16 + 2 * (2 * (w & 3) + dt) + half) * 64 + lane] = acc_f16(v, half);
+          dstf[(tt * 16 + 2 * (2 * (w & 3) + dt) + half) * 64 + lane] = acc_op<T>(v, half);
       }
     }
   }
   // V^T fragments (+ bias of column li), key k-step 2 tt + half: the A operand of O^T.
-  f16x8 vA[8];
+  V8 vA[8];
   {
     const float bvl = bqkv ? bqkv[2 * D + hh * kQaHd + 32 * w + li] : 0.f;
 #pragma unroll
@@ -182,7 +207,7 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) v[r] += bvl;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) vA[2 * tt + half] = acc_f16(v, half);
+      for (int half = 0; half < 2; ++half) vA[2 * tt + half] = acc_op<T>(v, half);
     }
   }
   lds_barrier();
@@ -194,9 +219,9 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
   float* const ssum = smax + kQaWaves * 32;
   f32x16 sacc[2];
   {
-    const f16x8* Kf = reinterpret_cast<const f16x8*>(smem + kQaOffK);
-    const f16x8* Qf = reinterpret_cast<const f16x8*>(smem + kQaOffQ);
-    f16x8 qf[16];
+    const V8* Kf = reinterpret_cast<const V8*>(smem + kQaOffK);
+    const V8* Qf = reinterpret_cast<const V8*>(smem + kQaOffQ);
+    V8 qf[16];
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) qf[ks] = Qf[(qt * 16 + ks) * 64 + lane];
 #pragma unroll
@@ -234,16 +259,16 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
   float m = mx * c2;
   if constexpr (MASKED) m = mx == kNegInf ? 0.f : m;
   {
-    f16x8* const Pf = reinterpret_cast<f16x8*>(smem + kQaOffP);
+    V8* const Pf = reinterpret_cast<V8*>(smem + kQaOffP);
     float lp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int kt = 2 * kh + j;
-      f16x8 pB[2];
+      V8 pB[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pB[r >> 3][r & 7] = (f16)__builtin_amdgcn_exp2f(fmaf(sacc[j][r], c2, -m));
-      add_probs(pB[0], lp[0], lp[1]);
-      add_probs(pB[1], lp[2], lp[3]);
+      for (int r = 0; r < 16; ++r) pB[r >> 3][r & 7] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[j][r], c2, -m));
+      add_probs_op<T>(pB[0], lp[0], lp[1]);
+      add_probs_op<T>(pB[1], lp[2], lp[3]);
 #pragma unroll
       for (int half = 0; half < 2; ++half) Pf[(qt * 8 + 2 * kt + half) * 64 + lane] = pB[half];
     }
@@ -254,8 +279,8 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
   lds_barrier();  // the probabilities and row sums of every wave
 
   // ---- O^T (d-tile w) for every query tile, / row sum, -> ctx ----------------------------
-  const f16x8* Pf = reinterpret_cast<const f16x8*>(smem + kQaOffP);
-  f16* const crow0 = ctx + (int64_t)b * S * D + hh * kQaHd + 32 * w;
+  const V8* Pf = reinterpret_cast<const V8*>(smem + kQaOffP);
+  T* const crow0 = ctx + (int64_t)b * S * D + hh * kQaHd + 32 * w;
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4) {
     f32x16 o = zero16();
@@ -269,15 +294,15 @@ __global__ __launch_bounds__(64 * kQaWaves) void qkv_attn_head_kernel(
     // contiguous columns 8 (q + g) .. + 7 with one 16-byte store (every lane swaps).
 #pragma unroll
     for (int qp = 0; qp < 4; qp += 2) {
-      f16x4 hv[2];
+      V4 hv[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hv[j][e] = (f16)(o[4 * (qp + j) + e] * inv);
+        for (int e = 0; e < 4; ++e) hv[j][e] = (T)(o[4 * (qp + j) + e] * inv);
       swap_halves(hv[0], hv[1]);
       if (query < S) {
-        const f16x8 h8 = {hv[0][0], hv[0][1], hv[0][2], hv[0][3], hv[1][0], hv[1][1], hv[1][2], hv[1][3]};
-        *reinterpret_cast<f16x8*>(crow0 + (int64_t)query * D + 8 * (qp + g)) = h8;
+        const V8 h8 = {hv[0][0], hv[0][1], hv[0][2], hv[0][3], hv[1][0], hv[1][1], hv[1][2], hv[1][3]};
+        *reinterpret_cast<V8*>(crow0 + (int64_t)query * D + 8 * (qp + g)) = h8;
       }
     }
   }
@@ -289,25 +314,31 @@ bool qkv_attn_head_ok(int64_t seq_len, int64_t heads, int64_t head_dim) {
   return head_dim == kQaHd && seq_len >= 1 && seq_len <= kQaTok && heads >= 1 && D <= 16384;
 }
 
-template <bool CAUSAL, bool MASKED>
+template <bool CAUSAL, bool MASKED, typename T>
 static hipError_t launch_qkv_attn_head(const QkvAttnArgs& a, float c2) {
   const int64_t grid = a.batch * a.heads;
   if (grid > 0x7fffffff || a.batch > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((qkv_attn_head_kernel<CAUSAL, MASKED>), dim3((unsigned)grid), dim3(64 * kQaWaves), 0, a.stream,
-                     (int)a.seq_len, (int)a.heads, (int)(a.heads * a.head_dim), (int)a.batch,
-                     static_cast<const f16*>(a.h), static_cast<const f16*>(a.w_qkv), a.b_qkv, static_cast<f16*>(a.ctx),
-                     c2, a.key_bits, (int)mask_words(a.seq_len), a.fill, a.fill ? a.nfill : (int64_t)0);
+  hipLaunchKernelGGL((qkv_attn_head_kernel<CAUSAL, MASKED, T>), dim3((unsigned)grid), dim3(64 * kQaWaves), 0,
+                     a.stream, (int)a.seq_len, (int)a.heads, (int)(a.heads * a.head_dim), (int)a.batch,
+                     static_cast<const T*>(a.h), static_cast<const T*>(a.w_qkv), a.b_qkv, static_cast<T*>(a.ctx), c2,
+                     a.key_bits, (int)mask_words(a.seq_len), a.fill, a.fill ? a.nfill : (int64_t)0);
   return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t dispatch_qkv_attn_head(const QkvAttnArgs& a, float c2) {
+  if (a.key_bits)
+    return a.causal ? launch_qkv_attn_head<true, true, T>(a, c2) : launch_qkv_attn_head<false, true, T>(a, c2);
+  return a.causal ? launch_qkv_attn_head<true, false, T>(a, c2) : launch_qkv_attn_head<false, false, T>(a, c2);
 }
 
 hipError_t run_qkv_attn_head(const QkvAttnArgs& a) {
   if (!qkv_attn_head_ok(a.seq_len, a.heads, a.head_dim) || a.batch < 0 || !(a.scale > 0.f) || a.nfill < 0)
     return hipErrorInvalidValue;
+  if (a.dtype != kF16 && a.dtype != kBF16) return hipErrorInvalidValue;
   if (a.batch == 0) return hipSuccess;
   const float c2 = a.scale * 1.4426950408889634f;
-  if (a.key_bits)
-    return a.causal ? launch_qkv_attn_head<true, true>(a, c2) : launch_qkv_attn_head<false, true>(a, c2);
-  return a.causal ? launch_qkv_attn_head<true, false>(a, c2) : launch_qkv_attn_head<false, false>(a, c2);
+  return a.dtype == kBF16 ? dispatch_qkv_attn_head<bf16>(a, c2) : dispatch_qkv_attn_head<f16>(a, c2);
 }
 
 }  // namespace cobra

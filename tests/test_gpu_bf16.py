@@ -167,7 +167,13 @@ def test_sublayer_bf16(B, S, D, H, causal, masked):
         torch.cuda.synchronize()
     assert y.dtype == torch.bfloat16 and r.dtype == torch.float32
     assert mod.plan == (ops.PLAN_PADDED if D % 8 or (D // H) % 8 else ops.PLAN_STAGED)
-    assert torch.equal(y, y2)  # the residual request does not change y (fp32 r either way)
+    # The residual request does not change y beyond rounding: fp32 r either way, but at
+    # head_dim 256 (S <= 128) the call without it runs LN2 in the out-projection's
+    # epilogue, whose row statistics sum in another order.
+    if D % 256 == 0 and D // H == 256 and S <= 128:
+        torch.testing.assert_close(y2.float(), y.float(), atol=2 * U_BF16, rtol=2 * U_BF16)
+    else:
+        assert torch.equal(y, y2)
     dev = "cpu" if B * S * D <= (1 << 21) else DEV
     want_r, want = oracle_on(ref, x.float(), causal, dev, return_residual=True, mask=mask)
     assert bf16_gate(want, y.float().cpu(), f"sublayer B{B} S{S} D{D} H{H}").passed
