@@ -347,11 +347,12 @@ static hipError_t dispatch_dma(const GemmArgs& a) {
 //
 // Co-residency: the launcher runs this kernel only when the whole grid fits the chip
 // at one workgroup per CU.  Tile ids are dealt to XCDs in contiguous ranges
-// (xcd_remap) and a row block's tiles are consecutive ids, so each XCD dispatches the
-// tiles of one row block before those of the next: a tile only ever waits for tiles
-// dispatched no later than the ones its XCD has already placed, so the waits end even
-// when fewer CUs are free.  The wait is bounded all the same (spin_limit polls); a
-// wave that gives up writes NaN rows rather than hanging.
+// (xcd_remap) and a row block's tiles are consecutive ids, so every XCD dispatches all
+// of a row block's tiles before any tile of a later row block: the tiles a waiting tile
+// depends on are never queued behind tiles that wait on it, and with fewer CUs free the
+// row blocks still complete in order.  The wait is bounded all the same (spin_limit
+// polls); a wave that gives up writes NaN rows rather than hanging.  Each wave reads the
+// words of its own rows only, so no barrier follows the publication.
 template <int BM, int BN, int WM, int WN, int ST, int NB, bool MASKED, typename TA>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_dma_rowln_kernel(
     const TA* __restrict__ A, const TA* __restrict__ W, const float* __restrict__ bias, const TA* __restrict__ x,
