@@ -46,10 +46,13 @@ DEVICE_FLAGS = [
 # their accumulators feed VALU softmax / rescale / LayerNorm work directly, and
 # the default AGPR form adds an accumulator copy per use (~900 instructions in
 # the fused sublayer kernel, ~160 per key block in flash attention).  The fused
-# sublayer kernel's first eight (scalar) arguments are preloaded into SGPRs.
+# sublayer kernel's first eight (scalar) arguments are preloaded into SGPRs, and its
+# instructions are ordered by the backend's iterative ILP scheduler (same results,
+# 1-5 % faster on the fused shapes than the default schedule, same-process A/B).
 FILE_FLAGS = {
     "layer_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-    "layer_split.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=8"],
+    "layer_split.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=8",
+                        "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
