@@ -95,7 +95,7 @@ def _host_flags():
               "-DUSE_ROCM=1", *inc]
     torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
     ldflags = ["-shared", "-L", PKG_DIR, "-lcobra_amd", "-L", torch_lib, "-lc10_hip", "-lc10", "-ltorch_cpu",
-               "-ltorch", "-ltorch_python", "-Wl,-rpath,$ORIGIN"]
+               "-ltorch_hip", "-ltorch", "-ltorch_python", "-Wl,-rpath,$ORIGIN"]
     return cflags, ldflags
 
 

@@ -11,6 +11,7 @@
 // computes anything itself: the launch is the library's (libcobra_amd.so).
 #include <torch/extension.h>
 
+#include <ATen/hip/EmptyTensor.h>
 #include <c10/hip/HIPStream.h>
 
 #include <vector>
@@ -54,7 +55,9 @@ class BoundForward {
       if (now != snapshot_[i]) return py::none();
     }
     if (norm_.attr("eps").cast<double>() != eps_) return py::none();
-    at::Tensor y = at::empty_like(x);
+    // The device allocator directly (the caching allocator, as empty_like reaches it
+    // after two dispatcher round trips); x is contiguous, so y has x's layout.
+    at::Tensor y = at::detail::empty_cuda(sizes_, dtype_, device_, c10::nullopt);
     const hipStream_t s = c10::hip::getCurrentHIPStream(device_.index()).stream();
     const int code = cobra_layer_run(handle_, x.data_ptr(), nullptr, y.data_ptr(), nullptr, s);
     if (code != 0) {

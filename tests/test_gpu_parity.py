@@ -330,6 +330,15 @@ def test_steady_state_fast_path():
     assert torch.equal(y_e, y_e_full) and not torch.equal(y_e, y3)
     assert torch.equal(y_t, y_t_full)
     assert torch.equal(y_s, y3)
+    # The native call's output is a tensor of the calling mode, as the full path's is:
+    # an inference tensor under inference_mode only.
+    with torch.no_grad():
+        mod(x3)
+        y_n = mod(x3)
+        torch.cuda.synchronize()
+    assert mod._fast is not None and a.is_inference() and not y_n.is_inference()
+    assert y_n.shape == x3.shape and y_n.dtype == x3.dtype and y_n.device == x3.device and y_n.is_contiguous()
+    assert torch.equal(y_n, y3)
 
 
 # ---- op-level wrappers against fp32 references of the same op -------------
