@@ -326,6 +326,7 @@ const char* cobra_error_string(int c) { return hipGetErrorString(static_cast<hip
 int cobra_ln_fwd(const void* x, int x_dtype, const void* branch, int branch_dtype, const float* gamma,
                  const float* beta, const uint8_t* row_mask, int mask_flags, float* resid_out, void* y, int y_dtype,
                  int64_t rows, int64_t d, float eps, void* stream) {
+  if (rows == 0 && d > 0 && d <= cobra::kLnMaxD && is_act_dtype(x_dtype) && is_act_dtype(y_dtype)) return 0;
   if (!x || !y || !gamma || !beta || !is_act_dtype(x_dtype) || !is_act_dtype(y_dtype)) return kBad;
   if ((mask_flags & ~(COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT)) != 0 || (mask_flags && !row_mask)) return kBad;
   if (branch && !is_dtype(branch_dtype)) return kBad;
@@ -348,6 +349,7 @@ int cobra_ln_fwd_strided(const void* x, int x_dtype, int64_t ldx, const void* br
                          const float* gamma, const float* beta, const uint8_t* row_mask, int mask_flags,
                          float* resid_out, int64_t ldr, void* y, int y_dtype, int64_t ldy, int64_t rows, int64_t d,
                          float eps, void* stream) {
+  if (rows == 0 && d > 0 && d <= cobra::kLnMaxD && is_act_dtype(x_dtype) && is_act_dtype(y_dtype)) return 0;
   if (!x || !y || !gamma || !beta || !is_act_dtype(x_dtype) || !is_act_dtype(y_dtype)) return kBad;
   if ((mask_flags & ~(COBRA_EPI_MASK_RESID | COBRA_EPI_MASK_OUT)) != 0 || (mask_flags && !row_mask)) return kBad;
   if (branch && !is_dtype(branch_dtype)) return kBad;
@@ -375,6 +377,8 @@ int cobra_linear_fwd(const void* a, const void* w, int ab_dtype, const float* bi
                      void* stream) {
   // resid and c: fp16 or fp32 with fp16 operands, bf16 or fp32 with bf16 operands
   auto out_ok = [&](int dt) { return dt == kF32 || dt == ab_dtype; };
+  if (M == 0 && N > 0 && K > 0 && N <= 0x7fffffff && K <= 0x7fffffff && is_op_dtype(ab_dtype) && out_ok(c_dtype))
+    return 0;
   if (!a || !w || !c || !is_op_dtype(ab_dtype) || !out_ok(c_dtype) || (resid && !out_ok(resid_dtype))) return kBad;
   if ((epi & ~kEpiAll) != 0 || (epi & COBRA_EPI_MASK_OUT) || ((epi & ~COBRA_EPI_GELU) && !row_mask)) return kBad;
   if (!aligned16(a) || !aligned16(w) || !aligned16(c) || !opt_aligned16(resid) || !opt_aligned16(bias)) return kBad;
@@ -391,6 +395,7 @@ int cobra_linear_fwd(const void* a, const void* w, int ab_dtype, const float* bi
 int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const void* resid, int resid_dtype,
                         const uint8_t* row_mask, int epi, float* resid_out, const float* gamma, const float* beta,
                         void* y, int y_dtype, int64_t M, int64_t N, int64_t K, float eps, void* stream) {
+  if (M == 0 && N > 0 && N <= 128 && K > 0 && K <= 0x7fffffff && is_dtype(y_dtype)) return 0;
   if (!a || !w || !gamma || !beta || !y || !is_dtype(y_dtype) || (resid && !is_dtype(resid_dtype))) return kBad;
   if ((epi & ~kEpiAll) != 0 || ((epi & ~COBRA_EPI_GELU) && !row_mask)) return kBad;
   if (!aligned16(a) || !aligned16(w) || !aligned16(y) || !opt_aligned16(resid) || !opt_aligned16(resid_out) ||
@@ -407,6 +412,8 @@ int cobra_linear_ln_fwd(const void* a, const void* w, const float* bias, const v
 
 int cobra_ln_linear_fwd(const void* x, int x_dtype, const float* gamma, const float* beta, const void* w,
                         const float* bias, void* c, int64_t M, int64_t N, int64_t d, float eps, void* stream) {
+  if (M == 0 && is_dtype(x_dtype) && cobra::ln_gemm_ok(d, x_dtype) && N > 0 && N <= 0x7fffffff && N % 8 == 0)
+    return 0;
   if (!x || !gamma || !beta || !w || !c || !is_dtype(x_dtype)) return kBad;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(beta) || !aligned16(w) || !aligned16(c) ||
       !opt_aligned16(bias))
@@ -417,6 +424,7 @@ int cobra_ln_linear_fwd(const void* x, int x_dtype, const float* gamma, const fl
 }
 
 int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int64_t seq_len, void* stream) {
+  if ((batch == 0 || seq_len == 0) && batch >= 0 && seq_len >= 0 && seq_len <= 0x7fffffff) return 0;
   if (!mask || !key_bits || (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
   if (batch < 0 || seq_len < 0 || seq_len > 0x7fffffff) return kBad;
   return code(cobra::run_mask_bits(mask, key_bits, batch, (int)seq_len, static_cast<hipStream_t>(stream)));
@@ -424,6 +432,9 @@ int cobra_mask_bits(const uint8_t* mask, uint64_t* key_bits, int64_t batch, int6
 
 int cobra_attn_fwd(const void* qkv, void* ctx, int dtype, const uint64_t* key_bits, int64_t batch, int64_t seq_len,
                    int64_t heads, int64_t head_dim, float scale, int causal, void* stream) {
+  if ((batch == 0 || seq_len == 0) && batch >= 0 && seq_len >= 0 && seq_len <= 0x7fffffff && heads > 0 &&
+      heads <= 0x7fffffff && head_dim > 0 && head_dim <= 256 && scale > 0.f && is_op_dtype(dtype))
+    return 0;
   if (!qkv || !ctx || !aligned16(qkv) || !aligned16(ctx) || !is_op_dtype(dtype)) return kBad;
   if (key_bits && (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
   if (batch < 0 || seq_len < 0 || seq_len > 0x7fffffff || heads <= 0 || heads > 0x7fffffff || head_dim <= 0 ||
@@ -447,6 +458,7 @@ int cobra_qkv_attn_fwd(const void* h, const void* w_qkv, const float* b_qkv, voi
                        int64_t head_dim, float scale, int causal, void* stream) {
   const int64_t need = cobra_qkv_attn_workspace_bytes(batch, seq_len, heads, head_dim);
   if (need < 0 || seq_len > 0x7fffffff || heads > 0x7fffffff || !(scale > 0.f)) return kBad;
+  if (batch * seq_len == 0) return 0;
   if (!h || !w_qkv || !ctx || !aligned16(h) || !aligned16(w_qkv) || !aligned16(ctx) || !opt_aligned16(b_qkv))
     return kBad;
   if (key_bits && (reinterpret_cast<uintptr_t>(key_bits) & 7u) != 0) return kBad;
@@ -499,6 +511,7 @@ int cobra_layer_fwd(const void* x, int x_dtype, const uint8_t* valid_mask, const
   const bool masked = valid_mask != nullptr;
   const int plan = cobra_layer_plan(batch, seq_len, d_model, heads, masked, x_dtype);
   if (plan < 0) return kBad;
+  if (batch * seq_len == 0) return 0;
   const void* must[] = {x, w_qkv, b_qkv, w_o, b_o, ln2_w, ln2_b, y};
   for (const void* p : must)
     if (!p || !aligned16(p)) return kBad;
@@ -629,6 +642,7 @@ cobra_layer_launch* cobra_layer_bind(int x_dtype, int masked, const void* w_qkv,
 int cobra_layer_run(const cobra_layer_launch* h, const void* x, const uint8_t* valid_mask, void* y, float* resid_out,
                     void* stream) {
   if (!h || (valid_mask && !h->masked)) return kBad;
+  if (h->batch * h->seq_len == 0) return 0;
   if (h->split) {
     if (!x || !aligned16(x) || !y || !aligned16(y) || !opt_aligned16(resid_out)) return kBad;
     return code(cobra::launch_layer_split(h->sl, x, valid_mask, y, resid_out, static_cast<hipStream_t>(stream)));
@@ -648,6 +662,7 @@ int cobra_layer_fwd_noalloc(const void* x, int x_dtype, const uint8_t* valid_mas
   const int64_t need =
       cobra_layer_workspace_bytes(batch, seq_len, d_model, heads, valid_mask != nullptr, x_dtype);
   if (need < 0 || need > COBRA_NOALLOC_MAX_BYTES) return kBad;
+  if (batch * seq_len == 0) return 0;
   void* ws = nullptr;
   if (need > 0) {
     int cur = -1, sdev = -1;
@@ -674,6 +689,7 @@ int cobra_block_fwd(const void* h, const float* r, const uint8_t* valid_mask, co
                     float* r_out, void* out, int out_dtype, int mask_out, int64_t batch, int64_t seq_len,
                     int64_t d_model, int64_t heads, int64_t ffn_dim, int causal, float eps, void* stream) {
   if (cobra_block_plan(batch, seq_len, d_model, heads, ffn_dim) < 0 || !is_dtype(out_dtype)) return kBad;
+  if (batch * seq_len == 0) return 0;
   const void* must[] = {h, r, w_qkv, b_qkv, w_o, b_o, ln2_w, ln2_b, w1, b1, w2, b2, lnn_w, lnn_b, r_out, out};
   for (const void* p : must)
     if (!p || !aligned16(p)) return kBad;

@@ -17,7 +17,10 @@
  *     captured into a hipGraph;
  *   - the return value is a hipError_t code: 0 on success, non-zero when the
  *     arguments are rejected (nothing is enqueued then) or the launch failed.
- *     cobra_error_string() names it.  No C++ exception crosses the ABI.
+ *     cobra_error_string() names it.  No C++ exception crosses the ABI;
+ *   - a call with no rows (M, rows, batch or seq_len 0) checks its shape and dtype
+ *     arguments and returns 0 without reading any pointer or enqueueing work, so
+ *     empty tensors (whose data pointers may be NULL) pass through.
  */
 #ifndef COBRA_AMD_H
 #define COBRA_AMD_H

@@ -217,3 +217,24 @@ def test_state_dict_and_reload():
         b = mod(x)
     assert (a - b).abs().max().item() > 1e-3
     assert set(mod.state_dict()) == set(ref.state_dict())
+
+
+@pytest.mark.parametrize("cfg,shape", [((2, 128, 128, 4, 128, 2, True), (0, 128, 128)),
+                                       ((2, 128, 1024, 16, 1024, 2, False), (2, 0, 1024)),
+                                       ((2, 50, 96, 8, 100, 2, True), (0, 50, 96))])
+def test_empty_inputs(cfg, shape):
+    """An empty batch or sequence runs through the stack (fused block, staged and
+    padded paths) to an empty output, with and without a mask, and the next call with
+    tokens still matches the oracle."""
+    ref, mod = build(cfg)
+    x = torch.zeros(*shape, device=DEV, dtype=torch.float16)
+    m = torch.ones(shape[:2], dtype=torch.bool, device=DEV)
+    log(f"[model empty] cfg={cfg} x={shape}")
+    with torch.inference_mode():
+        y = mod(x)
+        y_m = mod(x, m)
+        x2 = make_input(2, 9, cfg[2], seed=3).half()
+        y2 = mod(x2.to(DEV)).float().cpu()
+        torch.cuda.synchronize()
+    assert y.shape == x.shape and y_m.shape == x.shape and y.dtype == x.dtype
+    assert compare_outputs(model_forward(ref, x2.float(), None), y2).passed

@@ -475,6 +475,26 @@ def test_attn_op(hd, causal):
         assert torch.allclose(got.float(), want, atol=2e-3, rtol=1e-2), (hd, S, causal, (got.float() - want).abs().max())
 
 
+@pytest.mark.parametrize("B,S,D,H,dtype", [(0, 128, 128, 4, torch.float16), (3, 0, 128, 4, torch.float16),
+                                             (0, 1024, 128, 4, torch.float16), (0, 128, 1024, 4, torch.float16),
+                                             (2, 0, 1024, 16, torch.float32), (0, 50, 96, 8, torch.float16)])
+def test_empty_inputs(B, S, D, H, dtype):
+    """An empty batch or sequence gives an empty y (and residual) of x's shape, with
+    or without a mask, on every plan family; the next non-empty call is unaffected."""
+    ref, mod = build_pair(D, H, dtype=dtype)
+    x = torch.zeros(B, S, D, device=DEV, dtype=dtype)
+    m = torch.ones(B, S, dtype=torch.bool, device=DEV)
+    log(f"[empty] B{B} S{S} D{D} H{H} {dtype}")
+    with torch.inference_mode():
+        y = mod(x)
+        y_m, r_m = mod(x, valid_token_mask=m, causal=True, return_residual=True)
+        x2 = make_input(2, 17, D, seed=2).to(dtype).to(DEV)
+        y2 = mod(x2)
+        torch.cuda.synchronize()
+    assert y.shape == x.shape and y.dtype == dtype and y_m.shape == x.shape and r_m.shape == x.shape
+    assert compare_outputs(oracle_on(ref, x2.float().cpu(), False, "cpu"), y2.float().cpu()).passed
+
+
 def test_invalid_shapes_raise():
     from cobra_amd import CobraError, ops
 

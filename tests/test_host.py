@@ -70,6 +70,40 @@ def test_argument_validation_rejects_before_any_launch():
     assert lib.cobra_layer_plan(2, 16, 128, 4, 0, 7) == -1
 
 
+def test_empty_calls_return_before_reading_pointers():
+    """A call with no rows checks its shape and dtype arguments and returns 0 with NULL
+    pointers (the data pointers of empty tensors), before any GPU call; a bad shape or
+    dtype is still rejected."""
+    from cobra_amd import _lib
+
+    lib = _lib.lib()
+    F16, F32 = _lib.F16, _lib.F32
+    assert lib.cobra_ln_fwd(None, F16, None, 0, None, None, None, 0, None, None, F16, 0, 128, 1e-5, None) == 0
+    assert lib.cobra_ln_fwd(None, 7, None, 0, None, None, None, 0, None, None, F16, 0, 128, 1e-5, None) != 0
+    assert lib.cobra_ln_fwd_strided(None, F32, 0, None, 0, 0, None, None, None, 0, None, 0, None, F16, 0, 0, 96,
+                                    1e-5, None) == 0
+    assert lib.cobra_linear_fwd(None, None, F16, None, None, 0, None, 0, None, F16, 0, 64, 64, None) == 0
+    assert lib.cobra_linear_fwd(None, None, F16, None, None, 0, None, 0, None, F16, 0, 0, 64, None) != 0  # N = 0
+    assert lib.cobra_linear_ln_fwd(None, None, None, None, 0, None, 0, None, None, None, None, F16, 0, 128, 64,
+                                   1e-5, None) == 0
+    assert lib.cobra_attn_fwd(None, None, F16, None, 0, 128, 4, 32, 0.1, 0, None) == 0
+    assert lib.cobra_attn_fwd(None, None, F16, None, 3, 0, 4, 32, 0.1, 0, None) == 0
+    assert lib.cobra_attn_fwd(None, None, F16, None, 0, 128, 4, 264, 0.1, 0, None) != 0  # head_dim
+    assert lib.cobra_mask_bits(None, None, 0, 128, None) == 0
+    layer_args = [None] * 12 + [None, None, 0]  # x .. resid_out, workspace, workspace bytes
+    for B, S, D, H, dt in [(0, 128, 128, 4, F16), (3, 0, 128, 4, F16), (0, 1024, 128, 4, F16),
+                           (0, 128, 1024, 4, F16), (2, 0, 1024, 16, F32), (0, 50, 96, 8, F16)]:
+        a = list(layer_args)
+        a[1] = dt
+        assert lib.cobra_layer_fwd(*a, B, S, D, H, 0, 1e-5, None) == 0, (B, S, D, H)
+        assert lib.cobra_layer_fwd_noalloc(*a[:13], B, S, D, H, 0, 1e-5, None) == 0, (B, S, D, H)
+    a = list(layer_args)
+    a[1] = F16
+    assert lib.cobra_layer_fwd(*a, 0, 16, 528, 2, 0, 1e-5, None) != 0  # head_dim 264
+    a[1] = 7
+    assert lib.cobra_layer_fwd(*a, 0, 16, 128, 4, 0, 1e-5, None) != 0  # dtype code
+
+
 def test_layer_bind_validates_and_releases():
     """cobra_layer_bind checks what cobra_layer_fwd would check, once; run rejects a
     mask on a handle bound without one, before any launch."""
