@@ -137,6 +137,8 @@ class CobraTransformer(nn.Module):
         self._graph_ok = False
         self._graph = None
         self._static_x = self._static_m = self._static_out = None
+        self._blocks = False  # the signature runs one whole-block kernel per block
+        self._fast = None     # native steady-state call (cobra_host.BoundStack) of that mode
 
     # -- parameters -----------------------------------------------------------
 
@@ -146,6 +148,7 @@ class CobraTransformer(nn.Module):
         self._versioned = [not p.is_inference() for p in self._params]
         self._packs = None
         self._sig = None
+        self._fast = None
         return out
 
     def _packed(self, x_dtype: torch.dtype = torch.float16) -> List[_BlockPack]:
@@ -160,11 +163,20 @@ class CobraTransformer(nn.Module):
                 self._final = (self.final_norm.weight.float().contiguous(), self.final_norm.bias.float().contiguous())
             self._versions = versions
             self._graph = None
+            self._fast = None
         return self._packs
 
     # -- entry point ----------------------------------------------------------
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        # Steady state of the one-kernel-per-block mode (same input signature, no mask,
+        # parameters and eps unchanged): the native call checks that, allocates and
+        # launches; it returns None for any other call.
+        f = self._fast
+        if f is not None and valid_token_mask is None:
+            y = f(x)
+            if y is not None:
+                return y
         self._validate(x)
         packs = self._packed(x.dtype)
         if not x.is_cuda or x.numel() * x.element_size() >= streaming.STREAM_MIN_BYTES:
@@ -181,6 +193,8 @@ class CobraTransformer(nn.Module):
                 ops.block_plan(x.shape[0], x.shape[1], cfg.d_model, cfg.num_heads, cfg.ffn_dim) == 1
             self._graph_ok = (self.graph if self.graph is not None else not blocks) and \
                 x.numel() * x.element_size() <= GRAPH_MAX_INPUT_BYTES
+            self._blocks = blocks
+            self._fast = None
             self._graph = None
             self._static_x = self._static_m = self._static_out = None
             self._sig = sig
@@ -188,7 +202,22 @@ class CobraTransformer(nn.Module):
         m = self._mask_bytes(valid_token_mask, x) if masked else None
         if self._graph_ok:
             return self._run_graphed(x, m, packs)
-        return self._run(x, m, packs)
+        out = self._run(x, m, packs)
+        if self._blocks and m is None and x.numel() * x.element_size() < streaming.STREAM_MIN_BYTES:
+            self._fast = self._make_fast(x, packs)
+        return out
+
+    def _make_fast(self, x: torch.Tensor, packs: List[_BlockPack]):
+        from . import _lib
+
+        flat = []
+        for i, p in enumerate(packs):
+            nw, nb = self._final if i == len(packs) - 1 else (packs[i + 1].ln1_w, packs[i + 1].ln1_b)
+            flat += [p.w_qkv, p.b_qkv, p.w_o, p.b_o, p.ln2_w, p.ln2_b, p.w1, p.b1, p.w2, p.b2, nw, nb]
+        cfg = self.config
+        return _lib.host().BoundStack(x, self._params, list(self._versions), self.final_norm,
+                                      float(self.final_norm.eps), packs[0].ln1_w, packs[0].ln1_b, flat,
+                                      cfg.num_heads, cfg.ffn_dim, bool(cfg.causal), ops.check_code).__call__
 
     def _validate(self, x: torch.Tensor) -> None:
         if x.dim() != 3 or x.shape[-1] != self.config.d_model:

@@ -238,3 +238,47 @@ def test_empty_inputs(cfg, shape):
         torch.cuda.synchronize()
     assert y.shape == x.shape and y_m.shape == x.shape and y.dtype == x.dtype
     assert compare_outputs(model_forward(ref, x2.float(), None), y2).passed
+
+
+def test_stack_steady_state_fast_path():
+    """Repeat calls of one signature in the one-kernel-per-block mode take the native
+    call (cobra_host.BoundStack): a new output per call, equal to the general path's;
+    a changed parameter or epsilon, a mask and another shape leave it."""
+    cfg = (8, 128, 128, 4, 128, 3, True)
+    ref, mod = build(cfg)
+    x = make_input(8, 128, 128, seed=4).half()
+    xd = x.to(DEV)
+    log("[model fast] B8 S128 D128 H4 F128 L3 causal")
+    with torch.inference_mode():
+        y0 = mod(xd).clone()  # general path; binds the native call
+        assert mod._fast is not None
+        y1 = mod(xd)
+        y2 = mod(xd)
+        torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(y1, y2) and y1.data_ptr() != y2.data_ptr()
+    assert compare_outputs(model_forward(ref, x.float(), None), y1.float().cpu()).passed
+    with torch.no_grad():
+        mod.layers[1].ffn_out.bias.add_(0.25)
+        ref.layers[1].ffn_out.bias.add_(0.25)
+        ref.layers[1].ffn_out.bias.copy_(ref.layers[1].ffn_out.bias.half().float())
+    with torch.inference_mode():
+        y3 = mod(xd).clone()  # repacks, rebinds
+        y4 = mod(xd)
+        torch.cuda.synchronize()
+    assert mod._fast is not None and torch.equal(y3, y4) and not torch.equal(y4, y1)
+    assert compare_outputs(model_forward(ref, x.float(), None), y4.float().cpu()).passed
+    with torch.inference_mode():
+        mod.final_norm.eps = 1e-2
+        y_e = mod(xd).clone()
+        y_e2 = mod(xd).clone()
+        mod.final_norm.eps = 1e-5
+        y_back = mod(xd).clone()
+        m = torch.ones(8, 128, dtype=torch.bool, device=DEV)
+        m[3, 100:] = False
+        y_m = mod(xd, m).float().cpu()
+        x5 = make_input(3, 77, 128, seed=6).half()
+        y5 = mod(x5.to(DEV)).float().cpu()
+        torch.cuda.synchronize()
+    assert not torch.equal(y_e, y4) and torch.equal(y_e, y_e2) and torch.equal(y_back, y4)
+    assert compare_outputs(model_forward(ref, x.float(), m.cpu()), y_m).passed
+    assert compare_outputs(model_forward(ref, x5.float(), None), y5).passed
