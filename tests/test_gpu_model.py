@@ -282,3 +282,12 @@ def test_stack_steady_state_fast_path():
     assert not torch.equal(y_e, y4) and torch.equal(y_e, y_e2) and torch.equal(y_back, y4)
     assert compare_outputs(model_forward(ref, x.float(), m.cpu()), y_m).passed
     assert compare_outputs(model_forward(ref, x5.float(), None), y5).passed
+    # fp32 activations (fp16 operands inside): the native call writes an fp32 output
+    ref32, mod32 = build(cfg, dtype=torch.float32)
+    x32 = make_input(8, 128, 128, seed=8)
+    with torch.inference_mode():
+        a32 = mod32(x32.to(DEV)).clone()
+        b32 = mod32(x32.to(DEV))
+        torch.cuda.synchronize()
+    assert mod32._fast is not None and b32.dtype == torch.float32 and torch.equal(a32, b32)
+    assert compare_outputs(model_forward(ref32, x32, None), b32.cpu()).passed
