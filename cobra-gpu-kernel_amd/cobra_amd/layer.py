@@ -201,17 +201,17 @@ class CobraAttentionSublayer(nn.Module):
         causal: Optional[bool] = None,
         return_residual: bool = False,
     ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
-        # Steady state of the common call (same input signature, no mask, weights and
-        # eps unchanged): the native call checks all of that, allocates y and launches;
-        # it returns None for any other call.  At the small shapes the kernel takes
-        # ~7 us, as long as the checks, the allocation and the launch took from
-        # Python, so this path is what back-to-back forwards are bound by.
+        # Steady state of the common call (same input signature, a device mask or none as
+        # bound, weights and eps unchanged): the native call checks all of that,
+        # allocates y and launches; it returns None for any other call.  At the small
+        # shapes the kernel takes ~7 us, as long as the checks, the allocation and the
+        # launch took from Python, so this path is what back-to-back forwards are bound by.
         f = self._fast
-        if f is not None and valid_token_mask is None and causal is None and not return_residual:
-            y = f.call(x)
+        if f is not None and causal is None and not return_residual:
+            y = f.call(x, valid_token_mask)
             if y is not None:
                 return y
-        fast_ok = valid_token_mask is None and causal is None and not return_residual
+        fast_ok = causal is None and not return_residual
         causal = self.causal if causal is None else bool(causal)
         pack = self._packed(x.dtype)
         # Free memory moves between calls, so big or host-resident inputs are
@@ -232,19 +232,19 @@ class CobraAttentionSublayer(nn.Module):
             return self._run_graphed(x, m, pack, causal, return_residual)
         out = self._run_eager(x, m, pack, causal, return_residual)
         if fast_ok and pack.pad is None and x.is_cuda and x.numel() * x.element_size() < streaming.STREAM_MIN_BYTES:
-            self._fast = self._make_fast(x, pack)
+            self._fast = self._make_fast(x, pack, masked)
         return out
 
-    def _make_fast(self, x: torch.Tensor, pack: _Pack) -> _Fast:
+    def _make_fast(self, x: torch.Tensor, pack: _Pack, masked: bool) -> _Fast:
         from . import _lib
 
         f = _Fast()
         B, S, D = x.shape
-        f.launch = ops.LayerLaunch(x.dtype, False, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w,
+        f.launch = ops.LayerLaunch(x.dtype, masked, pack.w_qkv, pack.b_qkv, pack.w_o, pack.b_o, pack.ln1_w,
                                    pack.ln1_b, pack.ln2_w, pack.ln2_b, self._ws, B, S, D,
                                    self.attention.num_heads, self.causal, self.norm1.eps)
         f.call = _lib.host().BoundForward(f.launch.handle, x, self._params, list(pack.versions), self.norm1,
-                                          float(self.norm1.eps), ops.check_code).__call__
+                                          float(self.norm1.eps), masked, ops.check_code).__call__
         return f
 
     # -- planning -------------------------------------------------------------

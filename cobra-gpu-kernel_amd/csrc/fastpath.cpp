@@ -30,10 +30,12 @@ class BoundForward {
   // of the bound signature.  params / snapshot: the tensors the bound weights were
   // packed from, and for each its version counter (or, for an inference tensor, which
   // keeps none, its data pointer) at packing time.  norm: the module whose `eps`
-  // attribute was bound (its value must still equal eps).  on_error(name, code) raises
+  // attribute was bound (its value must still equal eps).  masked: the launch was bound
+  // with a token mask, which every call must then pass ([B, S] bool or uint8 on the
+  // device, 0 = padded), and a call without one must not.  on_error(name, code) raises
   // the library's error.
   BoundForward(int64_t handle, const at::Tensor& like, std::vector<at::Tensor> params,
-               std::vector<int64_t> snapshot, py::object norm, double eps, py::object on_error)
+               std::vector<int64_t> snapshot, py::object norm, double eps, bool masked, py::object on_error)
       : handle_(reinterpret_cast<const cobra_layer_launch*>(handle)),
         sizes_(like.sizes().vec()),
         dtype_(like.scalar_type()),
@@ -42,16 +44,26 @@ class BoundForward {
         snapshot_(std::move(snapshot)),
         norm_(std::move(norm)),
         eps_(eps),
+        masked_(masked),
         on_error_(std::move(on_error)) {
     TORCH_CHECK(handle_ != nullptr, "BoundForward: null launch handle");
     TORCH_CHECK(params_.size() == snapshot_.size(), "BoundForward: one snapshot value per parameter");
     TORCH_CHECK(device_.is_cuda(), "BoundForward: the bound input must be a device tensor");
   }
 
-  py::object call(const at::Tensor& x) const {
+  py::object call(const at::Tensor& x, const c10::optional<at::Tensor>& mask) const {
     if (!x.defined() || x.device() != device_ || x.scalar_type() != dtype_ || x.sizes() != sizes_ ||
         !x.is_contiguous())
       return py::none();
+    const uint8_t* m = nullptr;
+    if (mask.has_value() != masked_) return py::none();
+    if (masked_) {
+      const at::Tensor& t = *mask;
+      if (!t.defined() || t.device() != device_ || (t.scalar_type() != at::kBool && t.scalar_type() != at::kByte) ||
+          t.dim() != 2 || t.size(0) != sizes_[0] || t.size(1) != sizes_[1] || !t.is_contiguous())
+        return py::none();
+      m = static_cast<const uint8_t*>(t.data_ptr());
+    }
     for (size_t i = 0; i < params_.size(); ++i) {
       const at::Tensor& p = params_[i];
       const int64_t now = p.is_inference() ? reinterpret_cast<int64_t>(p.data_ptr()) : p._version();
@@ -62,7 +74,7 @@ class BoundForward {
     // after two dispatcher round trips); x is contiguous, so y has x's layout.
     at::Tensor y = at::detail::empty_cuda(sizes_, dtype_, device_, c10::nullopt);
     const hipStream_t s = c10::hip::getCurrentHIPStream(device_.index()).stream();
-    const int code = cobra_layer_run(handle_, x.data_ptr(), nullptr, y.data_ptr(), nullptr, s);
+    const int code = cobra_layer_run(handle_, x.data_ptr(), m, y.data_ptr(), nullptr, s);
     if (code != 0) {
       on_error_("cobra_layer_run", code);  // raises
       throw std::runtime_error("cobra_layer_run failed");
@@ -79,6 +91,7 @@ class BoundForward {
   std::vector<int64_t> snapshot_;
   py::object norm_;
   double eps_;
+  bool masked_;
   py::object on_error_;
 };
 
@@ -182,8 +195,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Native steady-state forward of the cobra_amd attention sublayer";
   py::class_<BoundForward>(m, "BoundForward")
       .def(py::init<int64_t, const at::Tensor&, std::vector<at::Tensor>, std::vector<int64_t>, py::object, double,
-                    py::object>())
-      .def("__call__", &BoundForward::call);
+                    bool, py::object>())
+      .def("__call__", &BoundForward::call, py::arg("x"), py::arg("mask") = py::none());
   py::class_<BoundStack>(m, "BoundStack")
       .def(py::init<const at::Tensor&, std::vector<at::Tensor>, std::vector<int64_t>, py::object, double, at::Tensor,
                     at::Tensor, std::vector<at::Tensor>, int64_t, int64_t, bool, py::object>())

@@ -339,6 +339,28 @@ def test_steady_state_fast_path():
     assert mod._fast is not None and a.is_inference() and not y_n.is_inference()
     assert y_n.shape == x3.shape and y_n.dtype == x3.dtype and y_n.device == x3.device and y_n.is_contiguous()
     assert torch.equal(y_n, y3)
+    # Masked calls bind a masked launch: repeat calls with device masks (bool or uint8, any
+    # values) take it and give what the general path gives (an explicit causal argument
+    # takes that path); a call without a mask leaves it.
+    mk = torch.ones(8, 128, dtype=torch.bool)
+    mk[2, 90:] = False
+    mk[5, 1:] = False
+    mk2 = mk.clone()
+    mk2[0, 64:] = False
+    with torch.inference_mode():
+        mod(x2, mk.to(DEV))
+        assert mod._fast is not None
+        y_m1 = mod(x2, mk.to(DEV)).clone()
+        y_m2 = mod(x2, mk.to(DEV).to(torch.uint8)).clone()
+        y_mf = mod(x2, mk.to(DEV), causal=False).clone()
+        y_m3 = mod(x2, mk2.to(DEV)).clone()
+        y_m3f = mod(x2, mk2.to(DEV), causal=False).clone()
+        y_nm = mod(x2).clone()
+        y_nmf = mod(x2, causal=False).clone()
+        torch.cuda.synchronize()
+    assert torch.equal(y_m1, y_mf) and torch.equal(y_m2, y_mf) and torch.equal(y_m3, y_m3f)
+    assert not torch.equal(y_m3, y_m1) and torch.equal(y_nm, y_nmf)
+    assert compare_outputs(oracle_on(ref, x2.float().cpu(), False, "cpu", mask=mk), y_m1.float().cpu()).passed
 
 
 # ---- op-level wrappers against fp32 references of the same op -------------

@@ -148,11 +148,11 @@ def test_host_companion_loads_and_checks_its_arguments():
     host = _lib.host()
     x = torch.zeros(2, 16, 128, dtype=torch.float16)
     with pytest.raises(RuntimeError, match="null launch handle"):
-        host.BoundForward(0, x, [], [], None, 1e-5, None)
+        host.BoundForward(0, x, [], [], None, 1e-5, False, None)
     with pytest.raises(RuntimeError, match="device tensor"):
-        host.BoundForward(256, x, [], [], None, 1e-5, None)
+        host.BoundForward(256, x, [], [], None, 1e-5, False, None)
     with pytest.raises(RuntimeError, match="one snapshot value"):
-        host.BoundForward(256, x, [x], [], None, 1e-5, None)
+        host.BoundForward(256, x, [x], [], None, 1e-5, False, None)
 
 
 def test_padded_block_weights_reproduce_the_block():
